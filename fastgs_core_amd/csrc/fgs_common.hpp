@@ -1,0 +1,21 @@
+// fgs_common.hpp -- host-side helpers shared by the C-ABI entry points:
+// thread-local error message and launch checking.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fastgs_hip.h"
+#include "fgs_device.hpp"
+
+namespace fgs {
+
+// Records msg as the calling thread's last error and returns code.
+int32_t set_error(int32_t code, const char* msg);
+
+// Checks hipGetLastError() after a launch; returns FGS_OK or FGS_ERR_LAUNCH.
+int32_t check_launch(const char* what);
+
+inline unsigned ceil_div_u(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace fgs

@@ -1,0 +1,239 @@
+// fgs_device.hpp -- device-side building blocks shared by the FastGS HIP
+// kernels (gfx950, wave64).
+//
+// Numerics contract: every integer-deciding quantity (radii, tile counts,
+// depth bits, blend skip/stop decisions) is computed with the operation order
+// of the reference Metal source, with FP contraction disabled for the whole
+// library (-ffp-contract=off), IEEE correctly rounded '/' and sqrt, and the
+// deterministic exp/log below.  The CPU parity oracle evaluates the same
+// operations, so those integers agree bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fgs {
+
+constexpr int kTile = 16;
+constexpr int kTilePixels = kTile * kTile;
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Deterministic transcendental functions.
+// ---------------------------------------------------------------------------
+
+// exp(x) = 2^t with t = x*log2(e) split as t = n + f, n = floor(t), f in
+// [0,1); 2^f = 1 + f*q(f) with q a degree-5 polynomial fitted at 200
+// Chebyshev nodes on [0,1] (max relative error 5.8e-8), Horner with fused
+// multiply-adds; scaled by ldexp.  t is clamped at -126 (normal range).
+__device__ __forceinline__ float det_expf(float x) {
+  float t = x * 1.44269502973556519f;
+  t = fmaxf(t, -126.0f);
+  const float n = floorf(t);
+  const float f = t - n;
+  float q = 0.0002082919527310878f;
+  q = __builtin_fmaf(q, f, 0.0012689351569861174f);
+  q = __builtin_fmaf(q, f, 0.009652440436184406f);
+  q = __builtin_fmaf(q, f, 0.055495936423540115f);
+  q = __builtin_fmaf(q, f, 0.24022722244262695f);
+  q = __builtin_fmaf(q, f, 0.6931471824645996f);
+  const float p = __builtin_fmaf(f, q, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
+// ln(x): x = m*2^e with m in [sqrt(1/2), sqrt(2)); ln(m) = 2*atanh(s),
+// s = (m-1)/(m+1), Taylor series to s^19 in double, rounded to float.
+__device__ __forceinline__ float det_logf(float x) {
+  if (!(x > 0.0f)) return (x == 0.0f) ? -__builtin_huge_valf() : __builtin_nanf("");
+  if (__builtin_isinf(x)) return x;
+  int e;
+  float m = __builtin_frexpf(x, &e);
+  if (m < 0.70710678118654752f) {
+    m = m * 2.0f;
+    e = e - 1;
+  }
+  const double md = (double)m;
+  const double s = (md - 1.0) / (md + 1.0);
+  const double s2 = s * s;
+  double poly = 0.052631578947368418;
+  poly = poly * s2 + 0.058823529411764705;
+  poly = poly * s2 + 0.066666666666666666;
+  poly = poly * s2 + 0.076923076923076927;
+  poly = poly * s2 + 0.090909090909090912;
+  poly = poly * s2 + 0.1111111111111111;
+  poly = poly * s2 + 0.14285714285714285;
+  poly = poly * s2 + 0.2;
+  poly = poly * s2 + 0.33333333333333331;
+  poly = poly * s2 + 1.0;
+  const double r = (double)e * 0.69314718055994529 + 2.0 * s * poly;
+  return (float)r;
+}
+
+// float -> int: truncation toward zero, NaN -> 0, saturating.
+__device__ __forceinline__ int f2i(float v) {
+  if (!(v == v)) return 0;
+  if (v >= 2147483648.0f) return 2147483647;
+  if (v <= -2147483648.0f) return (-2147483647 - 1);
+  return (int)v;
+}
+
+__device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+__device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
+
+// ---------------------------------------------------------------------------
+// Exact tile footprint walk (reference fastgs_preprocess.metal:247-382 and
+// fastgs_binning.metal:23-180).  The longer tile axis is swept line by line,
+// intersecting the ellipse {d : 1/2 d^T Conic d <= t}, t = mult*2*ln(255 o),
+// with the tile-boundary lines.  emit(tile_id) is called for every touched
+// tile in sweep order; the number of touched tiles is returned.  A line whose
+// tile interval is empty or inverted contributes nothing.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void ellipse_isect(float4 co, float disc, float t, float px, float py,
+                                              bool is_y, float coord, float& lo, float& hi) {
+  const float p_u = is_y ? py : px;
+  const float p_v = is_y ? px : py;
+  const float coeff = is_y ? co.x : co.z;
+  const float h = coord - p_u;
+  const float sq = __builtin_sqrtf(disc * h * h + t * coeff);
+  lo = (-co.y * h - sq) / coeff + p_v;
+  hi = (-co.y * h + sq) / coeff + p_v;
+}
+
+template <typename Emit>
+__device__ __forceinline__ uint32_t tiles_walk(float px, float py, float4 co, int gx, int gy,
+                                               float mult, Emit&& emit) {
+  const float disc = co.y * co.y - co.x * co.z;
+  if (co.x <= 0.0f || co.z <= 0.0f || disc >= 0.0f) return 0u;
+  float t = 2.0f * det_logf(co.w * 255.0f);
+  t = mult * t;
+  float x_term = __builtin_sqrtf(-(co.y * co.y * t) / (disc * co.x));
+  x_term = (co.y < 0.0f) ? x_term : -x_term;
+  float y_term = __builtin_sqrtf(-(co.y * co.y * t) / (disc * co.z));
+  y_term = (co.y < 0.0f) ? y_term : -y_term;
+  float am0 = py - y_term, am1 = px - x_term;  // bbox_argmin
+  float aM0 = py + y_term, aM1 = px + x_term;  // bbox_argmax
+  float lo, hi;
+  float bmin0, bmin1, bmax0, bmax1;
+  ellipse_isect(co, disc, t, px, py, true, am0, lo, hi);
+  bmin0 = lo;
+  ellipse_isect(co, disc, t, px, py, false, am1, lo, hi);
+  bmin1 = lo;
+  ellipse_isect(co, disc, t, px, py, true, aM0, lo, hi);
+  bmax0 = hi;
+  ellipse_isect(co, disc, t, px, py, false, aM1, lo, hi);
+  bmax1 = hi;
+  int rmin0 = imax(0, imin(gx, f2i(bmin0 / 16.0f)));
+  int rmin1 = imax(0, imin(gy, f2i(bmin1 / 16.0f)));
+  int rmax0 = imax(0, imin(gx, f2i(bmax0 / 16.0f + 1.0f)));
+  int rmax1 = imax(0, imin(gy, f2i(bmax1 / 16.0f + 1.0f)));
+  const int y_span = rmax1 - rmin1;
+  const int x_span = rmax0 - rmin0;
+  if (y_span * x_span == 0) return 0u;
+  const bool is_y = y_span < x_span;
+  if (is_y) {
+    int ti;
+    float tf;
+    ti = rmin0; rmin0 = rmin1; rmin1 = ti;
+    ti = rmax0; rmax0 = rmax1; rmax1 = ti;
+    tf = bmin0; bmin0 = bmin1; bmin1 = tf;
+    tf = bmax0; bmax0 = bmax1; bmax1 = tf;
+    tf = am0; am0 = am1; am1 = tf;
+    tf = aM0; aM0 = aM1; aM1 = tf;
+  }
+  uint32_t count = 0;
+  float il0, il1;            // intersect_min_line
+  float iM0 = bmax1, iM1 = bmin1;  // intersect_max_line
+  float min_line = (float)rmin0 * 16.0f;
+  if (bmin0 <= min_line) {
+    ellipse_isect(co, disc, t, px, py, is_y, (float)rmin0 * 16.0f, il0, il1);
+  } else {
+    il0 = iM0;
+    il1 = iM1;
+  }
+  for (int u = rmin0; u < rmax0; ++u) {
+    const float max_line = min_line + 16.0f;
+    if (max_line <= bmax0) ellipse_isect(co, disc, t, px, py, is_y, max_line, iM0, iM1);
+    float e_min, e_max;
+    if (min_line <= am1 && am1 < max_line)
+      e_min = bmin1;
+    else
+      e_min = fminf(il0, iM0);
+    if (min_line <= aM1 && aM1 < max_line)
+      e_max = bmax1;
+    else
+      e_max = fmaxf(il1, iM1);
+    const int min_tile_v = imax(rmin1, imin(rmax1, f2i(e_min / 16.0f)));
+    const int max_tile_v = imin(rmax1, imax(rmin1, f2i(e_max / 16.0f + 1.0f)));
+    if (max_tile_v > min_tile_v) {
+      count += (uint32_t)(max_tile_v - min_tile_v);
+      emit(u, min_tile_v, max_tile_v, is_y);
+    }
+    il0 = iM0;
+    il1 = iM1;
+    min_line = max_line;
+  }
+  return count;
+}
+
+struct NoEmit {
+  __device__ __forceinline__ void operator()(int, int, int, bool) const {}
+};
+
+// ---------------------------------------------------------------------------
+// Wave64 primitives.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = lane_id();
+  return (l == 0) ? 0ull : ((~0ull) >> (64 - l));
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t t = __shfl_up(v, (unsigned)o, kWave);
+    if (l >= o) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const uint32_t t = __shfl_xor(v, o, kWave);
+    v = v > t ? v : t;
+  }
+  return v;
+}
+
+// Block-wide exclusive scan of one u32 per thread (blockDim.x a multiple of
+// 64, at most 1024).  Returns the exclusive prefix; *total gets the block sum.
+// s_tmp needs blockDim.x/64 + 1 entries.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
+  const int nw = (int)(blockDim.x / kWave);
+  const int w = (int)(threadIdx.x / kWave);
+  const uint32_t incl = wave_incl_scan(v);
+  if (lane_id() == kWave - 1) s_tmp[w] = incl;
+  __syncthreads();
+  if (w == 0) {
+    uint32_t x = (lane_id() < nw) ? s_tmp[lane_id()] : 0u;
+    const uint32_t xi = wave_incl_scan(x);
+    if (lane_id() < nw) s_tmp[lane_id()] = xi - x;
+    if (lane_id() == nw - 1) s_tmp[nw] = xi;
+  }
+  __syncthreads();
+  const uint32_t r = s_tmp[w] + incl - v;
+  if (total) *total = s_tmp[nw];
+  __syncthreads();
+  return r;
+}
+
+}  // namespace fgs

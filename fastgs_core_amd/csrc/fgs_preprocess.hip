@@ -1,0 +1,556 @@
+// fgs_preprocess.hip -- per-Gaussian projection, covariance, SH colour and
+// exact tile-footprint count (forward), and the chain rule back to the 3D
+// parameters (backward).  One thread per Gaussian, 256-thread workgroups;
+// every output row is written (zeros for culled rows), so no separate clear
+// pass is needed.
+//
+// Forward restates fastgs_preprocess.metal:384-484, backward
+// fastgs_preprocess_backward.metal:60-430.  Matrices arrive as 16 floats,
+// column-major; the Metal float3x3 constructor fills columns, so X[c][r]
+// below is column c, row r of the Metal matrix.
+#include "fgs_common.hpp"
+
+namespace fgs {
+
+__constant__ float kSH_C0 = 0.28209479177387814f;
+__constant__ float kSH_C1 = 0.4886025119029199f;
+__constant__ float kSH_C2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f,
+                                -1.0925484305920792f, 0.5462742152960396f};
+__constant__ float kSH_C3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f,
+                                0.3731763325901154f, -0.4570457994644658f, 1.445305721320277f,
+                                -0.5900435899266435f};
+
+struct Mat16 {
+  float m[16];
+};
+
+__device__ __forceinline__ Mat16 load_mat(const float* __restrict__ p) {
+  Mat16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r.m[i] = p[i];
+  return r;
+}
+
+// cov3d from scale and rotation (fastgs_preprocess.metal:207-231).
+__device__ __forceinline__ void cov3d_from_sr(float sx, float sy, float sz, float mod, float4 q,
+                                              float out[6]) {
+  const float r = q.x, x = q.y, y = q.z, z = q.w;
+  float R[3][3];
+  R[0][0] = 1.0f - 2.0f * (y * y + z * z);
+  R[0][1] = 2.0f * (x * y - r * z);
+  R[0][2] = 2.0f * (x * z + r * y);
+  R[1][0] = 2.0f * (x * y + r * z);
+  R[1][1] = 1.0f - 2.0f * (x * x + z * z);
+  R[1][2] = 2.0f * (y * z - r * x);
+  R[2][0] = 2.0f * (x * z - r * y);
+  R[2][1] = 2.0f * (y * z + r * x);
+  R[2][2] = 1.0f - 2.0f * (x * x + y * y);
+  const float s[3] = {mod * sx, mod * sy, mod * sz};
+  float M[3][3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c)
+#pragma unroll
+    for (int rr = 0; rr < 3; ++rr) M[c][rr] = s[rr] * R[c][rr];
+#define FGS_SIG(i, j) (M[j][0] * M[i][0] + M[j][1] * M[i][1] + M[j][2] * M[i][2])
+  out[0] = FGS_SIG(0, 0);
+  out[1] = FGS_SIG(0, 1);
+  out[2] = FGS_SIG(0, 2);
+  out[3] = FGS_SIG(1, 1);
+  out[4] = FGS_SIG(1, 2);
+  out[5] = FGS_SIG(2, 2);
+#undef FGS_SIG
+}
+
+struct Cov2D {
+  float t0, t1, t2;
+  float txtz, tytz, limx, limy;
+  float T[2][3];  // T[col][row]; third column is zero
+  float cov00, cov01, cov11;
+};
+
+// EWA cov2D (fastgs_preprocess.metal:171-205).  W = R (columns of the view
+// rotation), T = W*J, cov = T^T Vrk T; zero terms of the products omitted.
+__device__ __forceinline__ void cov2d_eval(const Mat16& V, float mx, float my, float mz, float fx,
+                                           float fy, float tan_fovx, float tan_fovy,
+                                           const float c3[6], Cov2D& o) {
+  float t0 = V.m[0] * mx + V.m[4] * my + V.m[8] * mz + V.m[12];
+  float t1 = V.m[1] * mx + V.m[5] * my + V.m[9] * mz + V.m[13];
+  const float t2 = V.m[2] * mx + V.m[6] * my + V.m[10] * mz + V.m[14];
+  const float limx = 1.3f * tan_fovx;
+  const float limy = 1.3f * tan_fovy;
+  const float txtz = t0 / t2;
+  const float tytz = t1 / t2;
+  t0 = fminf(limx, fmaxf(-limx, txtz)) * t2;
+  t1 = fminf(limy, fmaxf(-limy, tytz)) * t2;
+  o.t0 = t0;
+  o.t1 = t1;
+  o.t2 = t2;
+  o.txtz = txtz;
+  o.tytz = tytz;
+  o.limx = limx;
+  o.limy = limy;
+  const float j00 = fx / t2;
+  const float j02 = -(fx * t0) / (t2 * t2);
+  const float j11 = fy / t2;
+  const float j12 = -(fy * t1) / (t2 * t2);
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    o.T[0][r] = V.m[0 + r] * j00 + V.m[8 + r] * j02;
+    o.T[1][r] = V.m[4 + r] * j11 + V.m[8 + r] * j12;
+  }
+  const float Vr[3][3] = {{c3[0], c3[1], c3[2]}, {c3[1], c3[3], c3[4]}, {c3[2], c3[4], c3[5]}};
+  float U[2][3];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+      U[c][s] = o.T[c][0] * Vr[0][s] + o.T[c][1] * Vr[1][s] + o.T[c][2] * Vr[2][s];
+  o.cov00 = U[0][0] * o.T[0][0] + U[0][1] * o.T[0][1] + U[0][2] * o.T[0][2];
+  o.cov01 = U[1][0] * o.T[0][0] + U[1][1] * o.T[0][1] + U[1][2] * o.T[0][2];
+  o.cov11 = U[1][0] * o.T[1][0] + U[1][1] * o.T[1][1] + U[1][2] * o.T[1][2];
+}
+
+__global__ void __launch_bounds__(256)
+preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_io io,
+                      float focal_x, float focal_y) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= prm.P) return;
+  const size_t I = (size_t)i;
+  const float mx = io.means3d[3 * I + 0];
+  const float my = io.means3d[3 * I + 1];
+  const float mz = io.means3d[3 * I + 2];
+  const Mat16 V = load_mat(io.viewmatrix);
+  int32_t radius = 0;
+  uint32_t cnt = 0;
+  float xy0 = 0.f, xy1 = 0.f, depth = 0.f;
+  float4 co = make_float4(0.f, 0.f, 0.f, 0.f);
+  float col[3] = {0.f, 0.f, 0.f};
+  uint8_t clamp[3] = {0, 0, 0};
+  float4 vsp = make_float4(0.f, 0.f, 0.f, 0.f);
+  float c3[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // p_view (in_frustum, :96-115)
+  const float pv0 = V.m[0] * mx + V.m[4] * my + V.m[8] * mz + V.m[12];
+  const float pv1 = V.m[1] * mx + V.m[5] * my + V.m[9] * mz + V.m[13];
+  const float pv2 = V.m[2] * mx + V.m[6] * my + V.m[10] * mz + V.m[14];
+  if (pv2 > 0.2f) {
+    const Mat16 Pm = load_mat(io.projmatrix);
+    const float ph0 = Pm.m[0] * mx + Pm.m[4] * my + Pm.m[8] * mz + Pm.m[12];
+    const float ph1 = Pm.m[1] * mx + Pm.m[5] * my + Pm.m[9] * mz + Pm.m[13];
+    const float ph3 = Pm.m[3] * mx + Pm.m[7] * my + Pm.m[11] * mz + Pm.m[15];
+    const float p_w = 1.0f / (ph3 + 1.0e-7f);
+    const float pp0 = ph0 * p_w;
+    const float pp1 = ph1 * p_w;
+    if (prm.use_cov3d_precomp) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) c3[k] = io.cov3d_precomp[6 * I + k];
+    } else {
+      const float4 q = make_float4(io.rotations[4 * I + 0], io.rotations[4 * I + 1],
+                                   io.rotations[4 * I + 2], io.rotations[4 * I + 3]);
+      cov3d_from_sr(io.scales[3 * I + 0], io.scales[3 * I + 1], io.scales[3 * I + 2],
+                    prm.scale_modifier, q, c3);
+    }
+    Cov2D cv;
+    cov2d_eval(V, mx, my, mz, focal_x, focal_y, prm.tan_fovx, prm.tan_fovy, c3, cv);
+    const float cx = cv.cov00 + 0.3f, cy = cv.cov01, cz = cv.cov11 + 0.3f;
+    const float det = cx * cz - cy * cy;
+    if (det != 0.0f) {
+      const float det_inv = 1.0f / det;
+      const float conic0 = cz * det_inv, conic1 = -cy * det_inv, conic2 = cx * det_inv;
+      const float mid = 0.5f * (cx + cz);
+      const float lambda1 = mid + __builtin_sqrtf(fmaxf(0.1f, mid * mid - det));
+      const float lambda2 = mid - __builtin_sqrtf(fmaxf(0.1f, mid * mid - det));
+      const float my_radius = ceilf(3.0f * __builtin_sqrtf(fmaxf(lambda1, lambda2)));
+      const float px = ((pp0 + 1.0f) * (float)prm.image_width - 1.0f) * 0.5f;
+      const float py = ((pp1 + 1.0f) * (float)prm.image_height - 1.0f) * 0.5f;
+      const float4 con_o = make_float4(conic0, conic1, conic2, io.opacities[I]);
+      const uint32_t n = tiles_walk(px, py, con_o, prm.grid_x, prm.grid_y, prm.mult, NoEmit{});
+      if (n != 0u) {
+        if (prm.use_colors_precomp) {
+#pragma unroll
+          for (int c = 0; c < 3; ++c) col[c] = io.colors_precomp[3 * I + c];
+        } else {
+          const float v0 = mx - io.campos[0], v1 = my - io.campos[1], v2 = mz - io.campos[2];
+          const float len = __builtin_sqrtf(v0 * v0 + v1 * v1 + v2 * v2);
+          const float x = v0 / len, y = v1 / len, z = v2 / len;
+          const float* __restrict__ s = io.sh + I * (size_t)prm.max_sh_coeffs * 3;
+          const float* __restrict__ d = io.dc + 3 * I;
+          const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+#pragma unroll
+          for (int c = 0; c < 3; ++c) {
+            float res = kSH_C0 * d[c];
+            if (prm.degree > 0) {
+              res = res - kSH_C1 * y * s[0 * 3 + c] + kSH_C1 * z * s[1 * 3 + c] -
+                    kSH_C1 * x * s[2 * 3 + c];
+              if (prm.degree > 1) {
+                res += kSH_C2[0] * xy * s[3 * 3 + c] + kSH_C2[1] * yz * s[4 * 3 + c] +
+                       kSH_C2[2] * (2.0f * zz - xx - yy) * s[5 * 3 + c] +
+                       kSH_C2[3] * xz * s[6 * 3 + c] + kSH_C2[4] * (xx - yy) * s[7 * 3 + c];
+                if (prm.degree > 2) {
+                  res += kSH_C3[0] * y * (3.0f * xx - yy) * s[8 * 3 + c] +
+                         kSH_C3[1] * xy * z * s[9 * 3 + c] +
+                         kSH_C3[2] * y * (4.0f * zz - xx - yy) * s[10 * 3 + c] +
+                         kSH_C3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy) * s[11 * 3 + c] +
+                         kSH_C3[4] * x * (4.0f * zz - xx - yy) * s[12 * 3 + c] +
+                         kSH_C3[5] * z * (xx - yy) * s[13 * 3 + c] +
+                         kSH_C3[6] * x * (xx - 3.0f * yy) * s[14 * 3 + c];
+                }
+              }
+            }
+            res += 0.5f;
+            clamp[c] = res < 0.0f;
+            col[c] = fmaxf(res, 0.0f);
+          }
+        }
+        depth = pv2;
+        radius = f2i(my_radius);
+        xy0 = px;
+        xy1 = py;
+        co = con_o;
+        cnt = n;
+        vsp = make_float4(pv0, pv1, pv2, io.viewspace_in[4 * I + 3]);
+      }
+    }
+  }
+  io.radii[I] = radius;
+  io.tiles_touched[I] = cnt;
+  io.depths[I] = depth;
+  *reinterpret_cast<float2*>(io.xys + 2 * I) = make_float2(xy0, xy1);
+  *reinterpret_cast<float4*>(io.conic_opacity + 4 * I) = co;
+  *reinterpret_cast<float4*>(io.viewspace_out + 4 * I) = vsp;
+  float2* c3o = reinterpret_cast<float2*>(io.cov3d + 6 * I);
+  c3o[0] = make_float2(c3[0], c3[1]);
+  c3o[1] = make_float2(c3[2], c3[3]);
+  c3o[2] = make_float2(c3[4], c3[5]);
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    io.rgb[3 * I + c] = col[c];
+    io.clamped[3 * I + c] = clamp[c];
+  }
+}
+
+__global__ void __launch_bounds__(256)
+preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_io io,
+                      float focal_x, float focal_y) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= prm.P) return;
+  const size_t I = (size_t)i;
+  const int msh = prm.max_sh_coeffs;
+  float dm[3] = {0.f, 0.f, 0.f};
+  float ddc[3] = {0.f, 0.f, 0.f};
+  float dcol[3] = {0.f, 0.f, 0.f};
+  float dop = 0.f;
+  float dsc[3] = {0.f, 0.f, 0.f};
+  float dq[4] = {0.f, 0.f, 0.f, 0.f};
+  float4 dvsp = make_float4(0.f, 0.f, 0.f, 0.f);
+  float* __restrict__ ds = io.dL_dsh ? io.dL_dsh + I * (size_t)msh * 3 : nullptr;
+  int sh_written = 0;  // number of rest coefficients written below
+  if (io.radii[I] > 0) {
+    const float px = io.means3d[3 * I + 0], py = io.means3d[3 * I + 1], pz = io.means3d[3 * I + 2];
+    const Mat16 V = load_mat(io.viewmatrix);
+    const Mat16 Pm = load_mat(io.projmatrix);
+    const float ph3 = Pm.m[3] * px + Pm.m[7] * py + Pm.m[11] * pz + Pm.m[15];
+    const float gx = io.dL_dxys ? io.dL_dxys[2 * I + 0] : 0.f;
+    const float gy = io.dL_dxys ? io.dL_dxys[2 * I + 1] : 0.f;
+    float cg0 = 0.f, cg1 = 0.f, cg2 = 0.f, cg3 = 0.f;
+    if (io.dL_dconic_opacity) {
+      const float4 g = *reinterpret_cast<const float4*>(io.dL_dconic_opacity + 4 * I);
+      cg0 = g.x;
+      cg1 = g.y;
+      cg2 = g.z;
+      cg3 = g.w;
+    }
+    const float* __restrict__ cs =
+        (prm.use_cov3d_precomp ? io.cov3d_precomp : io.cov3d_fwd) + 6 * I;
+    float c3[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) c3[k] = cs[k];
+    float dcov_extra[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float dmc[3];
+    {
+      Cov2D cv;
+      cov2d_eval(V, px, py, pz, focal_x, focal_y, prm.tan_fovx, prm.tan_fovy, c3, cv);
+      const float x_grad_mul = (cv.txtz < -cv.limx || cv.txtz > cv.limx) ? 0.0f : 1.0f;
+      const float y_grad_mul = (cv.tytz < -cv.limy || cv.tytz > cv.limy) ? 0.0f : 1.0f;
+      // Metal indexing Tm[c][r]; the third column is zero.
+      float Tm[3][3];
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+        Tm[0][r] = cv.T[0][r];
+        Tm[1][r] = cv.T[1][r];
+        Tm[2][r] = 0.0f;
+      }
+      const float Vrk[3][3] = {{c3[0], c3[1], c3[2]}, {c3[1], c3[3], c3[4]}, {c3[2], c3[4], c3[5]}};
+      float Wm[3][3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+#pragma unroll
+        for (int r = 0; r < 3; ++r) Wm[c][r] = V.m[4 * c + r];
+      const float a = cv.cov00 + 0.3f;
+      const float b = cv.cov01;
+      const float c = cv.cov11 + 0.3f;
+      const float denom = a * c - b * b;
+      const float denom2inv = 1.0f / ((denom * denom) + 1e-7f);
+      float dL_da = 0.f, dL_db = 0.f, dL_dc = 0.f;
+      if (denom2inv != 0.0f) {
+        dL_da = denom2inv * (-c * c * cg0 + 2.0f * b * c * cg1 + (denom - a * c) * cg2);
+        dL_dc = denom2inv * (-a * a * cg2 + 2.0f * a * b * cg1 + (denom - a * c) * cg0);
+        dL_db = denom2inv * 2.0f * (b * c * cg0 - (denom + 2.0f * b * b) * cg1 + a * b * cg2);
+        dcov_extra[0] = (Tm[0][0] * Tm[0][0] * dL_da + Tm[0][0] * Tm[1][0] * dL_db + Tm[1][0] * Tm[1][0] * dL_dc);
+        dcov_extra[3] = (Tm[0][1] * Tm[0][1] * dL_da + Tm[0][1] * Tm[1][1] * dL_db + Tm[1][1] * Tm[1][1] * dL_dc);
+        dcov_extra[5] = (Tm[0][2] * Tm[0][2] * dL_da + Tm[0][2] * Tm[1][2] * dL_db + Tm[1][2] * Tm[1][2] * dL_dc);
+        dcov_extra[1] = 2.0f * Tm[0][0] * Tm[0][1] * dL_da + (Tm[0][0] * Tm[1][1] + Tm[0][1] * Tm[1][0]) * dL_db + 2.0f * Tm[1][0] * Tm[1][1] * dL_dc;
+        dcov_extra[2] = 2.0f * Tm[0][0] * Tm[0][2] * dL_da + (Tm[0][0] * Tm[1][2] + Tm[0][2] * Tm[1][0]) * dL_db + 2.0f * Tm[1][0] * Tm[1][2] * dL_dc;
+        dcov_extra[4] = 2.0f * Tm[0][2] * Tm[0][1] * dL_da + (Tm[0][1] * Tm[1][2] + Tm[0][2] * Tm[1][1]) * dL_db + 2.0f * Tm[1][1] * Tm[1][2] * dL_dc;
+      }
+      const float dL_dT00 = 2.0f * (Tm[0][0] * Vrk[0][0] + Tm[0][1] * Vrk[0][1] + Tm[0][2] * Vrk[0][2]) * dL_da +
+                            (Tm[1][0] * Vrk[0][0] + Tm[1][1] * Vrk[0][1] + Tm[1][2] * Vrk[0][2]) * dL_db;
+      const float dL_dT01 = 2.0f * (Tm[0][0] * Vrk[1][0] + Tm[0][1] * Vrk[1][1] + Tm[0][2] * Vrk[1][2]) * dL_da +
+                            (Tm[1][0] * Vrk[1][0] + Tm[1][1] * Vrk[1][1] + Tm[1][2] * Vrk[1][2]) * dL_db;
+      const float dL_dT02 = 2.0f * (Tm[0][0] * Vrk[2][0] + Tm[0][1] * Vrk[2][1] + Tm[0][2] * Vrk[2][2]) * dL_da +
+                            (Tm[1][0] * Vrk[2][0] + Tm[1][1] * Vrk[2][1] + Tm[1][2] * Vrk[2][2]) * dL_db;
+      const float dL_dT10 = 2.0f * (Tm[1][0] * Vrk[0][0] + Tm[1][1] * Vrk[0][1] + Tm[1][2] * Vrk[0][2]) * dL_dc +
+                            (Tm[0][0] * Vrk[0][0] + Tm[0][1] * Vrk[0][1] + Tm[0][2] * Vrk[0][2]) * dL_db;
+      const float dL_dT11 = 2.0f * (Tm[1][0] * Vrk[1][0] + Tm[1][1] * Vrk[1][1] + Tm[1][2] * Vrk[1][2]) * dL_dc +
+                            (Tm[0][0] * Vrk[1][0] + Tm[0][1] * Vrk[1][1] + Tm[0][2] * Vrk[1][2]) * dL_db;
+      const float dL_dT12 = 2.0f * (Tm[1][0] * Vrk[2][0] + Tm[1][1] * Vrk[2][1] + Tm[1][2] * Vrk[2][2]) * dL_dc +
+                            (Tm[0][0] * Vrk[2][0] + Tm[0][1] * Vrk[2][1] + Tm[0][2] * Vrk[2][2]) * dL_db;
+      const float dL_dJ00 = Wm[0][0] * dL_dT00 + Wm[0][1] * dL_dT01 + Wm[0][2] * dL_dT02;
+      const float dL_dJ02 = Wm[2][0] * dL_dT00 + Wm[2][1] * dL_dT01 + Wm[2][2] * dL_dT02;
+      const float dL_dJ11 = Wm[1][0] * dL_dT10 + Wm[1][1] * dL_dT11 + Wm[1][2] * dL_dT12;
+      const float dL_dJ12 = Wm[2][0] * dL_dT10 + Wm[2][1] * dL_dT11 + Wm[2][2] * dL_dT12;
+      const float tz = 1.0f / cv.t2;
+      const float tz2 = tz * tz;
+      const float tz3 = tz2 * tz;
+      const float dL_dtx = x_grad_mul * -focal_x * tz2 * dL_dJ02;
+      const float dL_dty = y_grad_mul * -focal_y * tz2 * dL_dJ12;
+      const float dL_dtz = -focal_x * tz2 * dL_dJ00 - focal_y * tz2 * dL_dJ11 +
+                           (2.0f * focal_x * cv.t0) * tz3 * dL_dJ02 +
+                           (2.0f * focal_y * cv.t1) * tz3 * dL_dJ12;
+      dmc[0] = V.m[0] * dL_dtx + V.m[1] * dL_dty + V.m[2] * dL_dtz;
+      dmc[1] = V.m[4] * dL_dtx + V.m[5] * dL_dty + V.m[6] * dL_dtz;
+      dmc[2] = V.m[8] * dL_dtx + V.m[9] * dL_dty + V.m[10] * dL_dtz;
+    }
+    const float m_w = 1.0f / (ph3 + 1.0e-7f);
+    const float mul1 = (Pm.m[0] * px + Pm.m[4] * py + Pm.m[8] * pz + Pm.m[12]) * m_w * m_w;
+    const float mul2 = (Pm.m[1] * px + Pm.m[5] * py + Pm.m[9] * pz + Pm.m[13]) * m_w * m_w;
+    const float dmx = (Pm.m[0] * m_w - Pm.m[3] * mul1) * gx + (Pm.m[1] * m_w - Pm.m[3] * mul2) * gy;
+    const float dmy = (Pm.m[4] * m_w - Pm.m[7] * mul1) * gx + (Pm.m[5] * m_w - Pm.m[7] * mul2) * gy;
+    const float dmz = (Pm.m[8] * m_w - Pm.m[11] * mul1) * gx + (Pm.m[9] * m_w - Pm.m[11] * mul2) * gy;
+    dm[0] = dmx + dmc[0];
+    dm[1] = dmy + dmc[1];
+    dm[2] = dmz + dmc[2];
+    dop = cg3;
+    float drgb[3] = {0.f, 0.f, 0.f};
+    if (io.dL_drgb) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) drgb[c] = io.dL_drgb[3 * I + c];
+    }
+    if (prm.use_colors_precomp) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) dcol[c] = drgb[c];
+    } else {
+      float dRGB[3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) dRGB[c] = io.clamped[3 * I + c] ? 0.0f : drgb[c];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) ddc[c] = kSH_C0 * dRGB[c];
+      if (prm.degree > 0 && msh >= 3) {
+        const float d0 = px - io.campos[0], d1 = py - io.campos[1], d2 = pz - io.campos[2];
+        const float len = __builtin_sqrtf(d0 * d0 + d1 * d1 + d2 * d2);
+        const float x = d0 / len, y = d1 / len, z = d2 / len;
+        const float* __restrict__ s = io.sh + I * (size_t)msh * 3;
+        float dRGBdx[3], dRGBdy[3], dRGBdz[3];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          ds[0 * 3 + c] = (-kSH_C1 * y) * dRGB[c];
+          ds[1 * 3 + c] = (kSH_C1 * z) * dRGB[c];
+          ds[2 * 3 + c] = (-kSH_C1 * x) * dRGB[c];
+          dRGBdx[c] = -kSH_C1 * s[2 * 3 + c];
+          dRGBdy[c] = -kSH_C1 * s[0 * 3 + c];
+          dRGBdz[c] = kSH_C1 * s[1 * 3 + c];
+        }
+        sh_written = 3;
+        if (prm.degree > 1 && msh >= 8) {
+          const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+#pragma unroll
+          for (int c = 0; c < 3; ++c) {
+            ds[3 * 3 + c] = (kSH_C2[0] * xy) * dRGB[c];
+            ds[4 * 3 + c] = (kSH_C2[1] * yz) * dRGB[c];
+            ds[5 * 3 + c] = (kSH_C2[2] * (2.0f * zz - xx - yy)) * dRGB[c];
+            ds[6 * 3 + c] = (kSH_C2[3] * xz) * dRGB[c];
+            ds[7 * 3 + c] = (kSH_C2[4] * (xx - yy)) * dRGB[c];
+            const float s3 = s[3 * 3 + c], s4 = s[4 * 3 + c], s5 = s[5 * 3 + c], s6 = s[6 * 3 + c],
+                        s7 = s[7 * 3 + c];
+            dRGBdx[c] += kSH_C2[0] * y * s3 + kSH_C2[2] * 2.0f * -x * s5 + kSH_C2[3] * z * s6 +
+                         kSH_C2[4] * 2.0f * x * s7;
+            dRGBdy[c] += kSH_C2[0] * x * s3 + kSH_C2[1] * z * s4 + kSH_C2[2] * 2.0f * -y * s5 +
+                         kSH_C2[4] * 2.0f * -y * s7;
+            dRGBdz[c] += kSH_C2[1] * y * s4 + kSH_C2[2] * 4.0f * z * s5 + kSH_C2[3] * x * s6;
+          }
+          sh_written = 8;
+          if (prm.degree > 2 && msh >= 15) {
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+              ds[8 * 3 + c] = (kSH_C3[0] * y * (3.0f * xx - yy)) * dRGB[c];
+              ds[9 * 3 + c] = (kSH_C3[1] * xy * z) * dRGB[c];
+              ds[10 * 3 + c] = (kSH_C3[2] * y * (4.0f * zz - xx - yy)) * dRGB[c];
+              ds[11 * 3 + c] = (kSH_C3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy)) * dRGB[c];
+              ds[12 * 3 + c] = (kSH_C3[4] * x * (4.0f * zz - xx - yy)) * dRGB[c];
+              ds[13 * 3 + c] = (kSH_C3[5] * z * (xx - yy)) * dRGB[c];
+              ds[14 * 3 + c] = (kSH_C3[6] * x * (xx - 3.0f * yy)) * dRGB[c];
+              const float s8 = s[8 * 3 + c], s9 = s[9 * 3 + c], s10 = s[10 * 3 + c],
+                          s11 = s[11 * 3 + c], s12 = s[12 * 3 + c], s13 = s[13 * 3 + c],
+                          s14 = s[14 * 3 + c];
+              dRGBdx[c] += (kSH_C3[0] * s8 * 6.0f * xy + kSH_C3[1] * s9 * yz +
+                            kSH_C3[2] * s10 * -2.0f * xy + kSH_C3[3] * s11 * -6.0f * xz +
+                            kSH_C3[4] * s12 * (-3.0f * xx + 4.0f * zz - yy) +
+                            kSH_C3[5] * s13 * 2.0f * xz + kSH_C3[6] * s14 * 3.0f * (xx - yy));
+              dRGBdy[c] += (kSH_C3[0] * s8 * 3.0f * (xx - yy) + kSH_C3[1] * s9 * xz +
+                            kSH_C3[2] * s10 * (-3.0f * yy + 4.0f * zz - xx) +
+                            kSH_C3[3] * s11 * -6.0f * yz + kSH_C3[4] * s12 * -2.0f * xy +
+                            kSH_C3[5] * s13 * -2.0f * yz + kSH_C3[6] * s14 * -6.0f * xy);
+              dRGBdz[c] += (kSH_C3[1] * s9 * xy + kSH_C3[2] * s10 * 8.0f * yz +
+                            kSH_C3[3] * s11 * 3.0f * (2.0f * zz - xx - yy) +
+                            kSH_C3[4] * s12 * 8.0f * xz + kSH_C3[5] * s13 * (xx - yy));
+            }
+            sh_written = 15;
+          }
+        }
+        const float ddir0 = dRGBdx[0] * dRGB[0] + dRGBdx[1] * dRGB[1] + dRGBdx[2] * dRGB[2];
+        const float ddir1 = dRGBdy[0] * dRGB[0] + dRGBdy[1] * dRGB[1] + dRGBdy[2] * dRGB[2];
+        const float ddir2 = dRGBdz[0] * dRGB[0] + dRGBdz[1] * dRGB[1] + dRGBdz[2] * dRGB[2];
+        const float l = fmaxf(__builtin_sqrtf(d0 * d0 + d1 * d1 + d2 * d2), 1e-6f);
+        const float n0 = d0 / l, n1 = d1 / l, n2 = d2 / l;
+        const float nd = n0 * ddir0 + n1 * ddir1 + n2 * ddir2;
+        dm[0] += (ddir0 - n0 * nd) / l;
+        dm[1] += (ddir1 - n1 * nd) / l;
+        dm[2] += (ddir2 - n2 * nd) / l;
+      }
+    }
+    if (!prm.use_cov3d_precomp) {
+      const float r = io.rotations[4 * I + 0], x = io.rotations[4 * I + 1],
+                  y = io.rotations[4 * I + 2], z = io.rotations[4 * I + 3];
+      float R[3][3];
+      R[0][0] = 1.0f - 2.0f * (y * y + z * z);
+      R[0][1] = 2.0f * (x * y - r * z);
+      R[0][2] = 2.0f * (x * z + r * y);
+      R[1][0] = 2.0f * (x * y + r * z);
+      R[1][1] = 1.0f - 2.0f * (x * x + z * z);
+      R[1][2] = 2.0f * (y * z - r * x);
+      R[2][0] = 2.0f * (x * z - r * y);
+      R[2][1] = 2.0f * (y * z + r * x);
+      R[2][2] = 1.0f - 2.0f * (x * x + y * y);
+      const float s[3] = {prm.scale_modifier * io.scales[3 * I + 0],
+                          prm.scale_modifier * io.scales[3 * I + 1],
+                          prm.scale_modifier * io.scales[3 * I + 2]};
+      float M[3][3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+#pragma unroll
+        for (int rr = 0; rr < 3; ++rr) M[c][rr] = s[rr] * R[c][rr];
+      float cc[6];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) cc[k] = (io.dL_dcov3d ? io.dL_dcov3d[6 * I + k] : 0.0f) + dcov_extra[k];
+      const float dS[3][3] = {{cc[0], 0.5f * cc[1], 0.5f * cc[2]},
+                              {0.5f * cc[1], cc[3], 0.5f * cc[4]},
+                              {0.5f * cc[2], 0.5f * cc[4], cc[5]}};
+      float dM[3][3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+#pragma unroll
+        for (int rr = 0; rr < 3; ++rr)
+          dM[c][rr] = (2.0f * M[0][rr]) * dS[c][0] + (2.0f * M[1][rr]) * dS[c][1] +
+                      (2.0f * M[2][rr]) * dS[c][2];
+      float dMt[3][3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int bb = 0; bb < 3; ++bb) dMt[a][bb] = dM[bb][a];
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+        dsc[a] = R[0][a] * dMt[a][0] + R[1][a] * dMt[a][1] + R[2][a] * dMt[a][2];
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int bb = 0; bb < 3; ++bb) dMt[a][bb] *= s[a];
+      dq[0] = 2.0f * z * (dMt[0][1] - dMt[1][0]) + 2.0f * y * (dMt[2][0] - dMt[0][2]) + 2.0f * x * (dMt[1][2] - dMt[2][1]);
+      dq[1] = 2.0f * y * (dMt[1][0] + dMt[0][1]) + 2.0f * z * (dMt[2][0] + dMt[0][2]) + 2.0f * r * (dMt[1][2] - dMt[2][1]) - 4.0f * x * (dMt[2][2] + dMt[1][1]);
+      dq[2] = 2.0f * x * (dMt[1][0] + dMt[0][1]) + 2.0f * r * (dMt[2][0] - dMt[0][2]) + 2.0f * z * (dMt[1][2] + dMt[2][1]) - 4.0f * y * (dMt[2][2] + dMt[0][0]);
+      dq[3] = 2.0f * r * (dMt[0][1] - dMt[1][0]) + 2.0f * x * (dMt[2][0] + dMt[0][2]) + 2.0f * y * (dMt[1][2] + dMt[2][1]) - 4.0f * z * (dMt[1][1] + dMt[0][0]);
+    }
+    if (io.dL_dviewspace_out) dvsp = *reinterpret_cast<const float4*>(io.dL_dviewspace_out + 4 * I);
+  }
+  // Write every element of every gradient row.
+#pragma unroll
+  for (int k = 0; k < 3; ++k) io.dL_dmeans3d[3 * I + k] = dm[k];
+  if (io.dL_ddc)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) io.dL_ddc[3 * I + k] = ddc[k];
+  if (io.dL_dcolors_precomp)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) io.dL_dcolors_precomp[3 * I + k] = dcol[k];
+  io.dL_dopacities[I] = dop;
+  if (io.dL_dscales)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) io.dL_dscales[3 * I + k] = dsc[k];
+  if (io.dL_drotations)
+    *reinterpret_cast<float4*>(io.dL_drotations + 4 * I) = make_float4(dq[0], dq[1], dq[2], dq[3]);
+  *reinterpret_cast<float4*>(io.dL_dviewspace_in + 4 * I) = dvsp;
+  if (ds) {
+    for (int k = sh_written * 3; k < msh * 3; ++k) ds[k] = 0.0f;
+  }
+}
+
+}  // namespace fgs
+
+using namespace fgs;
+
+extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
+                                      const fgs_preprocess_fwd_io* io, void* stream) {
+  if (!p || !io) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: null argument");
+  if (p->P < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: P < 0");
+  if (p->P == 0) return FGS_OK;
+  if (!io->means3d || !io->opacities || !io->viewmatrix || !io->projmatrix || !io->campos ||
+      !io->viewspace_in || !io->radii || !io->xys || !io->depths || !io->cov3d || !io->rgb ||
+      !io->conic_opacity || !io->tiles_touched || !io->clamped || !io->viewspace_out)
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing tensor");
+  if (p->use_cov3d_precomp ? !io->cov3d_precomp : (!io->scales || !io->rotations))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing geometry tensors");
+  if (p->use_colors_precomp ? !io->colors_precomp : (!io->dc || (p->degree > 0 && !io->sh)))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing colour tensors");
+  if (!p->use_colors_precomp && p->degree > 0) {
+    const int d = p->degree > 3 ? 3 : p->degree;
+    if (p->max_sh_coeffs < (d + 1) * (d + 1) - 1)
+      return set_error(FGS_ERR_INVALID_ARGUMENT,
+                       "fgs_preprocess_fwd: sh has fewer coefficients than the degree needs");
+  }
+  if (p->image_width <= 0 || p->image_height <= 0 || p->grid_x <= 0 || p->grid_y <= 0)
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: bad image size");
+  const float fx = (float)p->image_width / (2.0f * p->tan_fovx);
+  const float fy = (float)p->image_height / (2.0f * p->tan_fovy);
+  const unsigned blocks = (unsigned)((p->P + 255) / 256);
+  hipLaunchKernelGGL(preprocess_fwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, *p,
+                     *io, fx, fy);
+  return check_launch("preprocess_fwd_kernel");
+}
+
+extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
+                                      const fgs_preprocess_bwd_io* io, void* stream) {
+  if (!p || !io) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: null argument");
+  if (p->P < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: P < 0");
+  if (p->P == 0) return FGS_OK;
+  if (!io->means3d || !io->viewmatrix || !io->projmatrix || !io->campos || !io->radii ||
+      !io->clamped || !io->dL_dmeans3d || !io->dL_dopacities || !io->dL_dviewspace_in)
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing tensor");
+  if (p->use_cov3d_precomp ? !io->cov3d_precomp
+                           : (!io->cov3d_fwd || !io->scales || !io->rotations))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing geometry tensors");
+  if (!p->use_colors_precomp && p->degree > 0 && p->max_sh_coeffs >= 3 && (!io->sh || !io->dL_dsh))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing sh tensors");
+  const float fx = 0.5f * (float)p->image_width / fmaxf(p->tan_fovx, 1e-6f);
+  const float fy = 0.5f * (float)p->image_height / fmaxf(p->tan_fovy, 1e-6f);
+  const unsigned blocks = (unsigned)((p->P + 255) / 256);
+  hipLaunchKernelGGL(preprocess_bwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, *p,
+                     *io, fx, fy);
+  return check_launch("preprocess_bwd_kernel");
+}

@@ -1,0 +1,569 @@
+"""FastGS rasterizer API on PyTorch-ROCm tensors (drop-in for fastgs_core).
+
+Function names, positional order, keyword defaults, dict keys and error
+classes follow the reference nanobind module ``_fastgs_core``
+(fastgs_core/binding/binding.cpp:512-610).  Arithmetic runs in the HIP
+kernels of libfastgs_hip.so; this module validates, allocates outputs with
+the torch caching allocator, and wires autograd:
+
+* ``_Preprocess`` mirrors the FastGSPreprocess primitive and its vjp
+  (fastgs_preprocess.cpp:41-78, 191-206);
+* ``_Rasterize`` mirrors FastGSRasterize and its vjp
+  (fastgs_rasterize.cpp:32-88, 191-206).
+
+The ``viewspace_points`` input of ``rasterize_gaussians`` flows into
+``_Preprocess`` and its pass-through output into ``_Rasterize``, so the
+screen-space gradients (x, y, |x|, |y|) reach the caller's tensor exactly as
+on the reference route.
+
+dtype map (reference -> here): uint32 -> torch.int32 (same bits), uint64 ->
+torch.int64 (keys < 2^63), bool -> torch.bool, int32/float32 unchanged.
+There is no CPU fallback: without a ROCm GPU every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Any, Dict, Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+
+TILE = 16
+
+# Whether rasterize_gaussians / rasterize_forward also produce the per-bucket
+# sampled state (sample_t / sample_ar).  The backward here does not need it;
+# at 1M Gaussians and 1080p it is ~1 GB of writes per forward, so it is off
+# unless requested (zero-size tensors are returned otherwise).
+WRITE_SAMPLED_STATE = False
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _device(t) -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("fastgs_core_amd requires a ROCm GPU (torch.cuda is unavailable); "
+                           "there is no CPU fallback")
+    if torch.is_tensor(t) and t.is_cuda:
+        return t.device
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _to(x, dev, dtype) -> Optional[torch.Tensor]:
+    if x is None:
+        return None
+    if not torch.is_tensor(x):
+        arr = np.asarray(x)
+        if arr.dtype == np.uint64:
+            arr = arr.view(np.int64)
+        elif arr.dtype == np.uint32:
+            arr = arr.view(np.int32)
+        x = torch.from_numpy(np.ascontiguousarray(arr))
+    if x.dtype in (torch.uint32,):
+        x = x.view(torch.int32)
+    elif x.dtype in (torch.uint64,):
+        x = x.view(torch.int64)
+    x = x.to(device=dev, dtype=dtype).contiguous()
+    if x.numel() and x.data_ptr() % 16:
+        x = x.clone()  # kernels use 8/16-byte vector loads
+    return x
+
+
+def _p(t: Optional[torch.Tensor]):
+    """Device pointer of a tensor (None for absent or empty tensors)."""
+    if t is None or t.numel() == 0:
+        return None
+    return t.data_ptr()
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _size(x) -> int:
+    if x is None:
+        return 0
+    if torch.is_tensor(x):
+        return x.numel()
+    return int(np.asarray(x).size)
+
+
+def _ndim_shape(x):
+    if x is None:
+        return 0, ()
+    if torch.is_tensor(x):
+        return x.dim(), tuple(x.shape)
+    a = np.asarray(x)
+    return a.ndim, a.shape
+
+
+def _empty_like_path(dev, *shape, dtype=torch.float32):
+    return torch.zeros(shape, dtype=dtype, device=dev)
+
+
+def _tile_bounds(W, H, bx, by):
+    return (W + bx - 1) // bx, (H + by - 1) // by, 1
+
+
+def _check_blocks(bx, by):
+    if bx != TILE or by != TILE:
+        raise ValueError(f"fastgs_core_amd supports 16x16 tiles only (got {bx}x{by}); the "
+                         "reference kernels hard-code BLOCK_X = BLOCK_Y = 16")
+
+
+def _check_sh(degree: int, max_sh: int, sh_path: bool):
+    if sh_path and degree > 0:
+        d = min(degree, 3)
+        need = (d + 1) ** 2 - 1
+        if max_sh < need:
+            raise ValueError(f"sh has {max_sh} rest coefficients per Gaussian; degree {degree} "
+                             f"needs {need}")
+
+
+# ---------------------------------------------------------------------------
+# autograd Functions
+# ---------------------------------------------------------------------------
+class _Preprocess(torch.autograd.Function):
+    """Preprocess forward + vjp (fastgs_preprocess.cpp:41-78, 191-206)."""
+
+    @staticmethod
+    def forward(ctx, cfg, means3d, dc, sh, colors_precomp, opacities, scales, rotations,
+                cov3d_precomp, viewmatrix, projmatrix, campos, viewspace_in):
+        lib = _lib.load()
+        dev = means3d.device
+        P = means3d.shape[0]
+        f32 = dict(dtype=torch.float32, device=dev)
+        radii = torch.empty(P, dtype=torch.int32, device=dev)
+        xys = torch.empty((P, 2), **f32)
+        depths = torch.empty(P, **f32)
+        cov3d = torch.empty((P, 6), **f32)
+        rgb = torch.empty((P, 3), **f32)
+        conic = torch.empty((P, 4), **f32)
+        tiles = torch.empty(P, dtype=torch.int32, device=dev)
+        clamped = torch.empty((P, 3), dtype=torch.bool, device=dev)
+        vsp_out = torch.empty((P, 4), **f32)
+        prm = _lib.PreprocessParams(P, cfg["degree"], cfg["max_sh"], cfg["W"], cfg["H"], cfg["gx"],
+                                    cfg["gy"], int(cfg["use_cov"]), int(cfg["use_col"]),
+                                    cfg["scale_modifier"], cfg["mult"], cfg["tan_fovx"],
+                                    cfg["tan_fovy"])
+        io = _lib.PreprocessFwdIO(
+            _p(means3d), _p(dc), _p(sh), _p(colors_precomp), _p(opacities), _p(scales),
+            _p(rotations), _p(cov3d_precomp), _p(viewmatrix), _p(projmatrix), _p(campos),
+            _p(viewspace_in), _p(radii), _p(xys), _p(depths), _p(cov3d), _p(rgb), _p(conic),
+            _p(tiles), _p(clamped), _p(vsp_out))
+        if P > 0:
+            _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+        ctx.cfg = cfg
+        ctx.opacity_shape = opacities.shape
+        ctx.sh_shape = None if sh is None else sh.shape
+        ctx.save_for_backward(means3d, sh, scales, rotations, cov3d_precomp, viewmatrix,
+                              projmatrix, campos, cov3d, radii, clamped)
+        ctx.mark_non_differentiable(radii, tiles, clamped)
+        return radii, xys, depths, cov3d, rgb, conic, tiles, clamped, vsp_out
+
+    @staticmethod
+    def backward(ctx, g_radii, g_xys, g_depths, g_cov3d, g_rgb, g_conic, g_tiles, g_clamped,
+                 g_vsp):
+        lib = _lib.load()
+        (means3d, sh, scales, rotations, cov3d_precomp, viewmatrix, projmatrix, campos, cov3d,
+         radii, clamped) = ctx.saved_tensors
+        cfg = ctx.cfg
+        dev = means3d.device
+        P = means3d.shape[0]
+        f32 = dict(dtype=torch.float32, device=dev)
+        c = lambda g: None if g is None else g.to(torch.float32).contiguous()  # noqa: E731
+        g_xys, g_rgb, g_conic, g_cov3d, g_vsp = c(g_xys), c(g_rgb), c(g_conic), c(g_cov3d), c(g_vsp)
+        d_means3d = torch.empty((P, 3), **f32)
+        sh_path = not cfg["use_col"]
+        d_dc = torch.empty((P, 3), **f32) if sh_path else None
+        d_sh = torch.empty(ctx.sh_shape, **f32) if (sh_path and sh is not None) else None
+        d_col = torch.empty((P, 3), **f32) if not sh_path else None
+        d_opac = torch.empty(P, **f32)
+        d_scales = torch.empty((P, 3), **f32) if not cfg["use_cov"] else None
+        d_rot = torch.empty((P, 4), **f32) if not cfg["use_cov"] else None
+        d_vsp = torch.empty((P, 4), **f32)
+        prm = _lib.PreprocessParams(P, cfg["degree"], cfg["max_sh"], cfg["W"], cfg["H"], cfg["gx"],
+                                    cfg["gy"], int(cfg["use_cov"]), int(cfg["use_col"]),
+                                    cfg["scale_modifier"], cfg["mult"], cfg["tan_fovx"],
+                                    cfg["tan_fovy"])
+        io = _lib.PreprocessBwdIO(
+            _p(means3d), _p(scales), _p(rotations), _p(viewmatrix), _p(projmatrix), _p(campos),
+            _p(sh), _p(cov3d_precomp), _p(cov3d), _p(radii), _p(clamped), _p(g_xys), _p(g_rgb),
+            _p(g_conic), _p(g_cov3d), _p(g_vsp), _p(d_means3d), _p(d_dc), _p(d_sh), _p(d_col),
+            _p(d_opac), _p(d_scales), _p(d_rot), _p(d_vsp))
+        if P > 0:
+            _lib.check(lib.fgs_preprocess_bwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+        need = ctx.needs_input_grad
+        d_cov_pre = torch.zeros_like(cov3d_precomp) if (cov3d_precomp is not None and need[8]) \
+            else None
+        return (None, d_means3d, d_dc, d_sh, d_col, d_opac.view(ctx.opacity_shape), d_scales,
+                d_rot, d_cov_pre,
+                torch.zeros_like(viewmatrix) if need[9] else None,
+                torch.zeros_like(projmatrix) if need[10] else None,
+                torch.zeros_like(campos) if need[11] else None, d_vsp)
+
+
+class _Rasterize(torch.autograd.Function):
+    """Rasterize forward + vjp (fastgs_rasterize.cpp:32-88, 191-206)."""
+
+    @staticmethod
+    def forward(ctx, cfg, ranges, point_list, bucket_offsets, means2d, colors, conic_opacity,
+                background, radii, metric_map, metric_count, viewspace_points):
+        lib = _lib.load()
+        dev = means2d.device
+        W, H, C, T, B = cfg["W"], cfg["H"], cfg["C"], cfg["T"], cfg["B"]
+        P = means2d.shape[0]
+        HW = W * H
+        f32 = dict(dtype=torch.float32, device=dev)
+        ws = bool(cfg["write_sampled"])
+        ss = B * 256 if ws else 0
+        bucket_to_tile = torch.empty(B, dtype=torch.int32, device=dev)
+        sampled_t = torch.empty(ss, **f32)
+        sampled_ar = torch.empty((C, ss), **f32)
+        final_t = torch.empty(HW, **f32)
+        n_contrib = torch.empty(HW, dtype=torch.int32, device=dev)
+        max_contrib = torch.empty(T, dtype=torch.int32, device=dev)
+        pixel_colors = torch.empty((C, HW), **f32)
+        out_color = torch.empty((C, HW), **f32)
+        get_flag = bool(cfg["get_flag"])
+        mc = torch.zeros(metric_count.shape, dtype=torch.int32, device=dev)
+        if get_flag and mc.numel() < P:
+            raise ValueError(f"metric_count has {mc.numel()} entries, get_flag needs one per "
+                             f"Gaussian ({P})")
+        prm = _lib.RasterParams(W, H, C, T, B, int(get_flag), int(ws), P, point_list.numel())
+        io = _lib.RasterFwdIO(
+            _p(ranges), _p(point_list), _p(bucket_offsets), _p(means2d), _p(colors),
+            _p(conic_opacity), _p(background), _p(metric_map), _p(bucket_to_tile),
+            _p(sampled_t), _p(sampled_ar), _p(final_t), _p(n_contrib), _p(max_contrib),
+            _p(pixel_colors), _p(out_color), _p(mc))
+        _lib.check(lib.fgs_rasterize_fwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+        ctx.cfg = cfg
+        ctx.save_for_backward(ranges, point_list, means2d, colors, conic_opacity, background,
+                              final_t, n_contrib, max_contrib)
+        ctx.mark_non_differentiable(bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib,
+                                    max_contrib, mc)
+        return (bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib, max_contrib,
+                pixel_colors, out_color, mc)
+
+    @staticmethod
+    def backward(ctx, g_b2t, g_st, g_sar, g_ft, g_nc, g_mc, g_pc, g_out, g_metric):
+        lib = _lib.load()
+        (ranges, point_list, means2d, colors, conic_opacity, background, final_t, n_contrib,
+         max_contrib) = ctx.saved_tensors
+        cfg = ctx.cfg
+        dev = means2d.device
+        W, H, C, T, B = cfg["W"], cfg["H"], cfg["C"], cfg["T"], cfg["B"]
+        P = means2d.shape[0]
+        f32 = dict(dtype=torch.float32, device=dev)
+        if g_out is None:
+            g_out = torch.zeros((C, W * H), **f32)
+        g_out = g_out.to(torch.float32).contiguous()
+        d_means2d = torch.empty((P, 2), **f32)
+        d_colors = torch.empty((P, colors.shape[1] if colors.dim() == 2 else C), **f32)
+        d_conic = torch.empty((P, 4), **f32)
+        d_vsp = torch.empty((P, 4), **f32)
+        prm = _lib.RasterParams(W, H, C, T, B, 0, 0, P, point_list.numel())
+        io = _lib.RasterBwdIO(
+            _p(ranges), _p(point_list), _p(means2d), _p(colors), _p(conic_opacity),
+            _p(background), _p(final_t), _p(n_contrib), _p(max_contrib), _p(g_out),
+            _p(d_means2d), _p(d_colors), _p(d_conic), _p(d_vsp))
+        _lib.check(lib.fgs_rasterize_bwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+        need = ctx.needs_input_grad
+        d_bg = torch.zeros_like(background) if need[7] else None
+        return (None, None, None, None, d_means2d, d_colors.view(colors.shape), d_conic, d_bg,
+                None, None, None, d_vsp)
+
+
+# ---------------------------------------------------------------------------
+# stage helpers shared by the public functions
+# ---------------------------------------------------------------------------
+def _inclusive_scan_i32(x: torch.Tensor) -> torch.Tensor:
+    lib = _lib.load()
+    n = x.numel()
+    out = torch.empty(n, dtype=torch.int32, device=x.device)
+    if n == 0:
+        return out
+    ws = torch.empty(int(lib.fgs_scan_workspace_bytes(n)), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(out), n, _p(ws), _stream(x.device)))
+    return out
+
+
+def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: float):
+    lib = _lib.load()
+    dev = xys.device
+    P = xys.shape[0]
+    T = gx * gy
+    keys = torch.empty(K, dtype=torch.int64, device=dev)
+    plist = torch.empty(K, dtype=torch.int32, device=dev)
+    ranges = torch.empty((T, 2), dtype=torch.int32, device=dev)
+    bucket_count = torch.empty(T, dtype=torch.int32, device=dev)
+    bucket_offsets = torch.empty(T, dtype=torch.int32, device=dev)
+    ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
+    io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
+                        _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws))
+    _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
+    return keys, plist, ranges, bucket_count, bucket_offsets
+
+
+def _last_u32(t: torch.Tensor) -> int:
+    """read_last_u32 (binding.cpp:25-31): one blocking 4-byte read."""
+    if t.numel() == 0:
+        return 0
+    return int(t[-1].item()) & 0xFFFFFFFF
+
+
+# ---------------------------------------------------------------------------
+# public API (binding.cpp:512-610)
+# ---------------------------------------------------------------------------
+def dummy_add(a, b):
+    """binding.cpp:514 (build smoke of the reference)."""
+    return a + b
+
+
+def dummy_array_size(a) -> int:
+    """binding.cpp:515-518."""
+    return int(a.numel()) if torch.is_tensor(a) else int(np.asarray(a).size)
+
+
+def _colour_and_geometry(inputs: Dict[str, Any], fn: str, col_keys, rot_key: str):
+    col = None
+    for k in col_keys:
+        if _size(inputs.get(k)) != 0:
+            col = inputs[k]
+            break
+    has_dc, has_sh = "dc" in inputs, "sh" in inputs
+    has_col = col is not None
+    if has_col == (has_dc and has_sh):
+        alt = "colors_precomp (or colors)" if len(col_keys) > 1 else "colors_precomp"
+        raise RuntimeError(f"{fn} expects exactly one color path: either {alt} OR dc+sh")
+    cov = inputs.get("cov3d_precomp")
+    has_cov = _size(cov) != 0
+    has_sr = _size(inputs.get("scales")) != 0 and _size(inputs.get(rot_key)) != 0
+    if has_cov == has_sr:
+        raise RuntimeError(f"{fn} expects exactly one geometry path: either cov3d_precomp OR "
+                           f"scales+{rot_key}")
+    return col, has_col, has_cov
+
+
+def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block_y, tan_fovx,
+                    tan_fovy, degree, scale_modifier, mult, default_vsp: bool):
+    """Shared body of preprocess_forward / rasterize_gaussians (binding.cpp:61-153, 424-492)."""
+    def req(k):
+        if k not in inputs:
+            raise RuntimeError(f"{fn} missing required input tensor: {k}")
+        return inputs[k]
+
+    for k in names["required"]:
+        req(k)
+    col, has_col, has_cov = _colour_and_geometry(inputs, fn, names["col_keys"], names["rot"])
+    _check_blocks(block_x, block_y)
+    dev = _device(inputs[names["means3d"]])
+    f = lambda x: _to(x, dev, torch.float32)  # noqa: E731
+    means3d = f(inputs[names["means3d"]])
+    P = means3d.shape[0]
+    opac = f(inputs["opacities"])
+    if opac.numel() != P:
+        raise ValueError(f"opacities has {opac.numel()} entries for {P} Gaussians")
+    sh_nd, sh_shape = _ndim_shape(inputs.get("sh"))
+    max_sh = int(sh_shape[1]) if sh_nd >= 2 else 0
+    sh_path = not has_col
+    _check_sh(degree, max_sh, sh_path)
+    vsp = inputs.get("viewspace_points")
+    if vsp is None or _size(vsp) == 0:
+        if not default_vsp:
+            raise RuntimeError(f"{fn} missing required input tensor: viewspace_points")
+        vsp = torch.zeros((P, 4), dtype=torch.float32, device=dev)
+    vsp = f(vsp)
+    gx, gy, _ = _tile_bounds(image_width, image_height, block_x, block_y)
+    cfg = dict(degree=int(degree), max_sh=max_sh, W=int(image_width), H=int(image_height), gx=gx,
+               gy=gy, use_cov=has_cov, use_col=has_col, scale_modifier=float(scale_modifier),
+               mult=float(mult), tan_fovx=float(tan_fovx), tan_fovy=float(tan_fovy))
+    dc = f(inputs["dc"]) if sh_path else None
+    sh = f(inputs["sh"]) if sh_path else None
+    if sh is not None and sh.numel() == 0:
+        sh = sh.reshape(P, 0, 3) if sh.dim() < 3 else sh
+    outs = _Preprocess.apply(
+        cfg, means3d, dc, sh, f(col) if has_col else None, opac,
+        None if has_cov else f(inputs["scales"]), None if has_cov else f(inputs[names["rot"]]),
+        f(inputs["cov3d_precomp"]) if has_cov else None, f(inputs[names["view"]]),
+        f(inputs[names["proj"]]), f(inputs[names["campos"]]), vsp)
+    return outs, cfg, dev
+
+
+_RG_NAMES = dict(required=("means3d", "background", "opacities", "metric_map", "viewmatrix",
+                           "projmatrix", "campos"),
+                 col_keys=("colors_precomp", "colors"), rot="rotations", means3d="means3d",
+                 view="viewmatrix", proj="projmatrix", campos="campos")
+_PF_NAMES = dict(required=("means3d", "opacities", "viewmat", "projmat", "cam_pos",
+                           "viewspace_points"),
+                 col_keys=("colors_precomp",), rot="quats", means3d="means3d", view="viewmat",
+                 proj="projmat", campos="cam_pos")
+
+
+def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_height: int,
+                                block_x: int = 16, block_y: int = 16, tan_fovx: float = 1.0,
+                                tan_fovy: float = 1.0, degree: int = 0,
+                                scale_modifier: float = 1.0, mult: float = 1.0,
+                                prefiltered: bool = False, get_flag: bool = False,
+                                *, write_sampled: Optional[bool] = None) -> Dict[str, Any]:
+    """Full forward (binding.cpp:33-282): preprocess -> scan -> binning/sort ->
+    tile ranges -> bucket offsets -> rasterize.  Two blocking 4-byte reads
+    (K and B), as in the reference."""
+    fn = "rasterize_gaussians_forward"
+    outs, cfg, dev = _run_preprocess(inputs, fn, _RG_NAMES, image_width, image_height, block_x,
+                                     block_y, tan_fovx, tan_fovy, degree, scale_modifier, mult,
+                                     default_vsp=True)
+    radii, xys, depths, cov3d, rgb, conic, tiles, clamped, vsp_out = outs
+    P = xys.shape[0]
+    gx, gy = cfg["gx"], cfg["gy"]
+    T = gx * gy
+    point_offsets = _inclusive_scan_i32(tiles)
+    K = _last_u32(point_offsets)
+    i32 = dict(dtype=torch.int32, device=dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    point_list_keys = torch.zeros(0, dtype=torch.int64, device=dev)
+    point_list = torch.zeros(0, **i32)
+    ranges = torch.zeros((0, 2), **i32)
+    bucket_count = torch.zeros(0, **i32)
+    bucket_offsets = torch.zeros(0, **i32)
+    bucket_to_tile = torch.zeros(0, **i32)
+    sampled_t = torch.zeros(0, **f32)
+    sampled_ar = torch.zeros(0, **f32)
+    final_t = torch.zeros(0, **f32)
+    n_contrib = torch.zeros(0, **i32)
+    max_contrib = torch.zeros(0, **i32)
+    pixel_colors = torch.zeros(0, **f32)
+    out_color = torch.zeros(0, **f32)
+    metric_count = torch.zeros(P if get_flag else 0, **i32)
+    B = 0
+    if K > 0:
+        with torch.no_grad():
+            point_list_keys, point_list, ranges, bucket_count, bucket_offsets = _binning_sorted(
+                xys.detach(), depths.detach(), conic.detach(), tiles, K, gx, gy, float(mult))
+        B = _last_u32(bucket_offsets)
+        if B > 0:
+            background = _to(inputs["background"], dev, torch.float32)
+            metric_map = _to(inputs["metric_map"], dev, torch.int32)
+            ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
+            rcfg = dict(W=cfg["W"], H=cfg["H"], C=3, T=T, B=B, get_flag=bool(get_flag),
+                        write_sampled=ws)
+            (bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib, max_contrib,
+             pixel_colors, out_color, metric_count) = _Rasterize.apply(
+                rcfg, ranges, point_list, bucket_offsets, xys, rgb, conic, background, radii,
+                metric_map, metric_count, vsp_out)
+    return {
+        "rendered": K, "num_buckets": B, "out_color": out_color, "radii": radii,
+        "point_offsets": point_offsets, "ranges": ranges, "bucket_count": bucket_count,
+        "bucket_offsets": bucket_offsets, "point_list_keys": point_list_keys,
+        "point_list": point_list, "metric_count": metric_count, "viewspace_points": vsp_out,
+        "geom_means2d": xys, "geom_depths": depths, "geom_cov3d": cov3d, "geom_rgb": rgb,
+        "geom_conic_opacity": conic, "geom_tiles_touched": tiles, "geom_clamped": clamped,
+        "sample_bucket_to_tile": bucket_to_tile, "sample_t": sampled_t, "sample_ar": sampled_ar,
+        "img_final_t": final_t, "img_n_contrib": n_contrib, "img_max_contrib": max_contrib,
+        "img_pixel_colors": pixel_colors,
+    }
+
+
+rasterize_gaussians = rasterize_gaussians_forward
+
+
+def preprocess_forward(inputs: Dict[str, Any], image_width: int, image_height: int,
+                       block_x: int = 16, block_y: int = 16, tan_fovx: float = 1.0,
+                       tan_fovy: float = 1.0, degree: int = 0, scale_modifier: float = 1.0,
+                       mult: float = 1.0, prefiltered: bool = False) -> Dict[str, Any]:
+    """Preprocess only (binding.cpp:397-508); differentiable."""
+    outs, _, _ = _run_preprocess(inputs, "preprocess_forward", _PF_NAMES, image_width,
+                                 image_height, block_x, block_y, tan_fovx, tan_fovy, degree,
+                                 scale_modifier, mult, default_vsp=False)
+    keys = ("radii", "xys", "depths", "cov3d", "rgb", "conic_opacity", "tiles_touched", "clamped",
+            "viewspace_points")
+    return dict(zip(keys, outs))
+
+
+def binning_forward(xys, depths, point_offsets, conic_opacity, tiles_touched, mult: float,
+                    tile_bounds_x: int, tile_bounds_y: int, tile_bounds_z: int,
+                    num_rendered: int) -> Dict[str, Any]:
+    """Gaussian-order duplication with keys (binding.cpp:345-375)."""
+    lib = _lib.load()
+    dev = _device(xys)
+    K = int(num_rendered)
+    if K == 0:
+        return {"point_list_keys_unsorted": torch.zeros(0, dtype=torch.int64, device=dev),
+                "point_list_unsorted": torch.zeros(0, dtype=torch.int32, device=dev)}
+    xys = _to(xys, dev, torch.float32).detach()
+    P = xys.shape[0]
+    depths = _to(depths, dev, torch.float32).detach().reshape(-1)
+    offs = _to(point_offsets, dev, torch.int32).reshape(-1)
+    conic = _to(conic_opacity, dev, torch.float32).detach()
+    tiles = _to(tiles_touched, dev, torch.int32).reshape(-1)
+    for name, t, n in (("depths", depths, P), ("point_offsets", offs, P),
+                       ("conic_opacity", conic, 4 * P), ("tiles_touched", tiles, P)):
+        if t.numel() != n:
+            raise ValueError(f"binning_forward: {name} has {t.numel()} elements, expected {n}")
+    keys = torch.empty(K, dtype=torch.int64, device=dev)
+    vals = torch.empty(K, dtype=torch.int32, device=dev)
+    _lib.check(lib.fgs_duplicate_with_keys(P, _p(xys), _p(depths), _p(offs), _p(conic), _p(tiles),
+                                           float(mult), int(tile_bounds_x), int(tile_bounds_y), K,
+                                           _p(keys), _p(vals), _stream(dev)))
+    return {"point_list_keys_unsorted": keys, "point_list_unsorted": vals}
+
+
+def tile_prep_forward(point_list_keys, num_rendered: int, num_tiles: int) -> Dict[str, Any]:
+    """Tile ranges + bucket counts (binding.cpp:377-395)."""
+    lib = _lib.load()
+    dev = _device(point_list_keys)
+    T = int(num_tiles)
+    if T == 0:
+        return {"ranges": torch.zeros((0, 2), dtype=torch.int32, device=dev),
+                "bucket_count": torch.zeros(0, dtype=torch.int32, device=dev)}
+    keys = _to(point_list_keys, dev, torch.int64).reshape(-1)
+    K = min(int(num_rendered), keys.numel())
+    ranges = torch.empty((T, 2), dtype=torch.int32, device=dev)
+    bc = torch.empty(T, dtype=torch.int32, device=dev)
+    _lib.check(lib.fgs_tile_ranges(_p(keys), K, T, _p(ranges), _p(bc), _stream(dev)))
+    return {"ranges": ranges, "bucket_count": bc}
+
+
+def rasterize_forward(ranges, point_list, per_tile_bucket_offset, means2d, colors, conic_opacity,
+                      background, radii, metric_map, metric_count, viewspace_points,
+                      image_width: int, image_height: int, block_x: int, block_y: int,
+                      num_channels: int, num_tiles: int, bucket_sum: int, get_flag: bool = False,
+                      *, write_sampled: Optional[bool] = None) -> Dict[str, Any]:
+    """Rasterize only (binding.cpp:286-343); differentiable w.r.t. means2d,
+    colors, conic_opacity and viewspace_points."""
+    _check_blocks(block_x, block_y)
+    dev = _device(means2d)
+    nd_m, sh_m = _ndim_shape(means2d)
+    nd_v, sh_v = _ndim_shape(viewspace_points)
+    if nd_m != 2 or sh_m[1] != 2:
+        raise ValueError("FastGSRasterize expects means2d with shape (N, 2).")
+    if nd_v != 2 or sh_v[1] != 4:
+        raise ValueError("FastGSRasterize expects viewspace_points with shape (N, 4).")
+    if sh_m[0] != sh_v[0]:
+        raise ValueError("FastGSRasterize expects means2d and viewspace_points to share the same N.")
+    f = lambda x: _to(x, dev, torch.float32)  # noqa: E731
+    i = lambda x: _to(x, dev, torch.int32)  # noqa: E731
+    T = int(num_tiles)
+    W, H = int(image_width), int(image_height)
+    gx, gy, _ = _tile_bounds(W, H, block_x, block_y)
+    ranges_t = i(ranges).reshape(-1, 2) if _size(ranges) else torch.zeros((0, 2), dtype=torch.int32,
+                                                                            device=dev)
+    if ranges_t.shape[0] < min(T, gx * gy):
+        raise ValueError(f"rasterize_forward: ranges has {ranges_t.shape[0]} tiles, "
+                         f"num_tiles is {T}")
+    mc = i(metric_count) if metric_count is not None else torch.zeros(0, dtype=torch.int32,
+                                                                        device=dev)
+    ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
+    cfg = dict(W=W, H=H, C=int(num_channels), T=T, B=int(bucket_sum), get_flag=bool(get_flag),
+               write_sampled=ws)
+    colors_t = f(colors)
+    outs = _Rasterize.apply(cfg, ranges_t, i(point_list).reshape(-1),
+                            i(per_tile_bucket_offset).reshape(-1), f(means2d), colors_t,
+                            f(conic_opacity), f(background).reshape(-1), i(radii).reshape(-1),
+                            i(metric_map).reshape(-1) if metric_map is not None else None, mc,
+                            f(viewspace_points))
+    keys = ("bucket_to_tile", "sampled_t", "sampled_ar", "final_t", "n_contrib", "max_contrib",
+            "pixel_colors", "out_color", "metric_count")
+    return dict(zip(keys, outs))

@@ -1,0 +1,269 @@
+/*
+ * fastgs_hip.h -- C ABI of libfastgs_hip.so, the MI355X (gfx950) FastGS
+ * rasterizer.  Plain C: POD parameter/IO structs of raw device pointers,
+ * element counts, and a hipStream_t passed as void*.  No torch types.
+ *
+ * Ownership: the caller allocates every output and workspace buffer (sizes
+ * from the *_workspace_bytes queries); the library never allocates, frees or
+ * retains device memory and never synchronises the stream.  Every output
+ * element the reference zero-fills is written by the library on the stream
+ * (kernels, never host memsets and never hipMemsetAsync).
+ *
+ * Errors: every entry point returns FGS_OK (0) or a negative code; the
+ * message of the last failure on the calling thread is fgs_last_error().
+ *
+ * Each entry point names the reference interface it replaces
+ * (a1091150/fastgs_core, file:line).
+ */
+#ifndef FASTGS_HIP_H
+#define FASTGS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FGS_OK 0
+#define FGS_ERR_INVALID_ARGUMENT -1
+#define FGS_ERR_LAUNCH -2
+#define FGS_ERR_UNSUPPORTED -3
+
+/* Thread-local message of the last error ("" if none). */
+const char* fgs_last_error(void);
+
+/* ABI version of this header (bumped on any struct/signature change). */
+int32_t fgs_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Preprocess.                                                               */
+/* Replaces PreprocessParams/PreprocessKernelParams                          */
+/* (fastgs_preprocess.h:13-55, fastgs_preprocess.cpp:21-38).                  */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  int32_t P;                  /* number of Gaussians */
+  int32_t degree;             /* SH degree (0..3; >3 treated as 3) */
+  int32_t max_sh_coeffs;      /* sh.shape[1]: rest coefficients per Gaussian */
+  int32_t image_width;
+  int32_t image_height;
+  int32_t grid_x;             /* ceil(W/16) */
+  int32_t grid_y;             /* ceil(H/16) */
+  int32_t use_cov3d_precomp;  /* geometry path: 1 = cov3d_precomp, 0 = scales+rotations */
+  int32_t use_colors_precomp; /* colour path: 1 = colors_precomp, 0 = dc+sh */
+  float scale_modifier;
+  float mult;
+  float tan_fovx;
+  float tan_fovy;
+} fgs_preprocess_params;
+
+typedef struct {
+  /* inputs (device, float32, contiguous); unused paths may be NULL */
+  const float* means3d;        /* [P,3] */
+  const float* dc;             /* [P,3]            (SH path) */
+  const float* sh;             /* [P,max_sh,3]     (SH path) */
+  const float* colors_precomp; /* [P,3]            (precomp colour path) */
+  const float* opacities;      /* [P] */
+  const float* scales;         /* [P,3] */
+  const float* rotations;      /* [P,4] (r,x,y,z) */
+  const float* cov3d_precomp;  /* [P,6] */
+  const float* viewmatrix;     /* [16] column-major */
+  const float* projmatrix;     /* [16] column-major */
+  const float* campos;         /* [3] */
+  const float* viewspace_in;   /* [P,4] */
+  /* outputs (every element written) */
+  int32_t* radii;              /* [P] */
+  float* xys;                  /* [P,2] */
+  float* depths;               /* [P] */
+  float* cov3d;                /* [P,6] */
+  float* rgb;                  /* [P,3] */
+  float* conic_opacity;        /* [P,4] */
+  uint32_t* tiles_touched;     /* [P] */
+  uint8_t* clamped;            /* [P,3] bool */
+  float* viewspace_out;        /* [P,4] */
+} fgs_preprocess_fwd_io;
+
+/* Replaces FastGSPreprocess::eval_gpu (fastgs_preprocess.cpp:81-169) /
+ * fastgs_preprocess_forward_kernel (fastgs_preprocess.metal:384-484). */
+int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p, const fgs_preprocess_fwd_io* io,
+                           void* stream);
+
+typedef struct {
+  /* primals */
+  const float* means3d;
+  const float* scales;
+  const float* rotations;
+  const float* viewmatrix;
+  const float* projmatrix;
+  const float* campos;
+  const float* sh;
+  const float* cov3d_precomp;
+  /* forward outputs */
+  const float* cov3d_fwd;      /* [P,6] */
+  const int32_t* radii;        /* [P] */
+  const uint8_t* clamped;      /* [P,3] */
+  /* cotangents of the preprocess outputs (NULL = zero) */
+  const float* dL_dxys;            /* [P,2] */
+  const float* dL_drgb;            /* [P,3] */
+  const float* dL_dconic_opacity;  /* [P,4] */
+  const float* dL_dcov3d;          /* [P,6] */
+  const float* dL_dviewspace_out;  /* [P,4] */
+  /* gradients (every element written; rows with radii <= 0 are zero) */
+  float* dL_dmeans3d;          /* [P,3] */
+  float* dL_ddc;               /* [P,3] */
+  float* dL_dsh;               /* [P,max_sh,3] */
+  float* dL_dcolors_precomp;   /* [P,3] */
+  float* dL_dopacities;        /* [P] */
+  float* dL_dscales;           /* [P,3] */
+  float* dL_drotations;        /* [P,4] */
+  float* dL_dviewspace_in;     /* [P,4] */
+} fgs_preprocess_bwd_io;
+
+/* Replaces FastGSPreprocess::vjp -> FastGSPreprocessBackward::eval_gpu
+ * (fastgs_preprocess.cpp:191-206, fastgs_preprocess_backward.cpp:89-185) /
+ * fastgs_preprocess_backward_kernel (fastgs_preprocess_backward.metal:60-430). */
+int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p, const fgs_preprocess_bwd_io* io,
+                           void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Scan / binning / sort / tile ranges.                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace for fgs_inclusive_scan_u32 over n elements. */
+size_t fgs_scan_workspace_bytes(int64_t n);
+
+/* out[i] = sum(in[0..i]) mod 2^32.  Replaces mx::cumsum(..., inclusive)
+ * (binding.cpp:153,211).  in and out may alias. */
+int32_t fgs_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
+                               void* stream);
+
+/* Gaussian-order duplication: for each Gaussian with tiles_touched > 0, the
+ * keys (tile_id << 32 | float_bits(depth)) and values (index) of its touched
+ * tiles at [point_offsets[i-1], ...).  keys/values are fully written (zero
+ * where nothing is emitted).  Replaces FastGSBinning::eval_gpu
+ * (fastgs_binning.cpp:59-106) / fastgs_duplicate_with_keys_kernel
+ * (fastgs_binning.metal:182-213). */
+int32_t fgs_duplicate_with_keys(int32_t P, const float* xys, const float* depths,
+                                const uint32_t* point_offsets, const float* conic_opacity,
+                                const uint32_t* tiles_touched, float mult, int32_t grid_x,
+                                int32_t grid_y, int64_t num_rendered, uint64_t* keys_unsorted,
+                                uint32_t* values_unsorted, void* stream);
+
+/* Workspace for fgs_sort_pairs_u64 over n pairs. */
+size_t fgs_sort_workspace_bytes(int64_t n);
+
+/* Stable ascending LSD radix sort of (key, value) pairs on key bits
+ * [begin_bit, end_bit).  Output in keys_out/values_out.  Replaces
+ * mx::argsort + 2x mx::take (binding.cpp:195-197); ties keep input order. */
+int32_t fgs_sort_pairs_u64(const uint64_t* keys_in, const uint32_t* values_in, uint64_t* keys_out,
+                           uint32_t* values_out, int64_t n, int32_t begin_bit, int32_t end_bit,
+                           void* workspace, void* stream);
+
+/* ranges[T][2] and bucket_count[T] from (sorted) 64-bit keys with the exact
+ * semantics of fastgs_identify_tile_ranges_kernel and
+ * fastgs_per_tile_bucket_count_kernel (fastgs_tile_prep.metal:10-53); keys
+ * with tile 0xFFFFFFFF or tile >= T are ignored.  Replaces
+ * FastGSTilePrep::eval_gpu (fastgs_tile_prep.cpp:48-99). */
+int32_t fgs_tile_ranges(const uint64_t* keys, int64_t num_rendered, int32_t num_tiles,
+                        uint32_t* ranges, uint32_t* bucket_count, void* stream);
+
+/* Fused binning of the rasterize_gaussians path (binding.cpp:175-212):
+ * duplicate -> stable sort on (tile, depth) -> tile ranges -> bucket counts
+ * -> bucket offsets.  Produces exactly the arrays of the reference path. */
+typedef struct {
+  int32_t P;
+  int32_t grid_x;
+  int32_t grid_y;
+  int64_t num_rendered; /* K = point_offsets[P-1] */
+  float mult;
+  /* inputs */
+  const float* xys;
+  const float* depths;
+  const float* conic_opacity;
+  const uint32_t* tiles_touched;
+  /* outputs */
+  uint64_t* point_list_keys;  /* [K] sorted */
+  uint32_t* point_list;       /* [K] sorted */
+  uint32_t* ranges;           /* [T,2] */
+  uint32_t* bucket_count;     /* [T] */
+  uint32_t* bucket_offsets;   /* [T] inclusive */
+  void* workspace;            /* fgs_binning_workspace_bytes(P, K, T) */
+} fgs_binning_io;
+
+size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, int32_t num_tiles);
+int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Rasterize.                                                                */
+/* Replaces RasterizeParams/RasterizeKernelParams (fastgs_rasterize.h:14-51, */
+/* fastgs_rasterize.cpp:20-29).                                              */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  int32_t image_width;
+  int32_t image_height;
+  int32_t num_channels;   /* colour row stride; min(num_channels,3) blended */
+  int32_t num_tiles;
+  int64_t bucket_sum;     /* B */
+  int32_t get_flag;
+  int32_t write_sampled;  /* 1: also write sampled_t / sampled_ar */
+  int32_t num_points;     /* P: Gaussians; list entries >= P are treated as empty */
+  int64_t list_len;       /* K: length of point_list; ranges are clamped to it */
+} fgs_raster_params;
+
+typedef struct {
+  const uint32_t* ranges;          /* [T,2] */
+  const uint32_t* point_list;      /* [K] */
+  const uint32_t* bucket_offsets;  /* [T] inclusive */
+  const float* means2d;            /* [P,2] */
+  const float* colors;             /* [P,num_channels] */
+  const float* conic_opacity;      /* [P,4] */
+  const float* background;         /* [num_channels] */
+  const int32_t* metric_map;       /* [H*W] (read when get_flag) */
+  uint32_t* bucket_to_tile;        /* [B] */
+  float* sampled_t;                /* [B*256]      (when write_sampled) */
+  float* sampled_ar;               /* [B][C][256]  (when write_sampled) */
+  float* final_t;                  /* [H*W] */
+  uint32_t* n_contrib;             /* [H*W] */
+  uint32_t* max_contrib;           /* [T] */
+  float* pixel_colors;             /* [C,H*W] */
+  float* out_color;                /* [C,H*W] */
+  int32_t* metric_count;           /* [P] (zeroed and accumulated when get_flag) */
+} fgs_raster_fwd_io;
+
+/* Replaces FastGSRasterize::eval_gpu (fastgs_rasterize.cpp:91-169) /
+ * fastgs_render_forward_kernel (fastgs_rasterize.metal:25-159). */
+int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raster_fwd_io* io, void* stream);
+
+typedef struct {
+  const uint32_t* ranges;
+  const uint32_t* point_list;
+  const float* means2d;
+  const float* colors;
+  const float* conic_opacity;
+  const float* background;
+  const float* final_t;         /* [H*W] from the forward */
+  const uint32_t* n_contrib;    /* [H*W] from the forward */
+  const uint32_t* max_contrib;  /* [T] from the forward */
+  const float* dL_dout_color;   /* [C,H*W] */
+  float* dL_dmeans2d;           /* [P,2] */
+  float* dL_dcolors;            /* [P,num_channels] */
+  float* dL_dconic_opacity;     /* [P,4] */
+  float* dL_dviewspace;         /* [P,4] */
+} fgs_raster_bwd_io;
+
+/* Gradients of the blend w.r.t. means2d (scaled by (W/2,H/2)), colours,
+ * conic/opacity and the viewspace dummy (x, y, |x|, |y|).  Every output
+ * element is written.  Replaces FastGSRasterize::vjp ->
+ * FastGSRasterizeBackward::eval_gpu (fastgs_rasterize.cpp:191-206,
+ * fastgs_rasterize_backward.cpp:85-168) / fastgs_render_backward_kernel
+ * (fastgs_rasterize_backward.metal:24-278). */
+int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raster_bwd_io* io, void* stream);
+
+/* Fill a u32 buffer with a value on the stream (a kernel, graph-safe). */
+int32_t fgs_fill_u32(uint32_t* dst, uint32_t value, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTGS_HIP_H */
