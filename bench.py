@@ -1,0 +1,341 @@
+#!/usr/bin/env python3
+"""North-star benchmark of the MI355X FastGS rasterizer.
+
+Workload ("cfg3"): 1,000,000 Gaussians (means
+N(0,1)^3 clipped to [-2,2], log-scales N(-4.5,0.7), opacity logits N(0,1.5),
+DC U(0,1), higher-order SH N(0,0.05), SH degree 3), 1920x1080, 20 seeded
+poses on a radius-4 sphere looking at the origin, 60 degree horizontal FoV.
+A step is one training iteration without the optimizer: parameter
+activations (sigmoid / exp / quaternion normalise) -> rasterize_gaussians
+forward -> L1 + 0.2*(1 - SSIM) against a seeded U(0,1) target (11x11
+Gaussian window, sigma 1.5) -> backward to every Gaussian parameter and the
+viewspace_points means2d route.  Inputs are resident in HBM before timing.
+
+Prints ONE JSON line (the driver contract) with the headline fwd+bwd
+iters/s, forward Mpix/s, per-stage milliseconds and roofline fractions, the
+roofline object of the dominant kernel and the CPU baseline (the C oracle,
+a restatement of the reference Metal kernels, on the host cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd iters/s @1M Gaussians 1080p; fwd Mpix/s; achieved HBM GB/s"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP32_PEAK_TFLOPS = 157.3       # MI355X FP32 vector (no stage is a dense contraction)
+
+CONFIGS = {
+    "cfg3": dict(P=1_000_000, W=1920, H=1080, degree=3, poses=20, scene="cfg2",
+                 desc="cfg3: 1M Gaussians, 1920x1080, SH3, fwd+bwd L1+0.2(1-SSIM), 20 poses"),
+    "cfg2": dict(P=200_000, W=1280, H=720, degree=3, poses=8, scene="cfg2",
+                 desc="cfg2: 200k Gaussians, 1280x720, SH3, 8 poses"),
+    "cfg4": dict(P=3_000_000, W=1920, H=1080, degree=3, poses=4, scene="cfg4",
+                 desc="cfg4: 3M heavy-overlap Gaussians, 1920x1080, SH3, fwd+bwd"),
+    "cfg1": dict(P=16384, W=256, H=256, degree=0, poses=1, scene="cfg1",
+                 desc="cfg1: 16384 Gaussians, 256x256, SH0, fwd+bwd L1"),
+}
+
+
+# ---------------------------------------------------------------------------
+def make_scene(cfg, seed=0):
+    from fastgs_core_amd import synthetic as syn
+
+    if cfg["scene"] == "cfg1":
+        sc = syn.scene_config1(seed, cfg["P"])
+        cams = [syn.config1_camera(cfg["W"], cfg["H"])]
+    elif cfg["scene"] == "cfg4":
+        sc = syn.scene_config4(seed, cfg["P"], cfg["degree"])
+        cams = syn.sphere_cameras(cfg["poses"], seed + 1, cfg["W"], cfg["H"])
+    else:
+        sc = syn.scene_config2(seed, cfg["P"], cfg["degree"])
+        cams = syn.sphere_cameras(cfg["poses"], seed + 1, cfg["W"], cfg["H"])
+    return sc, cams
+
+
+def raw_params(sc):
+    """Pre-activation parameters (what an optimizer would own)."""
+    opac = np.clip(sc["opacities"].astype(np.float64), 1e-6, 1 - 1e-6)
+    return {
+        "means3d": sc["means3d"],
+        "log_scales": np.log(sc["scales"]).astype(np.float32),
+        "quats": sc["rotations"],
+        "opacity_logits": np.log(opac / (1 - opac)).astype(np.float32),
+        "dc": sc["dc"],
+        "sh": sc["sh"],
+    }
+
+
+def gaussian_window(torch, size=11, sigma=1.5):
+    x = torch.arange(size, dtype=torch.float32) - size // 2
+    g = torch.exp(-(x * x) / (2 * sigma * sigma))
+    return g / g.sum()
+
+
+def ssim(torch, F, img, tgt, win):
+    """Mean SSIM of [3,H,W] images, 11x11 Gaussian window (separable), C1=0.01^2, C2=0.03^2."""
+    C1, C2 = 0.01 ** 2, 0.03 ** 2
+    kx = win.view(1, 1, 1, -1).expand(3, 1, 1, win.numel()).contiguous()
+    ky = win.view(1, 1, -1, 1).expand(3, 1, win.numel(), 1).contiguous()
+    pad = win.numel() // 2
+
+    def blur(z):
+        z = F.conv2d(z, kx, padding=(0, pad), groups=3)
+        return F.conv2d(z, ky, padding=(pad, 0), groups=3)
+
+    x = img.unsqueeze(0)
+    y = tgt.unsqueeze(0)
+    mu_x, mu_y = blur(x), blur(y)
+    sxx = blur(x * x) - mu_x * mu_x
+    syy = blur(y * y) - mu_y * mu_y
+    sxy = blur(x * y) - mu_x * mu_y
+    num = (2 * mu_x * mu_y + C1) * (2 * sxy + C2)
+    den = (mu_x * mu_x + mu_y * mu_y + C1) * (sxx + syy + C2)
+    return (num / den).mean()
+
+
+class StageTimer:
+    """Event pairs recorded on the launch stream around each C-ABI stage."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.open = {}
+        self.done = []
+
+    def begin(self, name):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.open[name] = e
+
+    def end(self, name):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.done.append((name, self.open.pop(name), e))
+
+    def collect(self):
+        self.torch.cuda.synchronize()
+        out = {}
+        for name, a, b in self.done:
+            out.setdefault(name, []).append(a.elapsed_time(b))
+        self.done = []
+        return out
+
+
+# ---------------------------------------------------------------------------
+def algorithmic_work(stage, K, P, Pv, T, HW, S, B, N_f, N_b):
+    """Algorithmic HBM bytes and FP32 flops per stage."""
+    b = f = 0.0
+    if stage == "preprocess_fwd":
+        b = 103 * P + 32 * P + (16 + S) * Pv
+    elif stage == "scan":
+        b = 8 * P
+    elif stage == "binning":
+        bits = 32 + math.ceil(math.log2(max(T, 2)))
+        b = (8 * P + 28 * Pv + 12 * K) + K * (8 + 24 * math.ceil(bits / 8)) + 8 * K + 12 * T
+    elif stage == "rasterize_fwd":
+        b = 40 * K + 32 * HW
+        f = 26 * N_f
+    elif stage == "rasterize_bwd":
+        b = 32 * HW + 92 * K
+        f = 90 * N_b
+    elif stage == "preprocess_bwd":
+        b = (88 + S) * P + (119 + S) * Pv
+    return b, f
+
+
+def roofline_entry(stage, ms, b, f):
+    t = ms * 1e-3
+    t_hbm = b / (HBM_PEAK_GBS * 1e9)
+    t_flop = f / (FP32_PEAK_TFLOPS * 1e12)
+    if t_flop > t_hbm:
+        ach = f / t / 1e12
+        return {"bound": "valu", "achieved": ach, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": ach / FP32_PEAK_TFLOPS, "ms": ms, "bytes": b, "flops": f}
+    ach = b / t / 1e9
+    return {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": ach / HBM_PEAK_GBS, "ms": ms, "bytes": b, "flops": f}
+
+
+def cpu_baseline(cfg, sc, cams, seed=0):
+    """The C oracle (float build, OpenMP over host cores) on one pose of the same workload:
+    full forward + L1/SSIM loss gradient (torch CPU) + backward."""
+    import torch
+    import torch.nn.functional as F
+
+    from fastgs_core_amd import synthetic as syn
+    from oracle.oracle import Oracle
+
+    orc = Oracle()
+    cores = int(orc.lib.orc_num_threads())
+    cam = cams[0]
+    W, H = cfg["W"], cfg["H"]
+    inp = syn.make_inputs(sc, cam)
+    rng = np.random.default_rng(seed + 7)
+    target = torch.from_numpy(rng.uniform(0, 1, (3, H, W)).astype(np.float32))
+    win = gaussian_window(torch)
+    t0 = time.perf_counter()
+    fwd = orc.render(inp, W, H, cam.tan_fovx, cam.tan_fovy, cfg["degree"])
+    img = torch.from_numpy(fwd["out_color"].reshape(3, H, W).copy()).requires_grad_(True)
+    loss = (img - target).abs().mean() + 0.2 * (1 - ssim(torch, F, img, target, win))
+    loss.backward()
+    orc.render_backward(inp, fwd, img.grad.numpy().reshape(3, -1), W, H, cam.tan_fovx,
+                        cam.tan_fovy, cfg["degree"])
+    dt = time.perf_counter() - t0
+    return {"value": 1.0 / dt, "unit": "iters/s", "cores": cores, "kind": "port",
+            "sample": f"1 full training step (pose 0) of {cfg['desc']}; C oracle, "
+                      f"{cores} OpenMP threads; {dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-stage-profile", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "fastgs_core_amd runs on one GPU; multi-GPU is out of scope "
+                                   "for this build (see DESIGN.md: how the path would shard)",
+                          "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+
+    import torch
+    import torch.nn.functional as F
+
+    import fastgs_core
+    from fastgs_core_amd import rasterizer
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda", 0)
+    cfg = CONFIGS[args.config]
+    W, H, deg = cfg["W"], cfg["H"], cfg["degree"]
+    sc, cams = make_scene(cfg)
+    P = sc["means3d"].shape[0]
+    raw = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev).requires_grad_(True)
+           for k, v in raw_params(sc).items()}
+    rng = np.random.default_rng(7)
+    targets = [torch.from_numpy(rng.uniform(0, 1, (3, H, W)).astype(np.float32)).to(dev)
+               for _ in range(len(cams))]
+    cam_t = []
+    for c in cams:
+        cam_t.append({
+            "viewmatrix": torch.from_numpy(c.viewmatrix.reshape(-1).copy()).to(dev),
+            "projmatrix": torch.from_numpy(c.projmatrix.reshape(-1).copy()).to(dev),
+            "campos": torch.from_numpy(c.campos.copy()).to(dev),
+            "tan_fovx": c.tan_fovx, "tan_fovy": c.tan_fovy,
+        })
+    background = torch.zeros(3, device=dev)
+    metric_map = torch.zeros(W * H, dtype=torch.int32, device=dev)
+    win = gaussian_window(torch).to(dev)
+
+    def render(i, train=True):
+        c = cam_t[i % len(cam_t)]
+        vsp = torch.zeros((P, 4), device=dev, requires_grad=train)
+        opac = torch.sigmoid(raw["opacity_logits"])
+        scales = torch.exp(raw["log_scales"])
+        q = raw["quats"]
+        rots = q / (q.norm(dim=1, keepdim=True) + 1e-8)
+        inputs = {"means3d": raw["means3d"], "scales": scales, "rotations": rots,
+                  "opacities": opac, "dc": raw["dc"], "sh": raw["sh"], "background": background,
+                  "metric_map": metric_map, "viewmatrix": c["viewmatrix"],
+                  "projmatrix": c["projmatrix"], "campos": c["campos"], "viewspace_points": vsp}
+        out = fastgs_core.rasterize_gaussians(inputs, W, H, 16, 16, c["tan_fovx"], c["tan_fovy"],
+                                              deg)
+        return out, vsp
+
+    def step(i):
+        for p in raw.values():
+            p.grad = None
+        out, vsp = render(i)
+        img = out["out_color"].view(3, H, W)
+        tgt = targets[i % len(targets)]
+        loss = (img - tgt).abs().mean() + 0.2 * (1 - ssim(torch, F, img, tgt, win))
+        loss.backward()
+        return out
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_step = dt * 1e3 / max(args.steps, 1)
+    iters = args.steps / dt if dt > 0 else 0.0
+
+    # forward-only throughput (preprocess through rasterize, host syncs included)
+    with torch.no_grad():
+        for i in range(2):
+            render(i, train=False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        nf = len(cam_t)
+        for i in range(nf):
+            render(i, train=False)
+        torch.cuda.synchronize()
+        fwd_ms = (time.perf_counter() - t0) * 1e3 / nf
+    fwd_mpix = W * H / (fwd_ms * 1e-3) / 1e6
+
+    result = {
+        "metric": METRIC, "value": iters, "unit": "iters/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg["desc"], "gaussians": P, "width": W, "height": H,
+                   "sh_degree": deg, "poses": len(cams)},
+        "fwd_mpix_s": fwd_mpix, "fwd_ms": fwd_ms,
+    }
+
+    if not args.no_stage_profile:
+        timer = StageTimer(torch)
+        rasterizer.set_stage_timer(timer)
+        stats = []
+        for i in range(len(cam_t)):
+            out = step(i)
+            nc = out["img_n_contrib"]
+            stats.append((out["rendered"], out["num_buckets"], int((out["radii"] > 0).sum()),
+                          int(nc.to(torch.int64).sum()) if nc.numel() else 0))
+        times = timer.collect()
+        rasterizer.set_stage_timer(None)
+        K = float(np.median([s[0] for s in stats]))
+        B = float(np.median([s[1] for s in stats]))
+        Pv = float(np.median([s[2] for s in stats]))
+        Nb = float(np.median([s[3] for s in stats]))
+        T = ((W + 15) // 16) * ((H + 15) // 16)
+        S = 12 * ((deg + 1) ** 2 - 1)
+        stages = {}
+        for name, v in times.items():
+            ms = float(np.median(v))
+            b, f = algorithmic_work(name, K, P, Pv, T, W * H, S, B, Nb, Nb)
+            stages[name] = roofline_entry(name, ms, b, f)
+        dom = max(stages, key=lambda k: stages[k]["ms"])
+        d = stages[dom]
+        result["stages"] = stages
+        result["counts"] = {"K": K, "B": B, "P_visible": Pv, "N_contrib": Nb, "tiles": T}
+        result["roofline"] = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
+                              "peak": d["peak"], "unit": d["unit"], "frac": d["frac"],
+                              "traffic": None}
+    if not args.no_cpu_baseline:
+        try:
+            result["cpu_baseline"] = cpu_baseline(cfg, sc, cams)
+        except Exception as e:  # the baseline must never hide the GPU result
+            result["cpu_baseline"] = {"error": repr(e)}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

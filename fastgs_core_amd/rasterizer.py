@@ -38,6 +38,32 @@ TILE = 16
 # unless requested (zero-size tensors are returned otherwise).
 WRITE_SAMPLED_STATE = False
 
+# Optional stage timer (used by bench.py): an object with begin(name) and
+# end(name) methods, called around every C-ABI stage on the launch stream.
+_STAGE_TIMER = None
+
+
+def set_stage_timer(timer) -> None:
+    """Install (or clear, with None) a timer called around each hot-path stage."""
+    global _STAGE_TIMER
+    _STAGE_TIMER = timer
+
+
+class _stage:
+    __slots__ = ("name",)
+
+    def __init__(self, name: str):
+        self.name = name
+
+    def __enter__(self):
+        if _STAGE_TIMER is not None:
+            _STAGE_TIMER.begin(self.name)
+
+    def __exit__(self, *exc):
+        if _STAGE_TIMER is not None:
+            _STAGE_TIMER.end(self.name)
+        return False
+
 
 # ---------------------------------------------------------------------------
 # helpers
@@ -154,7 +180,9 @@ class _Preprocess(torch.autograd.Function):
             _p(viewspace_in), _p(radii), _p(xys), _p(depths), _p(cov3d), _p(rgb), _p(conic),
             _p(tiles), _p(clamped), _p(vsp_out))
         if P > 0:
-            _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+            with _stage("preprocess_fwd"):
+                _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io),
+                                                  _stream(dev)))
         ctx.cfg = cfg
         ctx.opacity_shape = opacities.shape
         ctx.sh_shape = None if sh is None else sh.shape
@@ -194,7 +222,9 @@ class _Preprocess(torch.autograd.Function):
             _p(g_conic), _p(g_cov3d), _p(g_vsp), _p(d_means3d), _p(d_dc), _p(d_sh), _p(d_col),
             _p(d_opac), _p(d_scales), _p(d_rot), _p(d_vsp))
         if P > 0:
-            _lib.check(lib.fgs_preprocess_bwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+            with _stage("preprocess_bwd"):
+                _lib.check(lib.fgs_preprocess_bwd(ctypes.byref(prm), ctypes.byref(io),
+                                                  _stream(dev)))
         need = ctx.needs_input_grad
         d_cov_pre = torch.zeros_like(cov3d_precomp) if (cov3d_precomp is not None and need[8]) \
             else None
@@ -238,7 +268,8 @@ class _Rasterize(torch.autograd.Function):
             _p(conic_opacity), _p(background), _p(metric_map), _p(bucket_to_tile),
             _p(sampled_t), _p(sampled_ar), _p(final_t), _p(n_contrib), _p(max_contrib),
             _p(pixel_colors), _p(out_color), _p(mc))
-        _lib.check(lib.fgs_rasterize_fwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+        with _stage("rasterize_fwd"):
+            _lib.check(lib.fgs_rasterize_fwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
         ctx.cfg = cfg
         ctx.save_for_backward(ranges, point_list, means2d, colors, conic_opacity, background,
                               final_t, n_contrib, max_contrib)
@@ -269,7 +300,8 @@ class _Rasterize(torch.autograd.Function):
             _p(ranges), _p(point_list), _p(means2d), _p(colors), _p(conic_opacity),
             _p(background), _p(final_t), _p(n_contrib), _p(max_contrib), _p(g_out),
             _p(d_means2d), _p(d_colors), _p(d_conic), _p(d_vsp))
-        _lib.check(lib.fgs_rasterize_bwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
+        with _stage("rasterize_bwd"):
+            _lib.check(lib.fgs_rasterize_bwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
         need = ctx.needs_input_grad
         d_bg = torch.zeros_like(background) if need[7] else None
         return (None, None, None, None, d_means2d, d_colors.view(colors.shape), d_conic, d_bg,
@@ -286,7 +318,8 @@ def _inclusive_scan_i32(x: torch.Tensor) -> torch.Tensor:
     if n == 0:
         return out
     ws = torch.empty(int(lib.fgs_scan_workspace_bytes(n)), dtype=torch.uint8, device=x.device)
-    _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(out), n, _p(ws), _stream(x.device)))
+    with _stage("scan"):
+        _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(out), n, _p(ws), _stream(x.device)))
     return out
 
 
@@ -303,7 +336,8 @@ def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: f
     ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
     io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
                         _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws))
-    _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
+    with _stage("binning"):
+        _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
     return keys, plist, ranges, bucket_count, bucket_offsets
 
 

@@ -25,6 +25,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 #ifdef ORC_DOUBLE
 typedef double real;
@@ -1032,3 +1035,12 @@ void orc_preprocess_bwd(const orc_params* prm, const real* means3d, const real* 
 }
 
 int orc_sizeof_real(void) { return (int)sizeof(real); }
+
+/* Threads the OpenMP loops use (1 without OpenMP). */
+int orc_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
