@@ -22,22 +22,24 @@ constexpr int kWave = 64;
 // Deterministic transcendental functions.
 // ---------------------------------------------------------------------------
 
-// exp(x) = 2^t with t = x*log2(e) split as t = n + f, n = floor(t), f in
-// [0,1); 2^f = 1 + f*q(f) with q a degree-5 polynomial fitted at 200
-// Chebyshev nodes on [0,1] (max relative error 5.8e-8), Horner with fused
-// multiply-adds; scaled by ldexp.  t is clamped at -126 (normal range).
+// exp(x): Cody-Waite reduction n = floor(x*log2(e)), r = x - n*ln2 (ln2 as a
+// float head and tail, fused multiply-adds); e^r = 1 + r*q(r), q a degree-5
+// polynomial fitted at 400 Chebyshev nodes on [-0.02, 0.72], Horner with fused
+// multiply-adds; scaled by ldexp.  x clamped at -87 (normal range).  Max
+// relative error 9.6e-8 on [-87, 0].
 __device__ __forceinline__ float det_expf(float x) {
-  float t = x * 1.44269502973556519f;
-  t = fmaxf(t, -126.0f);
+  x = fmaxf(x, -87.0f);
+  const float t = x * 1.44269504088896341f;
   const float n = floorf(t);
-  const float f = t - n;
-  float q = 0.0002082919527310878f;
-  q = __builtin_fmaf(q, f, 0.0012689351569861174f);
-  q = __builtin_fmaf(q, f, 0.009652440436184406f);
-  q = __builtin_fmaf(q, f, 0.055495936423540115f);
-  q = __builtin_fmaf(q, f, 0.24022722244262695f);
-  q = __builtin_fmaf(q, f, 0.6931471824645996f);
-  const float p = __builtin_fmaf(f, q, 1.0f);
+  float r = __builtin_fmaf(-n, 0.6931471824645996f, x);
+  r = __builtin_fmaf(-n, -1.9046542121259336e-09f, r);
+  float q = 0.0018846612656489015f;
+  q = __builtin_fmaf(q, r, 0.00792612787336111f);
+  q = __builtin_fmaf(q, r, 0.041812896728515625f);
+  q = __builtin_fmaf(q, r, 0.16664455831050873f);
+  q = __builtin_fmaf(q, r, 0.5000009536743164f);
+  q = __builtin_fmaf(q, r, 1.0f);
+  const float p = __builtin_fmaf(r, q, 1.0f);
   return __builtin_ldexpf(p, (int)n);
 }
 

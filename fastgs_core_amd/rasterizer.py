@@ -393,6 +393,10 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
         req(k)
     col, has_col, has_cov = _colour_and_geometry(inputs, fn, names["col_keys"], names["rot"])
     _check_blocks(block_x, block_y)
+    sh_nd, sh_shape = _ndim_shape(inputs.get("sh"))
+    max_sh = int(sh_shape[1]) if sh_nd >= 2 else 0
+    sh_path = not has_col
+    _check_sh(degree, max_sh, sh_path)
     dev = _device(inputs[names["means3d"]])
     f = lambda x: _to(x, dev, torch.float32)  # noqa: E731
     means3d = f(inputs[names["means3d"]])
@@ -400,10 +404,6 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     opac = f(inputs["opacities"])
     if opac.numel() != P:
         raise ValueError(f"opacities has {opac.numel()} entries for {P} Gaussians")
-    sh_nd, sh_shape = _ndim_shape(inputs.get("sh"))
-    max_sh = int(sh_shape[1]) if sh_nd >= 2 else 0
-    sh_path = not has_col
-    _check_sh(degree, max_sh, sh_path)
     vsp = inputs.get("viewspace_points")
     if vsp is None or _size(vsp) == 0:
         if not default_vsp:
@@ -568,7 +568,6 @@ def rasterize_forward(ranges, point_list, per_tile_bucket_offset, means2d, color
     """Rasterize only (binding.cpp:286-343); differentiable w.r.t. means2d,
     colors, conic_opacity and viewspace_points."""
     _check_blocks(block_x, block_y)
-    dev = _device(means2d)
     nd_m, sh_m = _ndim_shape(means2d)
     nd_v, sh_v = _ndim_shape(viewspace_points)
     if nd_m != 2 or sh_m[1] != 2:
@@ -577,6 +576,7 @@ def rasterize_forward(ranges, point_list, per_tile_bucket_offset, means2d, color
         raise ValueError("FastGSRasterize expects viewspace_points with shape (N, 4).")
     if sh_m[0] != sh_v[0]:
         raise ValueError("FastGSRasterize expects means2d and viewspace_points to share the same N.")
+    dev = _device(means2d)
     f = lambda x: _to(x, dev, torch.float32)  # noqa: E731
     i = lambda x: _to(x, dev, torch.int32)  # noqa: E731
     T = int(num_tiles)

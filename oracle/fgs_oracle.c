@@ -57,23 +57,25 @@ typedef float real;
 /* Deterministic transcendental functions (float build).                     */
 /* ------------------------------------------------------------------------ */
 
-/* exp(x) = 2^t, t = x*log2(e), reduced as t = n + f with n = floor(t), f in
- * [0,1).  2^f = 1 + f*q(f), q a degree-5 polynomial fitted at 200 Chebyshev
- * nodes on [0,1] (max relative error 5.8e-8 before rounding), evaluated by
- * Horner with correctly-rounded fused multiply-adds; the result is scaled by
- * ldexp (exact).  t is clamped below at -126 so the result stays normal. */
+/* exp(x) by Cody-Waite reduction: n = floor(x*log2(e)), r = x - n*ln2 with
+ * ln2 split in a float head and tail applied by fused multiply-adds, so r is
+ * in [0, ln2) up to rounding; e^r = 1 + r*q(r) with q a degree-5 polynomial
+ * fitted at 400 Chebyshev nodes on [-0.02, 0.72], Horner with correctly
+ * rounded fused multiply-adds; scaled by ldexp (exact).  x is clamped at -87
+ * so the result stays normal.  Max relative error 9.6e-8 on [-87, 0]. */
 float orc_expf(float x) {
-  float t = x * 1.44269502973556519f;
-  t = fmaxf(t, -126.0f);
-  float n = floorf(t);
-  float f = t - n;
-  float q = 0.0002082919527310878f;
-  q = fmaf(q, f, 0.0012689351569861174f);
-  q = fmaf(q, f, 0.009652440436184406f);
-  q = fmaf(q, f, 0.055495936423540115f);
-  q = fmaf(q, f, 0.24022722244262695f);
-  q = fmaf(q, f, 0.6931471824645996f);
-  float p = fmaf(f, q, 1.0f);
+  x = fmaxf(x, -87.0f);
+  const float t = x * 1.44269504088896341f;
+  const float n = floorf(t);
+  float r = fmaf(-n, 0.6931471824645996f, x);
+  r = fmaf(-n, -1.9046542121259336e-09f, r);
+  float q = 0.0018846612656489015f;
+  q = fmaf(q, r, 0.00792612787336111f);
+  q = fmaf(q, r, 0.041812896728515625f);
+  q = fmaf(q, r, 0.16664455831050873f);
+  q = fmaf(q, r, 0.5000009536743164f);
+  q = fmaf(q, r, 1.0f);
+  const float p = fmaf(r, q, 1.0f);
   return ldexpf(p, (int)n);
 }
 
@@ -370,6 +372,41 @@ uint32_t orc_tiles_touched_one(real px, real py, const real* co, int gx, int gy,
   return tiles_walk(px, py, co, gx, gy, mult, NULL, NULL);
 }
 
+/* compute_color_from_sh (fastgs_preprocess.metal:117-169): real SH basis up
+ * to degree 3 evaluated at dir = (mean - campos) / |mean - campos|, plus 0.5,
+ * clamped at 0 with the clamp mask.  s points at the Gaussian's rest
+ * coefficients s[k*3 + c], k = 0..14. */
+void orc_color_from_sh(int degree, const real* mean, const real* campos, const real* d,
+                       const real* s, real* col, uint8_t* clamped) {
+  real v[3] = {mean[0] - campos[0], mean[1] - campos[1], mean[2] - campos[2]};
+  real len = RSQRT(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  real x = v[0] / len, y = v[1] / len, z = v[2] / len;
+  for (int c = 0; c < 3; ++c) {
+    real res = SH_C0 * d[c];
+    if (degree > 0) {
+      res = res - SH_C1 * y * s[0 * 3 + c] + SH_C1 * z * s[1 * 3 + c] - SH_C1 * x * s[2 * 3 + c];
+      if (degree > 1) {
+        real xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+        res += SH_C2[0] * xy * s[3 * 3 + c] + SH_C2[1] * yz * s[4 * 3 + c] +
+               SH_C2[2] * ((real)2 * zz - xx - yy) * s[5 * 3 + c] +
+               SH_C2[3] * xz * s[6 * 3 + c] + SH_C2[4] * (xx - yy) * s[7 * 3 + c];
+        if (degree > 2) {
+          res += SH_C3[0] * y * ((real)3 * xx - yy) * s[8 * 3 + c] +
+                 SH_C3[1] * xy * z * s[9 * 3 + c] +
+                 SH_C3[2] * y * ((real)4 * zz - xx - yy) * s[10 * 3 + c] +
+                 SH_C3[3] * z * ((real)2 * zz - (real)3 * xx - (real)3 * yy) * s[11 * 3 + c] +
+                 SH_C3[4] * x * ((real)4 * zz - xx - yy) * s[12 * 3 + c] +
+                 SH_C3[5] * z * (xx - yy) * s[13 * 3 + c] +
+                 SH_C3[6] * x * (xx - (real)3 * yy) * s[14 * 3 + c];
+        }
+      }
+    }
+    res += (real)0.5;
+    clamped[c] = res < (real)0;
+    col[c] = RMAX(res, (real)0);
+  }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Preprocess forward (fastgs_preprocess.metal:384-484).                     */
 /* Outputs must be zero-filled by the caller (fastgs_preprocess.cpp:83-86).  */
@@ -428,36 +465,9 @@ void orc_preprocess_fwd(const orc_params* prm, const real* means3d, const real* 
       clamped[3 * (size_t)i + 1] = 0;
       clamped[3 * (size_t)i + 2] = 0;
     } else {
-      /* compute_color_from_sh (:117-169); dir = v / |v| */
-      real v[3] = {m[0] - campos[0], m[1] - campos[1], m[2] - campos[2]};
-      real len = RSQRT(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
-      real x = v[0] / len, y = v[1] / len, z = v[2] / len;
-      const real* d = dc + 3 * (size_t)i;
-      const real* s = sh + (size_t)i * (size_t)prm->max_sh_coeffs * 3;
-      for (int c = 0; c < 3; ++c) {
-        real res = SH_C0 * d[c];
-        if (prm->degree > 0) {
-          res = res - SH_C1 * y * s[0 * 3 + c] + SH_C1 * z * s[1 * 3 + c] - SH_C1 * x * s[2 * 3 + c];
-          if (prm->degree > 1) {
-            real xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
-            res += SH_C2[0] * xy * s[3 * 3 + c] + SH_C2[1] * yz * s[4 * 3 + c] +
-                   SH_C2[2] * ((real)2 * zz - xx - yy) * s[5 * 3 + c] +
-                   SH_C2[3] * xz * s[6 * 3 + c] + SH_C2[4] * (xx - yy) * s[7 * 3 + c];
-            if (prm->degree > 2) {
-              res += SH_C3[0] * y * ((real)3 * xx - yy) * s[8 * 3 + c] +
-                     SH_C3[1] * xy * z * s[9 * 3 + c] +
-                     SH_C3[2] * y * ((real)4 * zz - xx - yy) * s[10 * 3 + c] +
-                     SH_C3[3] * z * ((real)2 * zz - (real)3 * xx - (real)3 * yy) * s[11 * 3 + c] +
-                     SH_C3[4] * x * ((real)4 * zz - xx - yy) * s[12 * 3 + c] +
-                     SH_C3[5] * z * (xx - yy) * s[13 * 3 + c] +
-                     SH_C3[6] * x * (xx - (real)3 * yy) * s[14 * 3 + c];
-            }
-          }
-        }
-        res += (real)0.5;
-        clamped[3 * (size_t)i + c] = res < (real)0;
-        col[c] = RMAX(res, (real)0);
-      }
+      orc_color_from_sh(prm->degree, m, campos, dc + 3 * (size_t)i,
+                        sh + (size_t)i * (size_t)prm->max_sh_coeffs * 3, col,
+                        clamped + 3 * (size_t)i);
     }
     for (int c = 0; c < 3; ++c) rgb[3 * (size_t)i + c] = col[c];
     depths[i] = p_view[2];

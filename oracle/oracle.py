@@ -125,6 +125,18 @@ class Oracle:
         co = self._f(conic_opacity, (4,))
         return int(fn(px, py, _ptr(co), gx, gy, mult))
 
+    def color_from_sh(self, degree, mean, campos, dc, sh):
+        """orc_color_from_sh for one Gaussian: returns (rgb, clamped)."""
+        fn = self.lib.orc_color_from_sh
+        fn.restype = None
+        fn.argtypes = [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+        col = np.zeros(3, self.dt)
+        cl = np.zeros(3, np.uint8)
+        shv = self._f(sh, (-1,)) if sh is not None and np.asarray(sh).size else np.zeros(45, self.dt)
+        fn(degree, _ptr(self._f(mean, (3,))), _ptr(self._f(campos, (3,))), _ptr(self._f(dc, (3,))),
+           _ptr(shv), _ptr(col), _ptr(cl))
+        return col, cl.astype(bool)
+
     # -- stages ----------------------------------------------------------
     def preprocess_fwd(self, means3d, opacities, viewmatrix, projmatrix, campos, vsp_in,
                        image_width, image_height, tan_fovx=1.0, tan_fovy=1.0, degree=0,
