@@ -216,6 +216,27 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
+// DPP lane move (GFX9 data-parallel primitives): lanes whose source is out of
+// range, or whose row is masked off, read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the 64 lanes with DPP adds; the total is valid in lane 63 only.
+// quad_perm(1,0,3,2), quad_perm(2,3,0,1), row_shr:4, row_shr:8 sum each row
+// of 16 into its lane 15; row_bcast:15 and row_bcast:31 fold the four rows.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x114>(v);
+  v += dpp_mov<0x118>(v);
+  v += dpp_mov<0x142, 0xA>(v);
+  v += dpp_mov<0x143, 0xC>(v);
+  return v;
+}
+
 // Block-wide exclusive scan of one u32 per thread (blockDim.x a multiple of
 // 64, at most 1024).  Returns the exclusive prefix; *total gets the block sum.
 // s_tmp needs blockDim.x/64 + 1 entries.

@@ -9,14 +9,16 @@
 // pixel has stopped (__syncthreads_count).
 //
 // Backward (per-(pixel, splat) semantics of
-// fastgs_rasterize_backward.metal:24-278): same tiling, splats walked back to
-// front from the tile's max_contrib.  Each pixel recovers T_j = T_{j+1} /
-// (1 - alpha_j) starting from final_T and carries the colour accumulated
-// behind the splat, so no per-bucket sampled state is needed.  Per splat, each
-// wavefront sums its 64 pixels' 11 gradient terms with cross-lane reductions
-// (skipped when no lane contributes), adds them into an LDS accumulator for
-// the batch, and the batch is flushed with one set of global float atomics per
-// (splat, tile).
+// fastgs_rasterize_backward.metal:24-278): one wavefront per tile, each lane
+// owning four pixels (one per 16x4 strip); splats are walked back to front
+// from the tile's max_contrib in LDS batches of 64.  Each pixel recovers
+// T_j = T_{j+1} / (1 - alpha_j) starting from final_T and carries the colour
+// accumulated behind the splat, so no per-bucket sampled state is needed.
+// Strips a splat cannot reach (conservative alpha >= 1/255 extent) are skipped
+// wave-uniformly and exp is skipped below a per-splat power threshold.  Per
+// splat, the lane's four pixel terms are summed in registers and the 11
+// gradient terms are reduced across the wave with DPP adds into LDS; each
+// batch is flushed with one set of global float atomics per (splat, tile).
 #include "fgs_common.hpp"
 
 namespace fgs {
@@ -151,23 +153,53 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
 }
 
 constexpr int kGradTerms = 11;
+constexpr int kBwdBatch = 64;
 
+// Culling data of a splat for the backward: rows [lo, hi] outside which no
+// pixel can reach alpha >= 1/255, and a power threshold below which alpha <
+// 1/255 for certain.  alpha >= 1/255 needs o*exp(power) >= 1/255, i.e.
+// q(d) = d^T Conic d <= tau = 2 ln(255 o).  The row extent of {q <= tau} is
+// sqrt(tau * a / det); it is widened to tau' = 1.1 tau + 1 plus 2 pixels.
+// Ill-conditioned or non-positive conics and NaN opacities are not culled.
+__device__ __forceinline__ float4 splat_cull(float x, float y, float a, float b, float c, float o) {
+  const float inf = __builtin_huge_valf();
+  float4 r = make_float4(-inf, inf, -inf, 0.f);  // (row_lo, row_hi, power_min, -)
+  if (!(o == o)) return r;
+  if (!(255.0f * o >= 0.999f)) {  // alpha <= o < 1/255: never contributes
+    r.x = inf;
+    r.y = -inf;
+    r.z = inf;
+    return r;
+  }
+  const float tau = 2.0f * det_logf(255.0f * o);
+  r.z = -0.5f * tau - 0.01f;
+  const float det = a * c - b * b;
+  if (!(a > 0.f) || !(c > 0.f) || !(det > 1e-3f * a * c)) return r;
+  const float tq = fmaxf(tau, 0.0f) * 1.1f + 1.0f;
+  const float hy = __builtin_sqrtf(tq * a / det) + 2.0f;
+  r.x = y - hy;
+  r.y = y + hy;
+  (void)x;
+  return r;
+}
+
+// One wavefront per 16x16 tile; lane l owns the pixels (col l&15, row 4k +
+// l/16), k = 0..3, one in each 16x4 strip.
 template <int NCH>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64)
 raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, RasterShape sh) {
-  __shared__ float4 s_a[256];
-  __shared__ float4 s_b[256];
-  __shared__ float s_c[256];
-  __shared__ uint32_t s_g[256];
-  __shared__ float s_acc[256 * kGradTerms];
+  __shared__ float4 s_a[kBwdBatch];
+  __shared__ float4 s_b[kBwdBatch];
+  __shared__ float4 s_cull[kBwdBatch];
+  __shared__ float s_c[kBwdBatch];
+  __shared__ uint32_t s_g[kBwdBatch];
+  __shared__ float s_acc[kGradTerms][kBwdBatch];
   const int tile = (int)blockIdx.x;
   const int tx = tile % sh.gx, ty = tile / sh.gx;
-  const int t = (int)threadIdx.x;
-  const int lx = t & 15, ly = t >> 4;
-  const int px = tx * kTile + lx, py = ty * kTile + ly;
-  const bool inside = px < sh.W && py < sh.H;
+  const int l = (int)threadIdx.x;
+  const int px = tx * kTile + (l & 15);
+  const int row0 = ty * kTile + (l >> 4);
   const size_t HW = (size_t)sh.W * (size_t)sh.H;
-  const size_t pix = inside ? (size_t)py * sh.W + px : 0;
   uint32_t end = io.ranges[2 * tile + 1];
   if ((int64_t)end > prm.list_len) end = (uint32_t)prm.list_len;
   uint32_t start = io.ranges[2 * tile];
@@ -175,109 +207,125 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
   int last = (int)io.max_contrib[tile];
   if (last > (int)(end - start)) last = (int)(end - start);
   if (last <= 0) return;  // uniform per workgroup
-  const int nc = inside ? (int)io.n_contrib[pix] : 0;
-  const float Tf = inside ? io.final_t[pix] : 0.0f;
-  float T = Tf;
-  float dL[3] = {0.0f, 0.0f, 0.0f};
-  float bg_dot = 0.0f;
-  if (inside) {
+  const int P = prm.num_points;
+  int nc[4];
+  float T[4], Tf[4], bgd[4], dL[4][3], S[4][3];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      dL[c] = io.dL_dout_color[(size_t)c * HW + pix];
-      bg_dot += io.background[c] * dL[c];
+  for (int k = 0; k < 4; ++k) {
+    const int py = row0 + 4 * k;
+    const bool inside = px < sh.W && py < sh.H;
+    const size_t pix = inside ? (size_t)py * sh.W + px : 0;
+    nc[k] = inside ? (int)io.n_contrib[pix] : 0;
+    Tf[k] = inside ? io.final_t[pix] : 0.0f;
+    T[k] = Tf[k];
+    bgd[k] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      dL[k][c] = (inside && c < NCH) ? io.dL_dout_color[(size_t)c * HW + pix] : 0.0f;
+      S[k][c] = 0.0f;
     }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) bgd[k] += io.background[c] * dL[k][c];
   }
-  const float pxf = (float)px, pyf = (float)py;
+  int ncmax = imax(imax(nc[0], nc[1]), imax(nc[2], nc[3]));
+  const float pxf = (float)px;
   const float ddelx_dx = 0.5f * (float)sh.W;
   const float ddely_dy = 0.5f * (float)sh.H;
-  float S[3] = {0.0f, 0.0f, 0.0f};
-  const int P = prm.num_points;
-  const int rounds = (last + 255) / 256;
+  const int rounds = (last + kBwdBatch - 1) / kBwdBatch;
   for (int r = 0; r < rounds; ++r) {
-    const int hi = last - r * 256;
-    const int lo = hi > 256 ? hi - 256 : 0;
+    const int hi = last - r * kBwdBatch;
+    const int lo = hi > kBwdBatch ? hi - kBwdBatch : 0;
     const int cnt = hi - lo;
-    if (t < cnt) {
-      const uint32_t g = io.point_list[start + lo + t];
+    if (l < cnt) {
+      const uint32_t g = io.point_list[start + lo + l];
       float4 a, b;
       float c;
-      stage_splat<NCH>(g, (uint32_t)prm.num_points, io.means2d, io.colors, prm.num_channels, io.conic_opacity, a, b, c);
-      s_a[t] = a;
-      s_b[t] = b;
-      s_c[t] = c;
-      s_g[t] = g;
+      stage_splat<NCH>(g, (uint32_t)P, io.means2d, io.colors, prm.num_channels, io.conic_opacity,
+                       a, b, c);
+      s_a[l] = a;
+      s_b[l] = b;
+      s_c[l] = c;
+      s_g[l] = g;
+      s_cull[l] = splat_cull(a.x, a.y, a.z, a.w, b.x, b.y);
     }
 #pragma unroll
-    for (int k = 0; k < kGradTerms; ++k) s_acc[k * 256 + t] = 0.0f;
+    for (int k = 0; k < kGradTerms; ++k) s_acc[k][l] = 0.0f;
     __syncthreads();
     for (int j = cnt - 1; j >= 0; --j) {
       const int jj = lo + j;
+      if (__ballot(jj < ncmax) == 0ull) continue;  // no pixel of the tile reaches splat jj
+      const float4 a = s_a[j];
+      const float4 b = s_b[j];
+      const float4 cu = s_cull[j];
+      const float cz = s_c[j];
       float v[kGradTerms];
 #pragma unroll
       for (int k = 0; k < kGradTerms; ++k) v[k] = 0.0f;
-      bool contrib = false;
-      if (jj < nc) {
-        const float4 a = s_a[j];
-        const float4 b = s_b[j];
+      bool any = false;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float strip_lo = (float)(ty * kTile + 4 * k);
+        if (!(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;  // uniform
+        if (jj >= nc[k]) continue;
+        const float pyf = (float)(row0 + 4 * k);
         const float dx = a.x - pxf;
         const float dy = a.y - pyf;
         const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-        if (power <= 0.0f) {
-          const float G = det_expf(power);
-          const float alpha = fminf(0.99f, b.y * G);
-          if (alpha >= 1.0f / 255.0f) {
-            contrib = true;
-            const float oma = 1.0f - alpha;
-            T = T / oma;
-            const float rci = 1.0f / oma;
-            const float col[3] = {b.z, b.w, s_c[j]};
-            float dL_dalpha = 0.0f;
+        if (power > 0.0f || power < cu.z) continue;
+        const float G = det_expf(power);
+        const float alpha = fminf(0.99f, b.y * G);
+        if (alpha < 1.0f / 255.0f) continue;
+        any = true;
+        const float oma = 1.0f - alpha;
+        T[k] = T[k] / oma;
+        const float Tj = T[k];
+        const float rci = 1.0f / oma;
+        const float col[3] = {b.z, b.w, cz};
+        float dL_dalpha = 0.0f;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-              v[8 + c] = alpha * T * dL[c];
-              dL_dalpha += (col[c] * T - rci * S[c]) * dL[c];
-              S[c] += col[c] * alpha * T;
-            }
-            dL_dalpha += (-Tf * rci) * bg_dot;
-            if (!(b.y * G > 0.99f)) {
-              const float dL_dG = b.y * dL_dalpha;
-              const float gdx = G * dx, gdy = G * dy;
-              const float dG_ddelx = -gdx * a.z - gdy * a.w;
-              const float dG_ddely = -gdy * b.x - gdx * a.w;
-              const float tmp_x = dL_dG * dG_ddelx * ddelx_dx;
-              const float tmp_y = dL_dG * dG_ddely * ddely_dy;
-              v[0] = tmp_x;
-              v[1] = tmp_y;
-              v[2] = fabsf(tmp_x);
-              v[3] = fabsf(tmp_y);
-              v[4] = -0.5f * gdx * dx * dL_dG;
-              v[5] = -0.5f * gdx * dy * dL_dG;
-              v[6] = -0.5f * gdy * dy * dL_dG;
-              v[7] = G * dL_dalpha;
-            }
-          }
+        for (int c = 0; c < NCH; ++c) {
+          v[8 + c] += alpha * Tj * dL[k][c];
+          dL_dalpha += (col[c] * Tj - rci * S[k][c]) * dL[k][c];
+          S[k][c] += col[c] * alpha * Tj;
+        }
+        dL_dalpha += (-Tf[k] * rci) * bgd[k];
+        if (!(b.y * G > 0.99f)) {
+          const float dL_dG = b.y * dL_dalpha;
+          const float gdx = G * dx, gdy = G * dy;
+          const float dG_ddelx = -gdx * a.z - gdy * a.w;
+          const float dG_ddely = -gdy * b.x - gdx * a.w;
+          const float tmp_x = dL_dG * dG_ddelx * ddelx_dx;
+          const float tmp_y = dL_dG * dG_ddely * ddely_dy;
+          v[0] += tmp_x;
+          v[1] += tmp_y;
+          v[2] += fabsf(tmp_x);
+          v[3] += fabsf(tmp_y);
+          v[4] += -0.5f * gdx * dx * dL_dG;
+          v[5] += -0.5f * gdx * dy * dL_dG;
+          v[6] += -0.5f * gdy * dy * dL_dG;
+          v[7] += G * dL_dalpha;
         }
       }
-      if (__ballot(contrib) != 0ull) {
+      if (__ballot(any) != 0ull) {
 #pragma unroll
-        for (int k = 0; k < kGradTerms; ++k) v[k] = wave_sum(v[k]);
-        if (lane_id() == 0) {
+        for (int k = 0; k < kGradTerms; ++k) v[k] = wave_sum_lane63(v[k]);
+        if (l == kWave - 1) {
 #pragma unroll
-          for (int k = 0; k < kGradTerms; ++k) atomicAdd(&s_acc[k * 256 + j], v[k]);
+          for (int k = 0; k < kGradTerms; ++k) s_acc[k][j] = v[k];
         }
       }
     }
     __syncthreads();
-    if (t < cnt) {
+    if (l < cnt) {
       float w[kGradTerms];
-      bool any = false;
+      bool nz = false;
 #pragma unroll
       for (int k = 0; k < kGradTerms; ++k) {
-        w[k] = s_acc[k * 256 + t];
-        any = any || (w[k] != 0.0f);
+        w[k] = s_acc[k][l];
+        nz = nz || (w[k] != 0.0f);
       }
-      if (any && s_g[t] < (uint32_t)P) {
-        const size_t g = s_g[t];
+      if (nz && s_g[l] < (uint32_t)P) {
+        const size_t g = s_g[l];
         unsafeAtomicAdd(&io.dL_dmeans2d[2 * g + 0], w[0]);
         unsafeAtomicAdd(&io.dL_dmeans2d[2 * g + 1], w[1]);
         unsafeAtomicAdd(&io.dL_dviewspace[4 * g + 0], w[0]);
@@ -386,10 +434,10 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   const int NCH = C < 3 ? C : 3;
   RasterShape sh{W, H, gx, gy};
   if (NCH == 3)
-    hipLaunchKernelGGL(raster_bwd_kernel<3>, dim3(tiles), dim3(256), 0, st, *p, *io, sh);
+    hipLaunchKernelGGL(raster_bwd_kernel<3>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
   else if (NCH == 2)
-    hipLaunchKernelGGL(raster_bwd_kernel<2>, dim3(tiles), dim3(256), 0, st, *p, *io, sh);
+    hipLaunchKernelGGL(raster_bwd_kernel<2>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
   else
-    hipLaunchKernelGGL(raster_bwd_kernel<1>, dim3(tiles), dim3(256), 0, st, *p, *io, sh);
+    hipLaunchKernelGGL(raster_bwd_kernel<1>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
   return check_launch("raster_bwd_kernel");
 }
