@@ -168,6 +168,19 @@ def roofline_entry(stage, ms, b, f):
             "frac": ach / HBM_PEAK_GBS, "ms": ms, "bytes": b, "flops": f}
 
 
+def measured_traffic(config, stage):
+    """HBM bytes per launch of the stage's main kernel from the committed rocprofv3 counter
+    runs (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            tab = json.load(f)
+        e = tab[config][stage]
+        return e["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(cfg, sc, cams, seed=0):
     """The C oracle (float build, OpenMP over host cores) on one pose of the same workload:
     full forward + L1/SSIM loss gradient (torch CPU) + backward."""
@@ -206,6 +219,8 @@ def main():
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-profile", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run one plain 256 MiB copy kernel (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "fastgs_core_amd runs on one GPU; multi-GPU is out of scope "
@@ -267,6 +282,12 @@ def main():
         loss.backward()
         return out
 
+    if args.calibrate:
+        src = torch.ones(64 << 20, device=dev)
+        dst = torch.empty_like(src)
+        torch.mul(src, 1.0, out=dst)  # reads 256 MiB, writes 256 MiB
+        torch.cuda.synchronize()
+        del src, dst
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -328,7 +349,7 @@ def main():
         result["counts"] = {"K": K, "B": B, "P_visible": Pv, "N_contrib": Nb, "tiles": T}
         result["roofline"] = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
                               "peak": d["peak"], "unit": d["unit"], "frac": d["frac"],
-                              "traffic": None}
+                              "traffic": measured_traffic(args.config, dom)}
     if not args.no_cpu_baseline:
         try:
             result["cpu_baseline"] = cpu_baseline(cfg, sc, cams)
