@@ -5,6 +5,7 @@ python_package/fastgs_core/__init__.py re-exports ``_fastgs_core``): the
 same functions, signatures, dict keys and autograd routes, computed by the
 hand-written HIP kernels in ``libfastgs_hip.so``.
 """
+from .loss import l1_ssim_loss  # noqa: F401
 from .rasterizer import (  # noqa: F401
     binning_forward,
     dummy_add,

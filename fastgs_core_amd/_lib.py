@@ -100,6 +100,11 @@ SIGNATURES = {
     "fgs_rasterize_fwd": (c_int32, [POINTER(RasterParams), POINTER(RasterFwdIO), c_void_p]),
     "fgs_rasterize_bwd": (c_int32, [POINTER(RasterParams), POINTER(RasterBwdIO), c_void_p]),
     "fgs_fill_u32": (c_int32, [c_void_p, c_uint32, c_int64, c_void_p]),
+    "fgs_l1_ssim_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
+    "fgs_l1_ssim_fwd": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, c_float,
+                                  c_void_p, c_void_p, c_void_p, c_void_p]),
+    "fgs_l1_ssim_bwd": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                                  c_int32, c_float, c_float, c_void_p, c_void_p]),
 }
 
 _lib = None

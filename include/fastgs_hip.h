@@ -259,6 +259,25 @@ typedef struct {
  * (fastgs_rasterize_backward.metal:24-278). */
 int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raster_bwd_io* io, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Training-step loss (the caller side of the path, reference               */
+/* scripts/train_scanner_fastgs.py:911-966): L = w_l1 mean|x-y| +             */
+/* w_ssim (1 - mean SSIM(x,y)), 11x11 Gaussian window (sigma 1.5), zero       */
+/* padding, per channel; x, y are [C,H,W] float32.                            */
+/* ------------------------------------------------------------------------ */
+size_t fgs_l1_ssim_workspace_bytes(int32_t C, int32_t H, int32_t W);
+
+/* Writes the loss scalar to *loss (device).  When dmaps != NULL ([3,C,H,W])
+ * also writes the per-pixel partial derivatives the backward needs. */
+int32_t fgs_l1_ssim_fwd(const float* img, const float* tgt, int32_t C, int32_t H, int32_t W,
+                        float w_l1, float w_ssim, float* loss, float* dmaps, void* workspace,
+                        void* stream);
+
+/* dimg = grad_out[0] * dL/dimg (grad_out: device scalar, NULL = 1). */
+int32_t fgs_l1_ssim_bwd(const float* img, const float* tgt, const float* dmaps,
+                        const float* grad_out, int32_t C, int32_t H, int32_t W, float w_l1,
+                        float w_ssim, float* dimg, void* stream);
+
 /* Fill a u32 buffer with a value on the stream (a kernel, graph-safe). */
 int32_t fgs_fill_u32(uint32_t* dst, uint32_t value, int64_t n, void* stream);
 
