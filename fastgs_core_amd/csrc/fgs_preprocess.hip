@@ -110,9 +110,24 @@ __device__ __forceinline__ void cov2d_eval(const Mat16& V, float mx, float my, f
   o.cov11 = U[1][0] * o.T[1][0] + U[1][1] * o.T[1][1] + U[1][2] * o.T[1][2];
 }
 
+// Block-cooperative copy of the SH rows of Gaussians [b0, b0+256) into LDS
+// (coalesced 4-byte loads across the block; rows are 180 B apart at degree 3).
+__device__ __forceinline__ void stage_sh_rows(const float* __restrict__ sh, int P, int row,
+                                              float* __restrict__ s_sh) {
+  const int b0 = (int)blockIdx.x * 256;
+  const int nb = (P - b0) < 256 ? (P - b0) : 256;
+  const float* __restrict__ src = sh + (size_t)b0 * row;
+  for (int e = (int)threadIdx.x; e < nb * row; e += 256) s_sh[e] = src[e];
+  __syncthreads();
+}
+
+template <bool kStageSH>
 __global__ void __launch_bounds__(256)
 preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_io io,
                       float focal_x, float focal_y) {
+  extern __shared__ float s_sh[];
+  const int row = prm.max_sh_coeffs * 3;
+  if (kStageSH) stage_sh_rows(io.sh, prm.P, row, s_sh);
   const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= prm.P) return;
   const size_t I = (size_t)i;
@@ -172,7 +187,8 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
           const float v0 = mx - io.campos[0], v1 = my - io.campos[1], v2 = mz - io.campos[2];
           const float len = __builtin_sqrtf(v0 * v0 + v1 * v1 + v2 * v2);
           const float x = v0 / len, y = v1 / len, z = v2 / len;
-          const float* __restrict__ s = io.sh + I * (size_t)prm.max_sh_coeffs * 3;
+          const float* __restrict__ s =
+              kStageSH ? s_sh + threadIdx.x * row : io.sh + I * (size_t)row;
           const float* __restrict__ d = io.dc + 3 * I;
           const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
 #pragma unroll
@@ -228,13 +244,24 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   }
 }
 
+template <bool kStageSH>
 __global__ void __launch_bounds__(256)
 preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_io io,
                       float focal_x, float focal_y) {
-  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (i >= prm.P) return;
-  const size_t I = (size_t)i;
+  extern __shared__ float s_sh[];
   const int msh = prm.max_sh_coeffs;
+  const int row = msh * 3;
+  if (kStageSH) stage_sh_rows(io.sh, prm.P, row, s_sh);
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  const bool valid = i < prm.P;
+  const size_t I = valid ? (size_t)i : 0;
+  // SH coefficients in registers, so the LDS rows can be reused for the
+  // gradient rows (written back coalesced at the end)
+  float shv[45];
+  if (kStageSH) {
+#pragma unroll
+    for (int k = 0; k < 45; ++k) shv[k] = (k < row) ? s_sh[threadIdx.x * row + k] : 0.0f;
+  }
   float dm[3] = {0.f, 0.f, 0.f};
   float ddc[3] = {0.f, 0.f, 0.f};
   float dcol[3] = {0.f, 0.f, 0.f};
@@ -242,9 +269,12 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
   float dsc[3] = {0.f, 0.f, 0.f};
   float dq[4] = {0.f, 0.f, 0.f, 0.f};
   float4 dvsp = make_float4(0.f, 0.f, 0.f, 0.f);
-  float* __restrict__ ds = io.dL_dsh ? io.dL_dsh + I * (size_t)msh * 3 : nullptr;
+  float dsv[45];
+#pragma unroll
+  for (int k = 0; k < 45; ++k) dsv[k] = 0.0f;
+  float* __restrict__ ds = kStageSH ? dsv : (io.dL_dsh ? io.dL_dsh + I * (size_t)msh * 3 : nullptr);
   int sh_written = 0;  // number of rest coefficients written below
-  if (io.radii[I] > 0) {
+  if (valid && io.radii[I] > 0) {
     const float px = io.means3d[3 * I + 0], py = io.means3d[3 * I + 1], pz = io.means3d[3 * I + 2];
     const Mat16 V = load_mat(io.viewmatrix);
     const Mat16 Pm = load_mat(io.projmatrix);
@@ -358,7 +388,7 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
         const float d0 = px - io.campos[0], d1 = py - io.campos[1], d2 = pz - io.campos[2];
         const float len = __builtin_sqrtf(d0 * d0 + d1 * d1 + d2 * d2);
         const float x = d0 / len, y = d1 / len, z = d2 / len;
-        const float* __restrict__ s = io.sh + I * (size_t)msh * 3;
+        const float* __restrict__ s = kStageSH ? shv : io.sh + I * (size_t)msh * 3;
         float dRGBdx[3], dRGBdy[3], dRGBdz[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
@@ -480,6 +510,19 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
     }
     if (io.dL_dviewspace_out) dvsp = *reinterpret_cast<const float4*>(io.dL_dviewspace_out + 4 * I);
   }
+  if (kStageSH) {
+    // gradient rows through LDS, then one coalesced block store
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 45; ++k)
+      if (k < row) s_sh[threadIdx.x * row + k] = dsv[k];
+    __syncthreads();
+    const int b0 = (int)blockIdx.x * 256;
+    const int nb = (prm.P - b0) < 256 ? (prm.P - b0) : 256;
+    float* __restrict__ dst = io.dL_dsh + (size_t)b0 * row;
+    for (int e = (int)threadIdx.x; e < nb * row; e += 256) dst[e] = s_sh[e];
+  }
+  if (!valid) return;
   // Write every element of every gradient row.
 #pragma unroll
   for (int k = 0; k < 3; ++k) io.dL_dmeans3d[3 * I + k] = dm[k];
@@ -496,7 +539,7 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
   if (io.dL_drotations)
     *reinterpret_cast<float4*>(io.dL_drotations + 4 * I) = make_float4(dq[0], dq[1], dq[2], dq[3]);
   *reinterpret_cast<float4*>(io.dL_dviewspace_in + 4 * I) = dvsp;
-  if (ds) {
+  if (!kStageSH && ds) {
     for (int k = sh_written * 3; k < msh * 3; ++k) ds[k] = 0.0f;
   }
 }
@@ -504,6 +547,13 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
 }  // namespace fgs
 
 using namespace fgs;
+
+// SH rows are staged through LDS when the SH colour path is active and a row
+// has at most 15 rest coefficients (45 floats: 45 KB of LDS per workgroup).
+static bool stage_sh(const fgs_preprocess_params* p) {
+  return !p->use_colors_precomp && p->degree > 0 && p->max_sh_coeffs > 0 &&
+         p->max_sh_coeffs <= 15;
+}
 
 extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
                                       const fgs_preprocess_fwd_io* io, void* stream) {
@@ -529,8 +579,11 @@ extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
   const float fx = (float)p->image_width / (2.0f * p->tan_fovx);
   const float fy = (float)p->image_height / (2.0f * p->tan_fovy);
   const unsigned blocks = (unsigned)((p->P + 255) / 256);
-  hipLaunchKernelGGL(preprocess_fwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, *p,
-                     *io, fx, fy);
+  // The forward reads SH rows only for visible Gaussians, directly: staging
+  // every row of the block through LDS measured slower (more bytes, lower
+  // occupancy) than the strided reads, which the L2 serves.
+  hipLaunchKernelGGL(preprocess_fwd_kernel<false>, dim3(blocks), dim3(256), 0,
+                     (hipStream_t)stream, *p, *io, fx, fy);
   return check_launch("preprocess_fwd_kernel");
 }
 
@@ -550,7 +603,13 @@ extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
   const float fx = 0.5f * (float)p->image_width / fmaxf(p->tan_fovx, 1e-6f);
   const float fy = 0.5f * (float)p->image_height / fmaxf(p->tan_fovy, 1e-6f);
   const unsigned blocks = (unsigned)((p->P + 255) / 256);
-  hipLaunchKernelGGL(preprocess_bwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, *p,
-                     *io, fx, fy);
+  if (stage_sh(p) && io->dL_dsh) {
+    const size_t lds = (size_t)256 * p->max_sh_coeffs * 3 * sizeof(float);
+    hipLaunchKernelGGL(preprocess_bwd_kernel<true>, dim3(blocks), dim3(256), lds,
+                       (hipStream_t)stream, *p, *io, fx, fy);
+  } else {
+    hipLaunchKernelGGL(preprocess_bwd_kernel<false>, dim3(blocks), dim3(256), 0,
+                       (hipStream_t)stream, *p, *io, fx, fy);
+  }
   return check_launch("preprocess_bwd_kernel");
 }

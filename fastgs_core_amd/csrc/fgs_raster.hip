@@ -1,12 +1,15 @@
 // fgs_raster.hip -- tile rasterization forward and backward (gfx950, wave64).
 //
 // Forward (semantics of fastgs_rasterize.metal:25-159): one 256-thread
-// workgroup per 16x16 tile, one pixel per thread.  The tile's sorted splat
-// list is streamed through LDS in batches of 256 (each thread stages one
-// splat: 2D mean, conic, opacity, colour), then every pixel blends the batch
-// front to back.  Pixels stop at T < 1e-4; a wavefront whose pixels have all
-// stopped skips the blend loop, and the workgroup leaves as soon as every
-// pixel has stopped (__syncthreads_count).
+// workgroup per 16x16 tile, one pixel per thread, wavefront w owning rows
+// 4w..4w+3.  The tile's sorted splat list is streamed through LDS in batches
+// of 256 (each thread stages one splat: 2D mean, conic, opacity, colour and
+// opacity), then every pixel blends the batch front to back.  Pixels stop at
+// T < 1e-4; a wavefront whose pixels have all stopped skips the blend loop,
+// and the workgroup leaves as soon as every pixel has stopped
+// (__syncthreads_count).  (Culling by row extent or by a power threshold
+// measured slower here: the batch barrier makes the block wait for its
+// busiest wavefront, and staging the culling data costs more than it saves.)
 //
 // Backward (per-(pixel, splat) semantics of
 // fastgs_rasterize_backward.metal:24-278): one wavefront per tile, each lane
@@ -20,6 +23,15 @@
 // gradient terms are reduced across the wave with DPP adds into LDS; each
 // batch is flushed with one set of global float atomics per (splat, tile).
 #include "fgs_common.hpp"
+
+// Backward tuning knobs (results are identical either way): skip strips a
+// splat cannot reach, and skip exp below the splat's power threshold.
+#ifndef FGS_BWD_STRIP_CULL
+#define FGS_BWD_STRIP_CULL 1
+#endif
+#ifndef FGS_BWD_POWER_CULL
+#define FGS_BWD_POWER_CULL 1
+#endif
 
 namespace fgs {
 
@@ -46,6 +58,44 @@ __device__ __forceinline__ void stage_splat(uint32_t g, uint32_t P, const float*
   a = make_float4(xy.x, xy.y, co.x, co.y);
   b = make_float4(co.z, co.w, col[0], NCH > 1 ? col[1] : 0.0f);
   c = NCH > 2 ? col[2] : 0.0f;
+}
+
+// Power below which a splat of opacity o cannot reach alpha >= 1/255:
+// o * exp(power) >= 1/255 needs power >= -ln(255 o); 0.01 of margin covers the
+// rounding of exp and of the hardware log.  +inf when o < 0.999/255 (alpha <= o: never
+// contributes), -inf for a NaN opacity (no culling).
+__device__ __forceinline__ float splat_power_min(float o) {
+  if (!(o == o)) return -__builtin_huge_valf();
+  if (!(255.0f * o >= 0.999f)) return __builtin_huge_valf();
+  return -__logf(255.0f * o) - 0.01f;
+}
+
+// Culling data of a splat: rows [lo, hi] outside which no
+// pixel can reach alpha >= 1/255, and a power threshold below which alpha <
+// 1/255 for certain.  alpha >= 1/255 needs o*exp(power) >= 1/255, i.e.
+// q(d) = d^T Conic d <= tau = 2 ln(255 o).  The row extent of {q <= tau} is
+// sqrt(tau * a / det); it is widened to tau' = 1.1 tau + 1 plus 2 pixels.
+// Ill-conditioned or non-positive conics and NaN opacities are not culled.
+__device__ __forceinline__ float4 splat_cull(float x, float y, float a, float b, float c, float o) {
+  const float inf = __builtin_huge_valf();
+  float4 r = make_float4(-inf, inf, -inf, 0.f);  // (row_lo, row_hi, power_min, -)
+  if (!(o == o)) return r;
+  if (!(255.0f * o >= 0.999f)) {  // alpha <= o < 1/255: never contributes
+    r.x = inf;
+    r.y = -inf;
+    r.z = inf;
+    return r;
+  }
+  const float tau = 2.0f * __logf(255.0f * o);
+  r.z = splat_power_min(o);
+  const float det = a * c - b * b;
+  if (!(a > 0.f) || !(c > 0.f) || !(det > 1e-3f * a * c)) return r;
+  const float tq = fmaxf(tau, 0.0f) * 1.1f + 1.0f;
+  const float hy = __builtin_sqrtf(tq * a / det) + 2.0f;
+  r.x = y - hy;
+  r.y = y + hy;
+  (void)x;
+  return r;
 }
 
 template <int NCH>
@@ -126,7 +176,8 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
         acc[0] += b.z * alpha * T;
         if (NCH > 1) acc[1] += b.w * alpha * T;
         if (NCH > 2) acc[2] += s_c[j] * alpha * T;
-        if (count_metric && s_g[j] < (uint32_t)prm.num_points) atomicAdd(&io.metric_count[s_g[j]], 1);
+        if (count_metric && s_g[j] < (uint32_t)prm.num_points)
+          atomicAdd(&io.metric_count[s_g[j]], 1);
         T = test_t;
         last = contributor;
       }
@@ -154,34 +205,6 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
 
 constexpr int kGradTerms = 11;
 constexpr int kBwdBatch = 64;
-
-// Culling data of a splat for the backward: rows [lo, hi] outside which no
-// pixel can reach alpha >= 1/255, and a power threshold below which alpha <
-// 1/255 for certain.  alpha >= 1/255 needs o*exp(power) >= 1/255, i.e.
-// q(d) = d^T Conic d <= tau = 2 ln(255 o).  The row extent of {q <= tau} is
-// sqrt(tau * a / det); it is widened to tau' = 1.1 tau + 1 plus 2 pixels.
-// Ill-conditioned or non-positive conics and NaN opacities are not culled.
-__device__ __forceinline__ float4 splat_cull(float x, float y, float a, float b, float c, float o) {
-  const float inf = __builtin_huge_valf();
-  float4 r = make_float4(-inf, inf, -inf, 0.f);  // (row_lo, row_hi, power_min, -)
-  if (!(o == o)) return r;
-  if (!(255.0f * o >= 0.999f)) {  // alpha <= o < 1/255: never contributes
-    r.x = inf;
-    r.y = -inf;
-    r.z = inf;
-    return r;
-  }
-  const float tau = 2.0f * det_logf(255.0f * o);
-  r.z = -0.5f * tau - 0.01f;
-  const float det = a * c - b * b;
-  if (!(a > 0.f) || !(c > 0.f) || !(det > 1e-3f * a * c)) return r;
-  const float tq = fmaxf(tau, 0.0f) * 1.1f + 1.0f;
-  const float hy = __builtin_sqrtf(tq * a / det) + 2.0f;
-  r.x = y - hy;
-  r.y = y + hy;
-  (void)x;
-  return r;
-}
 
 // One wavefront per 16x16 tile; lane l owns the pixels (col l&15, row 4k +
 // l/16), k = 0..3, one in each 16x4 strip.
@@ -265,21 +288,22 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float strip_lo = (float)(ty * kTile + 4 * k);
-        if (!(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;  // uniform
+        if (FGS_BWD_STRIP_CULL && !(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;
         if (jj >= nc[k]) continue;
         const float pyf = (float)(row0 + 4 * k);
         const float dx = a.x - pxf;
         const float dy = a.y - pyf;
         const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-        if (power > 0.0f || power < cu.z) continue;
+        if (power > 0.0f || (FGS_BWD_POWER_CULL && power < cu.z)) continue;
         const float G = det_expf(power);
         const float alpha = fminf(0.99f, b.y * G);
         if (alpha < 1.0f / 255.0f) continue;
         any = true;
-        const float oma = 1.0f - alpha;
-        T[k] = T[k] / oma;
+        // 1/(1-alpha) by the hardware reciprocal (1 ulp): the backward takes no
+        // decision from T, so IEEE division is not needed here.
+        const float rci = __builtin_amdgcn_rcpf(1.0f - alpha);
+        T[k] = T[k] * rci;
         const float Tj = T[k];
-        const float rci = 1.0f / oma;
         const float col[3] = {b.z, b.w, cz};
         float dL_dalpha = 0.0f;
 #pragma unroll
