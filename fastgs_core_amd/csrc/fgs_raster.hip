@@ -24,15 +24,6 @@
 // batch is flushed with one set of global float atomics per (splat, tile).
 #include "fgs_common.hpp"
 
-// Backward tuning knobs (results are identical either way): skip strips a
-// splat cannot reach, and skip exp below the splat's power threshold.
-#ifndef FGS_BWD_STRIP_CULL
-#define FGS_BWD_STRIP_CULL 1
-#endif
-#ifndef FGS_BWD_POWER_CULL
-#define FGS_BWD_POWER_CULL 1
-#endif
-
 namespace fgs {
 
 struct RasterShape {
@@ -60,42 +51,23 @@ __device__ __forceinline__ void stage_splat(uint32_t g, uint32_t P, const float*
   c = NCH > 2 ? col[2] : 0.0f;
 }
 
-// Power below which a splat of opacity o cannot reach alpha >= 1/255:
-// o * exp(power) >= 1/255 needs power >= -ln(255 o); 0.01 of margin covers the
-// rounding of exp and of the hardware log.  +inf when o < 0.999/255 (alpha <= o: never
-// contributes), -inf for a NaN opacity (no culling).
-__device__ __forceinline__ float splat_power_min(float o) {
-  if (!(o == o)) return -__builtin_huge_valf();
-  if (!(255.0f * o >= 0.999f)) return __builtin_huge_valf();
-  return -__logf(255.0f * o) - 0.01f;
-}
-
-// Culling data of a splat: rows [lo, hi] outside which no
-// pixel can reach alpha >= 1/255, and a power threshold below which alpha <
-// 1/255 for certain.  alpha >= 1/255 needs o*exp(power) >= 1/255, i.e.
-// q(d) = d^T Conic d <= tau = 2 ln(255 o).  The row extent of {q <= tau} is
-// sqrt(tau * a / det); it is widened to tau' = 1.1 tau + 1 plus 2 pixels.
-// Ill-conditioned or non-positive conics and NaN opacities are not culled.
-__device__ __forceinline__ float4 splat_cull(float x, float y, float a, float b, float c, float o) {
+// Rows [lo, hi] outside which no pixel of a splat can reach alpha >= 1/255.
+// alpha >= 1/255 needs o*exp(power) >= 1/255, i.e. q(d) = d^T Conic d <= tau =
+// 2 ln(255 o).  The row extent of {q <= tau} is sqrt(tau * a / det); it is
+// widened to tau' = 1.1 tau + 1 plus 2 pixels, which covers the rounding of
+// the hardware log and of the forward's exp.  Ill-conditioned or non-positive
+// conics and NaN opacities are not culled; o < 0.999/255 never blends.
+__device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c, float o) {
   const float inf = __builtin_huge_valf();
-  float4 r = make_float4(-inf, inf, -inf, 0.f);  // (row_lo, row_hi, power_min, -)
+  float2 r = make_float2(-inf, inf);
   if (!(o == o)) return r;
-  if (!(255.0f * o >= 0.999f)) {  // alpha <= o < 1/255: never contributes
-    r.x = inf;
-    r.y = -inf;
-    r.z = inf;
-    return r;
-  }
+  if (!(255.0f * o >= 0.999f)) return make_float2(inf, -inf);  // alpha <= o < 1/255
   const float tau = 2.0f * __logf(255.0f * o);
-  r.z = splat_power_min(o);
   const float det = a * c - b * b;
   if (!(a > 0.f) || !(c > 0.f) || !(det > 1e-3f * a * c)) return r;
   const float tq = fmaxf(tau, 0.0f) * 1.1f + 1.0f;
   const float hy = __builtin_sqrtf(tq * a / det) + 2.0f;
-  r.x = y - hy;
-  r.y = y + hy;
-  (void)x;
-  return r;
+  return make_float2(y - hy, y + hy);
 }
 
 template <int NCH>
@@ -204,7 +176,164 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
 }
 
 constexpr int kGradTerms = 11;
+constexpr int kRec = 12;  // per-splat gradient record in LDS (11 terms + 1 pad)
 constexpr int kBwdBatch = 64;
+
+// Gradient record terms: 0..3 viewspace (dx, dy, |dx|, |dy|), 4..7 conic and
+// opacity, 8..10 colour.
+__device__ __forceinline__ void permlane32_swap(float& d, float& s) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(s), false, false);
+  d = __uint_as_float(r[0]);
+  s = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void permlane16_swap(float& d, float& s) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(d), __float_as_uint(s), false, false);
+  d = __uint_as_float(r[0]);
+  s = __uint_as_float(r[1]);
+}
+
+// Sums the 11 terms over the 64 lanes and writes them into rec[0..11].
+// Stage 1 swaps the upper half of term 2i with the lower half of term 2i+1
+// (v_permlane32_swap), so one add halves two terms at once: u[i] holds term 2i
+// in lanes 0-31 and term 2i+1 in lanes 32-63.  Stage 2 does the same across
+// odd/even 16-lane rows (v_permlane16_swap): row r of w[m] then holds term
+// 4m + {0,2,1,3}[r].  Stage 3 sums each 16-lane row with four DPP adds; lane 15
+// of each row holds its row's term.
+__device__ __forceinline__ void wave_reduce_terms(float (&v)[kGradTerms], float* rec, int l) {
+  float u[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    float d = v[2 * i];
+    float s = (2 * i + 1 < kGradTerms) ? v[2 * i + 1] : 0.0f;
+    permlane32_swap(d, s);
+    u[i] = d + s;
+  }
+  float w[3];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    float d = u[2 * m], s = u[2 * m + 1];
+    permlane16_swap(d, s);
+    w[m] = d + s;
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    w[m] += dpp_mov<0xB1>(w[m]);
+    w[m] += dpp_mov<0x4E>(w[m]);
+    w[m] += dpp_mov<0x114>(w[m]);
+    w[m] += dpp_mov<0x118>(w[m]);
+  }
+  if ((l & 15) == 15) {
+    const int r = l >> 4;
+    const int t = ((r & 1) << 1) | (r >> 1);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) rec[4 * m + t] = w[m];
+  }
+}
+
+// Gradient terms of one splat for the lane's four pixels (one per 16x4
+// strip), accumulated into v.  The blend decisions repeat the forward's
+// operations exactly (same power, exp and thresholds), so T recovery and the
+// set of contributing splats match it.
+//
+// Per pixel the colour behind the splat enters only through
+// SdL = T_final * (bg . dL) + sum_c S_c dL_c (S_c: colour accumulated behind
+// the splat), so one scalar is carried instead of S_c:
+//   dL/dalpha = T_j (col . dL) - SdL / (1 - alpha),  SdL += alpha T_j (col . dL).
+// With w = G o dL/dalpha and h = (a W/2, b W/2, c H/2, b H/2) from the conic
+// (a, b, c):  d/dmean2d = -w (h.x dx + h.y dy, h.z dy + h.w dx),
+// d/dconic = -w/2 (dx^2, dx dy, dy^2), d/dopacity = G dL/dalpha.
+//
+// kSafe = false is the fast form: the terms of pixels that do not blend the
+// splat are driven to exact zeros by three selects, which needs every operand
+// finite (the caller checks the splat records, the loss gradients and the
+// carried T and SdL).
+// kSafe = true selects every accumulated term, so non-finite values reach only
+// pixels that blend the splat, as in the per-pixel definition.  Returns
+// whether any pixel of the wave blends the splat (wave-uniform); v is left
+// untouched otherwise.
+template <int NCH, bool kSafe>
+__device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, const float cz,
+                                                const float4 h, const float2 rows, const int jj,
+                                                const float pxf, const float pyf0,
+                                                const float ty0, const int (&nc)[4],
+                                                float (&T)[4], float (&SdL)[4],
+                                                const float (&dL)[4][3],
+                                                float (&v)[kGradTerms]) {
+  bool any = false;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float strip_lo = ty0 + (float)(4 * k);
+    if (!(rows.y >= strip_lo && rows.x <= strip_lo + 3.0f)) continue;  // wave-uniform
+    const float dx = a.x - pxf;
+    const float dy = a.y - (pyf0 + (float)(4 * k));
+    const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
+    const float G = det_expf(power);
+    const float oG = b.y * G;
+    const float alpha = fminf(0.99f, oG);
+    const bool act = jj < nc[k] && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
+    if (__ballot(act) == 0ull) continue;  // wave-uniform
+    any = true;
+    // 1/(1-alpha) by the hardware reciprocal (1 ulp): the backward takes no
+    // decision from T, so IEEE division is not needed here.
+    const float rci = __builtin_amdgcn_rcpf(1.0f - alpha);
+    const float Tj = act ? T[k] * rci : T[k];
+    T[k] = Tj;
+    {
+#pragma clang fp contract(fast)
+      const float aT = act ? alpha * Tj : 0.0f;
+      const float col[3] = {b.z, b.w, cz};
+      float cdl = col[0] * dL[k][0];
+#pragma unroll
+      for (int c = 1; c < NCH; ++c) cdl += col[c] * dL[k][c];
+      const float dL_dalpha = Tj * cdl - rci * SdL[k];
+      if (kSafe) {
+        SdL[k] += act ? aT * cdl : 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) v[8 + c] += act ? aT * dL[k][c] : 0.0f;
+      } else {
+        SdL[k] += aT * cdl;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) v[8 + c] += aT * dL[k][c];
+      }
+      const bool geo = act && !(oG > 0.99f);
+      const float gm = geo ? G : 0.0f;
+      const float w = gm * (b.y * dL_dalpha);
+      const float tmp_x = -w * (h.x * dx + h.y * dy);
+      const float tmp_y = -w * (h.z * dy + h.w * dx);
+      const float hw = -0.5f * w;
+      const float t[8] = {tmp_x,       tmp_y,       fabsf(tmp_x), fabsf(tmp_y),
+                          hw * dx * dx, hw * dx * dy, hw * dy * dy, gm * dL_dalpha};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] += kSafe ? (geo ? t[i] : 0.0f) : t[i];
+    }
+  }
+  return any;
+}
+
+// Splats lo+cnt-1 .. lo of the staged batch, back to front: per splat the
+// gradient terms of the lane's pixels, then (when any pixel blends it) the
+// wave reduction into the splat's LDS record.  kSafe is fixed per batch, so
+// the accumulators stay in one set of registers through the loop.
+template <int NCH, bool kSafe>
+__device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, const float4* s_h,
+                                          const float4* s_cull, float* s_rec, const int lo,
+                                          const int cnt, const int l, const float pxf,
+                                          const float pyf0, const float ty0, const int (&nc)[4],
+                                          float (&T)[4], float (&SdL)[4],
+                                          const float (&dL)[4][3], float (&v)[kGradTerms]) {
+  for (int j = cnt - 1; j >= 0; --j) {
+    const float4 a = s_a[j];
+    const float4 b = s_b[j];
+    const float4 hh = s_h[j];
+    const float4 cu = s_cull[j];
+    if (bwd_splat_terms<NCH, kSafe>(a, b, cu.w, hh, make_float2(cu.x, cu.y), lo + j, pxf, pyf0,
+                                    ty0, nc, T, SdL, dL, v)) {
+      wave_reduce_terms(v, s_rec + j * kRec, l);
+#pragma unroll
+      for (int k = 0; k < kGradTerms; ++k) v[k] = 0.0f;
+    }
+  }
+}
 
 // One wavefront per 16x16 tile; lane l owns the pixels (col l&15, row 4k +
 // l/16), k = 0..3, one in each 16x4 strip.
@@ -213,10 +342,10 @@ __global__ void __launch_bounds__(64)
 raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, RasterShape sh) {
   __shared__ float4 s_a[kBwdBatch];
   __shared__ float4 s_b[kBwdBatch];
-  __shared__ float4 s_cull[kBwdBatch];
-  __shared__ float s_c[kBwdBatch];
+  __shared__ float4 s_h[kBwdBatch];     // conic scaled by (W/2, H/2)
+  __shared__ float4 s_cull[kBwdBatch];  // (row_lo, row_hi, -, colour 3)
   __shared__ uint32_t s_g[kBwdBatch];
-  __shared__ float s_acc[kGradTerms][kBwdBatch];
+  __shared__ float s_rec[kBwdBatch * kRec];
   const int tile = (int)blockIdx.x;
   const int tx = tile % sh.gx, ty = tile / sh.gx;
   const int l = (int)threadIdx.x;
@@ -232,141 +361,108 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
   if (last <= 0) return;  // uniform per workgroup
   const int P = prm.num_points;
   int nc[4];
-  float T[4], Tf[4], bgd[4], dL[4][3], S[4][3];
+  float T[4], SdL[4], dL[4][3];
+  bool lane_finite = true;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int py = row0 + 4 * k;
     const bool inside = px < sh.W && py < sh.H;
     const size_t pix = inside ? (size_t)py * sh.W + px : 0;
     nc[k] = inside ? (int)io.n_contrib[pix] : 0;
-    Tf[k] = inside ? io.final_t[pix] : 0.0f;
-    T[k] = Tf[k];
-    bgd[k] = 0.0f;
+    T[k] = inside ? io.final_t[pix] : 0.0f;
+    float bgd = 0.0f;
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
       dL[k][c] = (inside && c < NCH) ? io.dL_dout_color[(size_t)c * HW + pix] : 0.0f;
-      S[k][c] = 0.0f;
+      lane_finite = lane_finite && __builtin_isfinite(dL[k][c]);
     }
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) bgd[k] += io.background[c] * dL[k][c];
+    for (int c = 0; c < NCH; ++c) bgd += io.background[c] * dL[k][c];
+    SdL[k] = T[k] * bgd;
+    lane_finite = lane_finite && __builtin_isfinite(SdL[k]) && __builtin_isfinite(T[k]);
   }
-  int ncmax = imax(imax(nc[0], nc[1]), imax(nc[2], nc[3]));
+  const bool tile_finite = __ballot(!lane_finite) == 0ull;
   const float pxf = (float)px;
-  const float ddelx_dx = 0.5f * (float)sh.W;
-  const float ddely_dy = 0.5f * (float)sh.H;
+  const float pyf0 = (float)row0;
+  const float ty0 = (float)(ty * kTile);
+  const float hx = 0.5f * (float)sh.W;
+  const float hy = 0.5f * (float)sh.H;
+  float v[kGradTerms];
+#pragma unroll
+  for (int k = 0; k < kGradTerms; ++k) v[k] = 0.0f;
   const int rounds = (last + kBwdBatch - 1) / kBwdBatch;
   for (int r = 0; r < rounds; ++r) {
     const int hi = last - r * kBwdBatch;
     const int lo = hi > kBwdBatch ? hi - kBwdBatch : 0;
     const int cnt = hi - lo;
+    bool fin = true;
     if (l < cnt) {
       const uint32_t g = io.point_list[start + lo + l];
       float4 a, b;
       float c;
       stage_splat<NCH>(g, (uint32_t)P, io.means2d, io.colors, prm.num_channels, io.conic_opacity,
                        a, b, c);
+      const float4 hh = make_float4(a.z * hx, a.w * hx, b.x * hy, a.w * hy);
       s_a[l] = a;
       s_b[l] = b;
-      s_c[l] = c;
+      s_h[l] = hh;
       s_g[l] = g;
-      s_cull[l] = splat_cull(a.x, a.y, a.z, a.w, b.x, b.y);
+      const float2 cu = splat_rows(a.y, a.z, a.w, b.x, b.y);
+      fin = __builtin_isfinite(a.x) && __builtin_isfinite(a.y) &&
+                       __builtin_isfinite(hh.x) && __builtin_isfinite(hh.y) &&
+                       __builtin_isfinite(hh.z) && __builtin_isfinite(hh.w) &&
+                       __builtin_isfinite(a.z) && __builtin_isfinite(a.w) &&
+                       __builtin_isfinite(b.x) && __builtin_isfinite(b.y) &&
+                       __builtin_isfinite(b.z) && __builtin_isfinite(b.w) && __builtin_isfinite(c);
+      s_cull[l] = make_float4(cu.x, cu.y, 0.0f, c);
     }
 #pragma unroll
-    for (int k = 0; k < kGradTerms; ++k) s_acc[k][l] = 0.0f;
+    for (int i = 0; i < kRec; ++i) s_rec[i * kBwdBatch + l] = 0.0f;
+    // The fast form needs finite operands: the tile's loss gradients, every
+    // splat record of the batch and the carried pixel state (an infinite
+    // colour makes SdL infinite for the splats in front of it).
+    bool ok = fin;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ok = ok && __builtin_isfinite(T[k]) && __builtin_isfinite(SdL[k]);
+    const bool fast = tile_finite && __ballot(!ok) == 0ull;
     __syncthreads();
-    for (int j = cnt - 1; j >= 0; --j) {
-      const int jj = lo + j;
-      if (__ballot(jj < ncmax) == 0ull) continue;  // no pixel of the tile reaches splat jj
-      const float4 a = s_a[j];
-      const float4 b = s_b[j];
-      const float4 cu = s_cull[j];
-      const float cz = s_c[j];
-      float v[kGradTerms];
-#pragma unroll
-      for (int k = 0; k < kGradTerms; ++k) v[k] = 0.0f;
-      bool any = false;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float strip_lo = (float)(ty * kTile + 4 * k);
-        if (FGS_BWD_STRIP_CULL && !(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;
-        if (jj >= nc[k]) continue;
-        const float pyf = (float)(row0 + 4 * k);
-        const float dx = a.x - pxf;
-        const float dy = a.y - pyf;
-        const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-        if (power > 0.0f || (FGS_BWD_POWER_CULL && power < cu.z)) continue;
-        const float G = det_expf(power);
-        const float alpha = fminf(0.99f, b.y * G);
-        if (alpha < 1.0f / 255.0f) continue;
-        any = true;
-        // 1/(1-alpha) by the hardware reciprocal (1 ulp): the backward takes no
-        // decision from T, so IEEE division is not needed here.
-        const float rci = __builtin_amdgcn_rcpf(1.0f - alpha);
-        T[k] = T[k] * rci;
-        const float Tj = T[k];
-        const float col[3] = {b.z, b.w, cz};
-        float dL_dalpha = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          v[8 + c] += alpha * Tj * dL[k][c];
-          dL_dalpha += (col[c] * Tj - rci * S[k][c]) * dL[k][c];
-          S[k][c] += col[c] * alpha * Tj;
-        }
-        dL_dalpha += (-Tf[k] * rci) * bgd[k];
-        if (!(b.y * G > 0.99f)) {
-          const float dL_dG = b.y * dL_dalpha;
-          const float gdx = G * dx, gdy = G * dy;
-          const float dG_ddelx = -gdx * a.z - gdy * a.w;
-          const float dG_ddely = -gdy * b.x - gdx * a.w;
-          const float tmp_x = dL_dG * dG_ddelx * ddelx_dx;
-          const float tmp_y = dL_dG * dG_ddely * ddely_dy;
-          v[0] += tmp_x;
-          v[1] += tmp_y;
-          v[2] += fabsf(tmp_x);
-          v[3] += fabsf(tmp_y);
-          v[4] += -0.5f * gdx * dx * dL_dG;
-          v[5] += -0.5f * gdx * dy * dL_dG;
-          v[6] += -0.5f * gdy * dy * dL_dG;
-          v[7] += G * dL_dalpha;
-        }
-      }
-      if (__ballot(any) != 0ull) {
-#pragma unroll
-        for (int k = 0; k < kGradTerms; ++k) v[k] = wave_sum_lane63(v[k]);
-        if (l == kWave - 1) {
-#pragma unroll
-          for (int k = 0; k < kGradTerms; ++k) s_acc[k][j] = v[k];
-        }
-      }
-    }
+    if (fast)
+      bwd_batch<NCH, false>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, T, SdL,
+                            dL, v);
+    else
+      bwd_batch<NCH, true>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, T, SdL,
+                           dL, v);
     __syncthreads();
-    if (l < cnt) {
-      float w[kGradTerms];
-      bool nz = false;
-#pragma unroll
-      for (int k = 0; k < kGradTerms; ++k) {
-        w[k] = s_acc[k][l];
-        nz = nz || (w[k] != 0.0f);
-      }
-      if (nz && s_g[l] < (uint32_t)P) {
-        const size_t g = s_g[l];
-        unsafeAtomicAdd(&io.dL_dmeans2d[2 * g + 0], w[0]);
-        unsafeAtomicAdd(&io.dL_dmeans2d[2 * g + 1], w[1]);
-        unsafeAtomicAdd(&io.dL_dviewspace[4 * g + 0], w[0]);
-        unsafeAtomicAdd(&io.dL_dviewspace[4 * g + 1], w[1]);
-        unsafeAtomicAdd(&io.dL_dviewspace[4 * g + 2], w[2]);
-        unsafeAtomicAdd(&io.dL_dviewspace[4 * g + 3], w[3]);
-        unsafeAtomicAdd(&io.dL_dconic_opacity[4 * g + 0], w[4]);
-        unsafeAtomicAdd(&io.dL_dconic_opacity[4 * g + 1], w[5]);
-        unsafeAtomicAdd(&io.dL_dconic_opacity[4 * g + 2], w[6]);
-        unsafeAtomicAdd(&io.dL_dconic_opacity[4 * g + 3], w[7]);
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-          unsafeAtomicAdd(&io.dL_dcolors[g * (size_t)prm.num_channels + c], w[8 + c]);
+    // Flush: item q = (splat q/12, term q%12), so the lanes of one atomic
+    // instruction cover the consecutive terms of about five splats.
+    const uint32_t C = (uint32_t)prm.num_channels;
+#pragma unroll 1
+    for (int i = 0; i < kRec; ++i) {
+      const int q = i * kBwdBatch + l;
+      const int s = q / kRec, t = q - (q / kRec) * kRec;
+      if (s < cnt && t < 8 + NCH) {
+        const float w = s_rec[q];
+        const uint32_t g = s_g[s];
+        if (w != 0.0f && g < (uint32_t)P) {
+          float* dst = t < 4 ? io.dL_dviewspace + 4 * (size_t)g + t
+                             : (t < 8 ? io.dL_dconic_opacity + 4 * (size_t)g + (t - 4)
+                                      : io.dL_dcolors + (size_t)g * C + (t - 8));
+          unsafeAtomicAdd(dst, w);
+        }
       }
     }
     __syncthreads();
   }
+}
+
+// dL/dmeans2d equals the first two viewspace terms: copied after the
+// accumulation instead of being accumulated twice.
+__global__ void __launch_bounds__(256)
+copy_means2d_grad_kernel(const float* __restrict__ vsp, float* __restrict__ dmeans2d, int P) {
+  const int g = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (g >= P) return;
+  const float4 v = *reinterpret_cast<const float4*>(vsp + 4 * (size_t)g);
+  *reinterpret_cast<float2*>(dmeans2d + 2 * (size_t)g) = make_float2(v.x, v.y);
 }
 
 }  // namespace fgs
@@ -446,12 +542,16 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_rasterize_bwd: missing gradient tensor");
   hipStream_t st = (hipStream_t)stream;
   if (P > 0) {
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->dL_dmeans2d), 0u, 2 * (int64_t)P, stream);
     fgs_fill_u32(reinterpret_cast<uint32_t*>(io->dL_dcolors), 0u, (int64_t)C * P, stream);
     fgs_fill_u32(reinterpret_cast<uint32_t*>(io->dL_dconic_opacity), 0u, 4 * (int64_t)P, stream);
     fgs_fill_u32(reinterpret_cast<uint32_t*>(io->dL_dviewspace), 0u, 4 * (int64_t)P, stream);
   }
-  if (tiles == 0 || P == 0) return check_launch("rasterize_bwd");
+  if (P == 0) return check_launch("rasterize_bwd");
+  if (tiles == 0) {
+    hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
+                       io->dL_dviewspace, io->dL_dmeans2d, P);
+    return check_launch("copy_means2d_grad_kernel");
+  }
   if (!io->ranges || !io->point_list || !io->means2d || !io->colors || !io->conic_opacity ||
       !io->background || !io->final_t || !io->n_contrib || !io->max_contrib || !io->dL_dout_color)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_rasterize_bwd: missing tensor");
@@ -463,5 +563,8 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
     hipLaunchKernelGGL(raster_bwd_kernel<2>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
   else
     hipLaunchKernelGGL(raster_bwd_kernel<1>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
-  return check_launch("raster_bwd_kernel");
+  if (check_launch("raster_bwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
+  hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
+                     io->dL_dviewspace, io->dL_dmeans2d, P);
+  return check_launch("copy_means2d_grad_kernel");
 }

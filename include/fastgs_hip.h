@@ -9,6 +9,10 @@
  * element the reference zero-fills is written by the library on the stream
  * (kernels, never host memsets and never hipMemsetAsync).
  *
+ * Alignment: arrays of rows of 2 floats ([N,2]) must be 8-byte aligned and
+ * rows of 4 floats ([N,4]) 16-byte aligned, as hipMalloc returns them; the
+ * kernels read and write such rows as one vector.
+ *
  * Errors: every entry point returns FGS_OK (0) or a negative code; the
  * message of the last failure on the calling thread is fgs_last_error().
  *

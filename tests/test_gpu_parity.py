@@ -125,6 +125,57 @@ def test_backward_parity(oracle, case):
                                atol=1e-5 * np.abs(rg["raster"]["means2d"]).max())
 
 
+def _assert_nonfinite_pattern_and_close(name, got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    fin = np.isfinite(ref)
+    np.testing.assert_array_equal(np.isfinite(got), fin, err_msg=f"{name}: non-finite pattern")
+    assert_grad_close(name, np.where(fin, got, 0.0), np.where(fin, ref, 0.0))
+
+
+def test_rasterize_backward_nonfinite_inputs(oracle):
+    """NaN loss gradients at a few pixels and an infinite splat colour reach
+    exactly the gradient entries the per-(pixel, splat) definition sends them
+    to; every other entry still matches the oracle (the kernel's fast form is
+    used only where all operands are finite)."""
+    import torch
+
+    import fastgs_core
+
+    sc, cam = scene_small(6, 2500, 3, 128, 96)
+    inp = syn.make_inputs(sc, cam)
+    ref = oracle.render(inp, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, sc["degree"])
+    pre, r = ref["pre"], ref["raster"]
+    W, H = cam.width, cam.height
+    rng = np.random.default_rng(21)
+    dL = rng.standard_normal((3, W * H)).astype(np.float32)
+    dL[:, [5 * W + 7, 40 * W + 64, 90 * W + 100]] = np.nan  # three pixels, three tiles
+    colors = pre["rgb"].astype(np.float32).copy()
+    hot = int(np.flatnonzero(pre["radii"] > 0)[len(np.flatnonzero(pre["radii"] > 0)) // 2])
+    colors[hot, 1] = np.inf
+    _say("rasterize backward non-finite inputs, inf colour on", hot)
+    g = oracle.rasterize_bwd(ref["ranges"], ref["point_list"], pre["xys"], colors,
+                             pre["conic_opacity"], inp["background"], r["final_t"], r["n_contrib"],
+                             dL, W, H)
+    assert np.isnan(g["means2d"]).any() and np.isfinite(g["means2d"]).any()
+    dev = torch.device("cuda")
+    P = pre["xys"].shape[0]
+    m2 = torch.from_numpy(pre["xys"].astype(np.float32)).to(dev).requires_grad_(True)
+    col = torch.from_numpy(colors).to(dev).requires_grad_(True)
+    co = torch.from_numpy(pre["conic_opacity"].astype(np.float32)).to(dev).requires_grad_(True)
+    vsp = torch.zeros((P, 4), dtype=torch.float32, device=dev, requires_grad=True)
+    T = ref["ranges"].shape[0]
+    out = fastgs_core.rasterize_forward(
+        ref["ranges"], ref["point_list"], ref["bucket_offsets"], m2, col, co, inp["background"],
+        pre["radii"], None, None, vsp, W, H, 16, 16, 3, T, int(ref["bucket_offsets"][-1]), False)
+    np.testing.assert_array_equal(to_np(out["n_contrib"]).view(np.uint32), r["n_contrib"])
+    out["out_color"].backward(torch.from_numpy(dL).to(dev))
+    for name, t, rk in (("means2d", m2, "means2d"), ("colors", col, "colors"),
+                        ("conic_opacity", co, "conic_opacity"),
+                        ("viewspace", vsp, "viewspace_points")):
+        _assert_nonfinite_pattern_and_close(name, to_np(t.grad), g[rk])
+
+
 def test_rasterize_forward_standalone_closed_form():
     """Reference rasterize_smoke.py fixture: one splat at (8,8), conic (1,0,1)."""
     import fastgs_core
