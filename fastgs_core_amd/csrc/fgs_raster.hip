@@ -7,21 +7,22 @@
 // opacity), then every pixel blends the batch front to back.  Pixels stop at
 // T < 1e-4; a wavefront whose pixels have all stopped skips the blend loop,
 // and the workgroup leaves as soon as every pixel has stopped
-// (__syncthreads_count).  (Culling by row extent or by a power threshold
-// measured slower here: the batch barrier makes the block wait for its
-// busiest wavefront, and staging the culling data costs more than it saves.)
+// (__syncthreads_count).  (A one-wavefront-per-tile form with per-strip row
+// culling measured slower: at 1M splats over 1080p most splats reach every
+// row of the tiles they touch, so culling removes little work and one
+// wavefront per tile hides less latency.)
 //
 // Backward (per-(pixel, splat) semantics of
 // fastgs_rasterize_backward.metal:24-278): one wavefront per tile, each lane
 // owning four pixels (one per 16x4 strip); splats are walked back to front
 // from the tile's max_contrib in LDS batches of 64.  Each pixel recovers
-// T_j = T_{j+1} / (1 - alpha_j) starting from final_T and carries the colour
-// accumulated behind the splat, so no per-bucket sampled state is needed.
-// Strips a splat cannot reach (conservative alpha >= 1/255 extent) are skipped
-// wave-uniformly and exp is skipped below a per-splat power threshold.  Per
-// splat, the lane's four pixel terms are summed in registers and the 11
-// gradient terms are reduced across the wave with DPP adds into LDS; each
-// batch is flushed with one set of global float atomics per (splat, tile).
+// T_j = T_{j+1} / (1 - alpha_j) starting from final_T and carries one scalar
+// for the colour behind the splat, so no per-bucket sampled state is needed.
+// Strips a splat cannot reach (conservative alpha >= 1/255 row extent) are
+// skipped wave-uniformly; the pixel terms are computed without branches.  Per
+// splat, the 11 gradient terms are summed over the wave by permlane swaps and
+// DPP adds into an LDS record; each batch is flushed with global float
+// atomics whose lanes cover consecutive terms of a few splats.
 #include "fgs_common.hpp"
 
 namespace fgs {
@@ -56,11 +57,12 @@ __device__ __forceinline__ void stage_splat(uint32_t g, uint32_t P, const float*
 // 2 ln(255 o).  The row extent of {q <= tau} is sqrt(tau * a / det); it is
 // widened to tau' = 1.1 tau + 1 plus 2 pixels, which covers the rounding of
 // the hardware log and of the forward's exp.  Ill-conditioned or non-positive
-// conics and NaN opacities are not culled; o < 0.999/255 never blends.
+// conics, NaN opacities and non-finite centres are not culled; o < 0.999/255
+// never blends.
 __device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c, float o) {
   const float inf = __builtin_huge_valf();
   float2 r = make_float2(-inf, inf);
-  if (!(o == o)) return r;
+  if (!(o == o) || !__builtin_isfinite(y)) return r;
   if (!(255.0f * o >= 0.999f)) return make_float2(inf, -inf);  // alpha <= o < 1/255
   const float tau = 2.0f * __logf(255.0f * o);
   const float det = a * c - b * b;
@@ -70,7 +72,7 @@ __device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c,
   return make_float2(y - hy, y + hy);
 }
 
-template <int NCH>
+template <int NCH, bool kSampled>
 __global__ void __launch_bounds__(256)
 raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, RasterShape sh) {
   __shared__ float4 s_a[256];
@@ -122,7 +124,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
     if (!done) {
       for (int j = 0; j < cnt; ++j) {
         const int jj = base + j;
-        if (prm.write_sampled && (jj & 31) == 0) {
+        if (kSampled && (jj & 31) == 0) {
           const size_t bk = (size_t)bbm0 + (size_t)(jj >> 5);
           if ((int64_t)bk < prm.bucket_sum) {
             io.sampled_t[bk * 256 + t] = T;
@@ -145,9 +147,11 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           done = 1;
           break;
         }
-        acc[0] += b.z * alpha * T;
-        if (NCH > 1) acc[1] += b.w * alpha * T;
-        if (NCH > 2) acc[2] += s_c[j] * alpha * T;
+        // colour by fused multiply-adds (no decision depends on it)
+        const float aT = alpha * T;
+        acc[0] = __builtin_fmaf(b.z, aT, acc[0]);
+        if (NCH > 1) acc[1] = __builtin_fmaf(b.w, aT, acc[1]);
+        if (NCH > 2) acc[2] = __builtin_fmaf(s_c[j], aT, acc[2]);
         if (count_metric && s_g[j] < (uint32_t)prm.num_points)
           atomicAdd(&io.metric_count[s_g[j]], 1);
         T = test_t;
@@ -519,12 +523,18 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
     fgs_fill_u32(io->max_contrib + tiles, 0u, p->num_tiles - tiles, stream);
   if (tiles == 0) return check_launch("rasterize_fwd");
   RasterShape sh{W, H, gx, gy};
-  if (NCH == 3)
-    hipLaunchKernelGGL(raster_fwd_kernel<3>, dim3(tiles), dim3(256), 0, st, *p, *io, sh);
-  else if (NCH == 2)
-    hipLaunchKernelGGL(raster_fwd_kernel<2>, dim3(tiles), dim3(256), 0, st, *p, *io, sh);
-  else
-    hipLaunchKernelGGL(raster_fwd_kernel<1>, dim3(tiles), dim3(256), 0, st, *p, *io, sh);
+  const bool smp = p->write_sampled && p->bucket_sum > 0;
+  const dim3 grid(tiles), block(256);
+  if (NCH == 3) {
+    if (smp) hipLaunchKernelGGL((raster_fwd_kernel<3, true>), grid, block, 0, st, *p, *io, sh);
+    else hipLaunchKernelGGL((raster_fwd_kernel<3, false>), grid, block, 0, st, *p, *io, sh);
+  } else if (NCH == 2) {
+    if (smp) hipLaunchKernelGGL((raster_fwd_kernel<2, true>), grid, block, 0, st, *p, *io, sh);
+    else hipLaunchKernelGGL((raster_fwd_kernel<2, false>), grid, block, 0, st, *p, *io, sh);
+  } else {
+    if (smp) hipLaunchKernelGGL((raster_fwd_kernel<1, true>), grid, block, 0, st, *p, *io, sh);
+    else hipLaunchKernelGGL((raster_fwd_kernel<1, false>), grid, block, 0, st, *p, *io, sh);
+  }
   return check_launch("raster_fwd_kernel");
 }
 

@@ -77,6 +77,31 @@ def test_forward_pipeline_parity(oracle, case):
     np.testing.assert_allclose(to_np(out["img_final_t"]), ref["img_final_t"], rtol=0, atol=1e-5)
 
 
+def test_sampled_state_parity(oracle):
+    """write_sampled: T (bit for bit: the blend decisions depend on it) and the
+    accumulated colour (image tolerance) of every live pixel at each 32-splat
+    bucket start (sample_t / sample_ar); dead pixels keep the zero fill."""
+    import fastgs_core
+
+    sc, cam = scene_small(7, 3000, 3, 112, 80)
+    _say("sampled state", cam.width, cam.height)
+    inp = syn.make_inputs(sc, cam)
+    ref = oracle.render(inp, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, sc["degree"],
+                        write_sampled=True)
+    out = fastgs_core.rasterize_gaussians(to_torch(inp), cam.width, cam.height, 16, 16,
+                                          cam.tan_fovx, cam.tan_fovy, sc["degree"],
+                                          write_sampled=True)
+    assert ref["num_buckets"] > 0 and ref["sample_t"].size == ref["num_buckets"] * 256
+    np.testing.assert_array_equal(to_np(out["sample_t"]).reshape(-1),
+                                  np.asarray(ref["sample_t"]).reshape(-1))
+    np.testing.assert_allclose(to_np(out["sample_ar"]).reshape(-1),
+                               np.asarray(ref["sample_ar"]).reshape(-1), rtol=0, atol=IMAGE_ATOL)
+    assert (to_np(out["sample_ar"]) == 0).sum() == (np.asarray(ref["sample_ar"]) == 0).sum()
+    np.testing.assert_array_equal(to_np(out["img_n_contrib"]).view(np.uint32),
+                                  ref["img_n_contrib"])
+    np.testing.assert_allclose(to_np(out["out_color"]), ref["out_color"], rtol=0, atol=IMAGE_ATOL)
+
+
 def test_metric_count_parity(oracle):
     sc, cam = scene_small(3, 2000, 1, 96, 96)
     rng = np.random.default_rng(5)
