@@ -10,12 +10,13 @@
 //      (ceil(log2 T) bits only, 13 bits at 1080p).
 // That moves the 32 depth bits from a K-sized sort to a P-sized one.
 //
-// Radix sort: 8-bit digits, 4096-key chunks (256 threads x 16 keys),
-// per-chunk digit histograms -> one exclusive scan over the digit-major
-// histogram matrix -> a scatter pass.  The scatter ranks keys stably within
-// a wavefront with ballots over the digit bits (wave64 match-any), combines
-// the four wavefronts through LDS counters, permutes the chunk into digit
-// order in LDS, and writes each digit run contiguously to HBM.
+// Radix sort: digits of at most 8 bits (13 tile bits: 7 + 6), 4096-key
+// chunks (256 threads x 16 keys).  One kernel counts the digits of every
+// pass; each pass is then one kernel that ranks its chunk stably within each
+// wavefront with ballots over the digit bits (wave64 match-any), combines the
+// four wavefronts through LDS counters, gets each digit's global offset by
+// decoupled look-back over the earlier chunks, permutes the chunk into digit
+// order in LDS and writes each digit run contiguously to HBM.
 #include "fgs_common.hpp"
 
 namespace fgs {
@@ -26,53 +27,95 @@ constexpr int kChunk = kThreads * kItems;  // 4096
 constexpr int kWavesPerBlock = kThreads / kWave;
 
 // ---------------------------------------------------------------------------
-// Scan (u32, wrapping).  reduce -> scan partials -> final.
+// Decoupled look-back.  A pass over n items runs one workgroup per chunk of
+// kChunk items; a workgroup takes its chunk number from an atomic ticket, so
+// chunk c is only ever waited on by chunks > c whose workgroups started
+// later, and every wait ends.  Each chunk publishes, per counter, a 64-bit
+// status word: (flag << 32) | value, flag 1 = the chunk's own aggregate,
+// flag 2 = the inclusive prefix up to and including the chunk.  A chunk walks
+// back over its predecessors adding aggregates until it meets an inclusive
+// prefix.  Status words and tickets start at zero (one fill kernel per call).
+// Radix passes keep their status words chunk-major ([chunk][digit]): a
+// chunk's 256 counters are published and read as one contiguous block.
+// The spin is bounded as a backstop; it cannot run out while chunks are
+// taken in ticket order.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kThreads)
-scan_reduce_kernel(const uint32_t* __restrict__ in, int64_t n, uint32_t* __restrict__ partials) {
-  __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
-  const int64_t base = (int64_t)blockIdx.x * kChunk;
-  uint32_t sum = 0;
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + i * kThreads + threadIdx.x;
-    if (idx < n) sum += in[idx];
-  }
-  uint32_t total;
-  block_excl_scan(sum, s_tmp, &total);
-  if (threadIdx.x == 0) partials[blockIdx.x] = total;
-}
-
-// Exclusive scan of partials[0..nb) in place by one 1024-thread block.
-__global__ void __launch_bounds__(1024)
-scan_partials_kernel(uint32_t* __restrict__ partials, int64_t nb) {
-  __shared__ uint32_t s_tmp[1024 / kWave + 1];
-  uint32_t carry = 0;
-  for (int64_t base = 0; base < nb; base += 1024) {
-    const int64_t idx = base + threadIdx.x;
-    const uint32_t v = idx < nb ? partials[idx] : 0u;
-    uint32_t total;
-    const uint32_t ex = block_excl_scan(v, s_tmp, &total);
-    if (idx < nb) partials[idx] = carry + ex;
-    carry += total;
-  }
-}
-
 // Padded LDS index so that thread t reading its 16 consecutive elements is
 // free of bank conflicts.
 __device__ __forceinline__ int pad_idx(int i) { return i + (i >> 4); }
 
+constexpr uint32_t kFlagAggregate = 1u;
+constexpr uint32_t kFlagPrefix = 2u;
+constexpr uint32_t kSpinLimit = 1u << 24;
+
+__device__ __forceinline__ void status_store(uint64_t* p, uint32_t flag, uint32_t value) {
+  __hip_atomic_store(p, ((uint64_t)flag << 32) | (uint64_t)value, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Exclusive prefix for chunk `chunk` of one counter whose status words are
+// `stride` apart (status[c * stride], c < chunk): predecessors are read from
+// the nearest back, adding aggregates until an inclusive prefix is met; an
+// unpublished predecessor is polled after a short sleep.
+__device__ __forceinline__ uint32_t look_back(const uint64_t* status, int64_t chunk,
+                                              int64_t stride, uint32_t* err) {
+  uint32_t excl = 0;
+  uint32_t spins = 0;
+  int64_t c = chunk - 1;
+  while (c >= 0) {
+    const uint64_t w = __hip_atomic_load(status + c * stride, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t flag = (uint32_t)(w >> 32);
+    if (flag == 0u) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      continue;
+    }
+    excl += (uint32_t)w;
+    if (flag == kFlagPrefix) break;
+    --c;
+  }
+  return excl;
+}
+
+__device__ __forceinline__ int64_t take_ticket(uint32_t* ticket, uint32_t* s_slot) {
+  if (threadIdx.x == 0) *s_slot = atomicAdd(ticket, 1u);
+  __syncthreads();
+  return (int64_t)*s_slot;
+}
+
+// ---------------------------------------------------------------------------
+// Scan (u32, wrapping): one pass, chunk prefixes by look-back.
+// kGather: the input element i is tiles_touched[order[i]].
+// ---------------------------------------------------------------------------
+template <bool kGather>
 __global__ void __launch_bounds__(kThreads)
-scan_final_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out, int64_t n,
-                  const uint32_t* __restrict__ partials, int inclusive) {
+chained_scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict__ order,
+                    int64_t n_in, uint32_t* __restrict__ out, int64_t n, int inclusive,
+                    uint64_t* status, uint32_t* ticket, uint32_t* err) {
   __shared__ uint32_t s_data[kChunk + kChunk / 16];
   __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
-  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  __shared__ uint32_t s_slot;
+  __shared__ uint32_t s_excl;
+  const int64_t chunk = take_ticket(ticket, &s_slot);
+  const int64_t base = chunk * kChunk;
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int li = i * kThreads + threadIdx.x;
     const int64_t idx = base + li;
-    s_data[pad_idx(li)] = idx < n ? in[idx] : 0u;
+    uint32_t v = 0u;
+    if (idx < n) {
+      if (kGather) {
+        const uint32_t o = order[idx];  // indices outside [0, n_in) read as 0
+        v = (int64_t)o < n_in ? in[o] : 0u;
+      } else {
+        v = in[idx];
+      }
+    }
+    s_data[pad_idx(li)] = v;
   }
   __syncthreads();
   uint32_t v[kItems];
@@ -83,7 +126,20 @@ scan_final_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out, i
     tsum += v[k];
   }
   uint32_t total;
-  uint32_t run = block_excl_scan(tsum, s_tmp, &total) + partials[blockIdx.x];
+  const uint32_t texcl = block_excl_scan(tsum, s_tmp, &total);
+  if (threadIdx.x == 0) {
+    uint32_t excl = 0;
+    if (chunk == 0) {
+      status_store(status, kFlagPrefix, total);
+    } else {
+      status_store(status + chunk, kFlagAggregate, total);
+      excl = look_back(status, chunk, 1, err);
+      status_store(status + chunk, kFlagPrefix, excl + total);
+    }
+    s_excl = excl;
+  }
+  __syncthreads();
+  uint32_t run = texcl + s_excl;
 #pragma unroll
   for (int k = 0; k < kItems; ++k) {
     const uint32_t x = v[k];
@@ -106,22 +162,12 @@ scan_final_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out, i
   }
 }
 
-static size_t scan_ws_bytes(int64_t n) {
-  const int64_t nb = (n + kChunk - 1) / kChunk;
-  return (size_t)((nb + 1) * 4 + 255) & ~(size_t)255;
+// Zero-initialised state of one chained scan: status words, ticket, error.
+static size_t scan_state_bytes(int64_t n) {
+  const int64_t nc = (n + kChunk - 1) / kChunk;
+  return (size_t)(((nc < 1 ? 1 : nc) * 8 + 16 + 255) & ~(int64_t)255);
 }
-
-static int32_t launch_scan(const uint32_t* in, uint32_t* out, int64_t n, void* ws, bool inclusive,
-                           hipStream_t st) {
-  if (n <= 0) return FGS_OK;
-  const int64_t nb = (n + kChunk - 1) / kChunk;
-  uint32_t* partials = (uint32_t*)ws;
-  hipLaunchKernelGGL(scan_reduce_kernel, dim3((unsigned)nb), dim3(kThreads), 0, st, in, n, partials);
-  hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(1024), 0, st, partials, nb);
-  hipLaunchKernelGGL(scan_final_kernel, dim3((unsigned)nb), dim3(kThreads), 0, st, in, out, n,
-                     partials, inclusive ? 1 : 0);
-  return check_launch("scan");
-}
+static size_t scan_ws_bytes(int64_t n) { return scan_state_bytes(n); }
 
 // ---------------------------------------------------------------------------
 // Fill / copy helpers (kernels rather than hipMemsetAsync so that callers may
@@ -140,6 +186,27 @@ static void launch_fill(uint32_t* dst, uint32_t v, int64_t n, hipStream_t st) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, v, n);
 }
 
+// Scan with its state at `state` (scan_state_bytes(n), zeroed here unless
+// the caller has zeroed it already).
+template <bool kGather>
+static int32_t launch_chained_scan(const uint32_t* in, const uint32_t* order, int64_t n_in,
+                                   uint32_t* out, int64_t n, void* state, bool inclusive,
+                                   bool zeroed, hipStream_t st) {
+  if (n <= 0) return FGS_OK;
+  const int64_t nc = (n + kChunk - 1) / kChunk;
+  uint64_t* status = (uint64_t*)state;
+  uint32_t* ticket = (uint32_t*)(status + nc);
+  if (!zeroed) launch_fill((uint32_t*)state, 0u, (int64_t)(scan_state_bytes(n) / 4), st);
+  hipLaunchKernelGGL(chained_scan_kernel<kGather>, dim3((unsigned)nc), dim3(kThreads), 0, st, in,
+                     order, n_in, out, n, inclusive ? 1 : 0, status, ticket, ticket + 1);
+  return check_launch("chained_scan");
+}
+
+static int32_t launch_scan(const uint32_t* in, uint32_t* out, int64_t n, void* ws, bool inclusive,
+                           hipStream_t st) {
+  return launch_chained_scan<false>(in, nullptr, n, out, n, ws, inclusive, false, st);
+}
+
 template <typename K>
 __global__ void copy_pairs_kernel(const K* __restrict__ ki, const uint32_t* __restrict__ vi,
                                   K* __restrict__ ko, uint32_t* __restrict__ vo, int64_t n) {
@@ -151,35 +218,72 @@ __global__ void copy_pairs_kernel(const K* __restrict__ ki, const uint32_t* __re
 }
 
 // ---------------------------------------------------------------------------
-// Radix sort pass kernels.
+// One-sweep LSD radix sort: one histogram kernel for every digit pass, then
+// one kernel per pass that ranks its chunk, gets each digit's offset by
+// look-back and writes the chunk's digit runs.
 // ---------------------------------------------------------------------------
-template <typename K>
+struct SortPlan {
+  int begin, passes, bits[8];
+};
+
+static SortPlan sort_plan(int begin, int end) {
+  SortPlan pl{};
+  pl.begin = begin;
+  const int total = end - begin;
+  pl.passes = total <= 0 ? 0 : (total + 7) / 8;
+  for (int i = 0; i < pl.passes; ++i) {
+    const int rem = total - (total / pl.passes) * pl.passes;  // first `rem` passes take one more
+    pl.bits[i] = total / pl.passes + (i < rem ? 1 : 0);
+  }
+  return pl;
+}
+
+// Digit histograms of every pass: hist[pass * 256 + digit] (zeroed by the
+// caller).  kDepthKeys: the keys are made here from depths and tiles_touched
+// (visible Gaussians by depth bits, culled ones 0xFFFFFFFF) and written out.
+template <typename K, bool kDepthKeys>
 __global__ void __launch_bounds__(kThreads)
-radix_hist_kernel(const K* __restrict__ keys, int64_t n, int shift, int nbits,
-                  uint32_t* __restrict__ hist, int64_t nb) {
-  __shared__ uint32_t s_h[256];
-  s_h[threadIdx.x] = 0;
+radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* __restrict__ hist,
+                  const float* __restrict__ depths, const uint32_t* __restrict__ tiles_touched,
+                  uint32_t* __restrict__ dkeys_out) {
+  __shared__ uint32_t s_h[8][256];
+  for (int p = 0; p < pl.passes; ++p) s_h[p][threadIdx.x] = 0;
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kChunk;
-  const uint32_t mask = (1u << nbits) - 1u;
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + i * kThreads + threadIdx.x;
-    if (idx < n) atomicAdd(&s_h[(uint32_t)(keys[idx] >> shift) & mask], 1u);
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    K k;
+    if (kDepthKeys) {
+      const uint32_t dk = tiles_touched[i] ? __float_as_uint(depths[i]) : 0xFFFFFFFFu;
+      dkeys_out[i] = dk;
+      k = (K)dk;
+    } else {
+      k = keys[i];
+    }
+    int shift = pl.begin;
+    for (int p = 0; p < pl.passes; ++p) {
+      const uint32_t d = (uint32_t)(k >> shift) & ((1u << pl.bits[p]) - 1u);
+      atomicAdd(&s_h[p][d], 1u);
+      shift += pl.bits[p];
+    }
   }
   __syncthreads();
-  if ((int)threadIdx.x <= (int)mask) hist[(int64_t)threadIdx.x * nb + blockIdx.x] = s_h[threadIdx.x];
+  for (int p = 0; p < pl.passes; ++p) {
+    const uint32_t c = s_h[p][threadIdx.x];
+    if (c) atomicAdd(&hist[p * 256 + threadIdx.x], c);
+  }
 }
 
 template <typename K>
 __global__ void __launch_bounds__(kThreads)
-radix_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
-                     K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n,
-                     int shift, int nbits, const uint32_t* __restrict__ offsets, int64_t nb) {
+radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+                  K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift,
+                  int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
+                  int64_t nchunks, uint32_t* ticket, uint32_t* err) {
   __shared__ uint32_t s_wh[kWavesPerBlock][256];
   __shared__ uint32_t s_dstart[256];
   __shared__ uint32_t s_goff[256];
   __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
+  __shared__ uint32_t s_slot;
   __shared__ K s_keys[kChunk];
   __shared__ uint32_t s_vals[kChunk];
   const int t = (int)threadIdx.x;
@@ -188,8 +292,8 @@ radix_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__
   const uint32_t mask = (1u << nbits) - 1u;
 #pragma unroll
   for (int k = 0; k < kWavesPerBlock; ++k) s_wh[k][t] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kChunk + (int64_t)w * (kChunk / kWavesPerBlock);
+  const int64_t chunk = take_ticket(ticket, &s_slot);  // includes a barrier
+  const int64_t base = chunk * kChunk + (int64_t)w * (kChunk / kWavesPerBlock);
   const uint64_t lt = lanemask_lt();
   K key[kItems];
   uint32_t val[kItems];
@@ -222,6 +326,8 @@ radix_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__
       c[k] = ((uint32_t)t <= mask) ? s_wh[k][t] : 0u;
       tot += c[k];
     }
+    const uint32_t g = ((uint32_t)t <= mask) ? hist[t] : 0u;
+    const uint32_t gbase = block_excl_scan(g, s_tmp, nullptr);
     uint32_t total;
     const uint32_t ds = block_excl_scan(tot, s_tmp, &total);
     uint32_t run = ds;
@@ -231,7 +337,18 @@ radix_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__
       run += c[k];
     }
     s_dstart[t] = ds;
-    s_goff[t] = ((uint32_t)t <= mask) ? offsets[(int64_t)t * nb + blockIdx.x] : 0u;
+    if ((uint32_t)t <= mask) {
+      uint32_t excl = 0;
+      uint64_t* st = status + (size_t)t;  // chunk-major: [chunk][digit]
+      if (chunk == 0) {
+        status_store(st, kFlagPrefix, tot);
+      } else {
+        status_store(st + chunk * 256, kFlagAggregate, tot);
+        excl = look_back(st, chunk, 256, err);
+        status_store(st + chunk * 256, kFlagPrefix, excl + tot);
+      }
+      s_goff[t] = gbase + excl;
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -245,7 +362,7 @@ radix_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__
     }
   }
   __syncthreads();
-  const int64_t rem = n - (int64_t)blockIdx.x * kChunk;
+  const int64_t rem = n - chunk * kChunk;
   const int cnt = rem < kChunk ? (int)rem : kChunk;
   for (int j = t; j < cnt; j += kThreads) {
     const K k = s_keys[j];
@@ -256,58 +373,68 @@ radix_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__
   }
 }
 
+// Zero-initialised state of one sort: histograms (8 x 256), tickets (8),
+// error word, then the status words of every pass.
+static size_t sort_state_bytes(int64_t n, int passes) {
+  const int64_t nc = (n + kChunk - 1) / kChunk;
+  return (size_t)((8 * 256 * 4 + 64 + (int64_t)passes * (nc < 1 ? 1 : nc) * 256 * 8 + 255) &
+                  ~(int64_t)255);
+}
+
 template <typename K>
-static size_t sort_ws_bytes(int64_t n) {
-  const int64_t nb = (n + kChunk - 1) / kChunk;
+static size_t sort_ws_bytes(int64_t n, int passes = (int)sizeof(K)) {
   size_t b = 0;
-  b += ((size_t)n * sizeof(K) + 255) & ~(size_t)255;   // tmp keys
-  b += ((size_t)n * 4 + 255) & ~(size_t)255;           // tmp vals
-  b += ((size_t)nb * 256 * 4 + 255) & ~(size_t)255;    // histogram matrix
-  b += scan_ws_bytes(nb * 256);
+  b += ((size_t)n * sizeof(K) + 255) & ~(size_t)255;  // tmp keys
+  b += ((size_t)n * 4 + 255) & ~(size_t)255;          // tmp vals
+  b += sort_state_bytes(n, passes);
   return b;
 }
 
 // Stable sort on bits [begin, end).  vals_in may be NULL (values = index).
-// keys_in/vals_in are not modified.
-template <typename K>
+// keys_in/vals_in are not modified.  kDepthKeys: keys_in is ignored and the
+// keys are made from depths / tiles_touched (written to dkeys_out).
+template <typename K, bool kDepthKeys = false>
 static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* keys_out,
                                 uint32_t* vals_out, int64_t n, int begin, int end, void* ws,
-                                hipStream_t st) {
+                                hipStream_t st, const float* depths = nullptr,
+                                const uint32_t* tiles_touched = nullptr,
+                                uint32_t* dkeys_out = nullptr) {
   if (n <= 0) return FGS_OK;
-  const int nbits_total = end - begin;
-  if (nbits_total <= 0) {
+  const SortPlan pl = sort_plan(begin, end);
+  if (pl.passes == 0) {
     int64_t blocks = (n + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(copy_pairs_kernel<K>, dim3((unsigned)blocks), dim3(256), 0, st, keys_in,
                        vals_in, keys_out, vals_out, n);
     return check_launch("copy_pairs");
   }
-  const int passes = (nbits_total + 7) / 8;
-  const int64_t nb = (n + kChunk - 1) / kChunk;
+  const int64_t nc = (n + kChunk - 1) / kChunk;
   char* p = (char*)ws;
   K* tk = (K*)p;
   p += ((size_t)n * sizeof(K) + 255) & ~(size_t)255;
   uint32_t* tv = (uint32_t*)p;
   p += ((size_t)n * 4 + 255) & ~(size_t)255;
   uint32_t* hist = (uint32_t*)p;
-  p += ((size_t)nb * 256 * 4 + 255) & ~(size_t)255;
-  void* scan_ws = p;
-  const K* src_k = keys_in;
+  uint32_t* tickets = hist + 8 * 256;
+  uint32_t* err = tickets + 8;
+  uint64_t* status = (uint64_t*)(p + 8 * 256 * 4 + 64);
+  launch_fill(hist, 0u, (int64_t)(sort_state_bytes(n, pl.passes) / 4), st);
+  int64_t hb = nc < 1024 ? nc : 1024;
+  hipLaunchKernelGGL((radix_hist_kernel<K, kDepthKeys>), dim3((unsigned)hb), dim3(kThreads), 0, st,
+                     keys_in, n, pl, hist, depths, tiles_touched, dkeys_out);
+  const K* src_k = kDepthKeys ? (const K*)dkeys_out : keys_in;
   const uint32_t* src_v = vals_in;
-  for (int pass = 0; pass < passes; ++pass) {
-    const int shift = begin + pass * 8;
-    const int nbits = (end - shift) < 8 ? (end - shift) : 8;
-    const bool to_out = ((passes - 1 - pass) % 2) == 0;
+  int shift = begin;
+  for (int pass = 0; pass < pl.passes; ++pass) {
+    const bool to_out = ((pl.passes - 1 - pass) % 2) == 0;
     K* dk = to_out ? keys_out : tk;
     uint32_t* dv = to_out ? vals_out : tv;
-    hipLaunchKernelGGL(radix_hist_kernel<K>, dim3((unsigned)nb), dim3(kThreads), 0, st, src_k, n,
-                       shift, nbits, hist, nb);
-    const int32_t e = launch_scan(hist, hist, nb * (int64_t)(1 << nbits), scan_ws, false, st);
-    if (e != FGS_OK) return e;
-    hipLaunchKernelGGL(radix_scatter_kernel<K>, dim3((unsigned)nb), dim3(kThreads), 0, st, src_k,
-                       src_v, dk, dv, n, shift, nbits, hist, nb);
-    const int32_t e2 = check_launch("radix_scatter");
+    hipLaunchKernelGGL(radix_pass_kernel<K>, dim3((unsigned)nc), dim3(kThreads), 0, st, src_k,
+                       src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
+                       status + (size_t)pass * nc * 256, nc, tickets + pass, err);
+    const int32_t e2 = check_launch("radix_pass");
     if (e2 != FGS_OK) return e2;
+    shift += pl.bits[pass];
     src_k = dk;
     src_v = dv;
   }
@@ -360,24 +487,6 @@ duplicate_keys_kernel(int32_t P, const float* __restrict__ xys, const float* __r
   tiles_walk(xy.x, xy.y, co, gx, gy, mult, e);
 }
 
-// Depth keys of the stage-1 sort: visible Gaussians by depth bits, culled
-// ones (tiles_touched == 0) last.
-__global__ void depth_keys_kernel(int32_t P, const float* __restrict__ depths,
-                                  const uint32_t* __restrict__ tiles_touched,
-                                  uint32_t* __restrict__ dkeys) {
-  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (i >= P) return;
-  dkeys[i] = tiles_touched[i] ? __float_as_uint(depths[i]) : 0xFFFFFFFFu;
-}
-
-__global__ void gather_counts_kernel(int32_t P, const uint32_t* __restrict__ order,
-                                     const uint32_t* __restrict__ tiles_touched,
-                                     uint32_t* __restrict__ cnt) {
-  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (i >= P) return;
-  cnt[i] = tiles_touched[order[i]];
-}
-
 struct EmitTiles {
   uint32_t* tkeys;
   uint32_t* tvals;
@@ -407,6 +516,7 @@ duplicate_sorted_kernel(int32_t P, const uint32_t* __restrict__ order,
   const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= P) return;
   const uint32_t g = order[i];
+  if (g >= (uint32_t)P) return;
   const uint32_t n = tiles_touched[g];
   if (n == 0u) return;
   EmitTiles e;
@@ -423,7 +533,9 @@ duplicate_sorted_kernel(int32_t P, const uint32_t* __restrict__ order,
 }
 
 // Sorted tile ids -> 64-bit keys and tile ranges (fastgs_tile_prep.metal:10-37).
-__global__ void finalize_keys_ranges_kernel(int64_t K, const uint32_t* __restrict__ tiles,
+// Tile ids >= T and Gaussian indices >= P are never used as addresses.
+__global__ void finalize_keys_ranges_kernel(int64_t K, int32_t T, int32_t P,
+                                            const uint32_t* __restrict__ tiles,
                                             const uint32_t* __restrict__ point_list,
                                             const float* __restrict__ depths,
                                             uint64_t* __restrict__ keys64,
@@ -432,15 +544,16 @@ __global__ void finalize_keys_ranges_kernel(int64_t K, const uint32_t* __restric
   if (i >= K) return;
   const uint32_t cur = tiles[i];
   const uint32_t g = point_list[i];
-  keys64[i] = ((uint64_t)cur << 32) | (uint64_t)__float_as_uint(depths[g]);
+  const uint32_t db = g < (uint32_t)P ? __float_as_uint(depths[g]) : 0xFFFFFFFFu;
+  keys64[i] = ((uint64_t)cur << 32) | (uint64_t)db;
   if (i > 0) {
     const uint32_t prev = tiles[i - 1];
     if (cur != prev) {
-      ranges[2 * (size_t)prev + 1] = (uint32_t)i;
-      ranges[2 * (size_t)cur] = (uint32_t)i;
+      if (prev < (uint32_t)T) ranges[2 * (size_t)prev + 1] = (uint32_t)i;
+      if (cur < (uint32_t)T) ranges[2 * (size_t)cur] = (uint32_t)i;
     }
   }
-  if (i == K - 1) ranges[2 * (size_t)cur + 1] = (uint32_t)K;
+  if (i == K - 1 && cur < (uint32_t)T) ranges[2 * (size_t)cur + 1] = (uint32_t)K;
 }
 
 // Reference tile_prep semantics on 64-bit keys (any order).
@@ -470,6 +583,28 @@ __global__ void bucket_count_kernel(int32_t T, const uint32_t* __restrict__ rang
   bucket_count[t] = (uint32_t)((n + 31) / 32);
 }
 
+// Bucket counts (ceil(n / 32) per tile) and their inclusive scan, by one
+// 1024-thread workgroup walking the tiles in chunks of 1024.
+__global__ void __launch_bounds__(1024)
+bucket_scan_kernel(int32_t T, const uint32_t* __restrict__ ranges,
+                   uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets) {
+  __shared__ uint32_t s_tmp[1024 / kWave + 1];
+  uint32_t carry = 0;
+  for (int base = 0; base < T; base += 1024) {
+    const int t = base + (int)threadIdx.x;
+    uint32_t c = 0;
+    if (t < T) {
+      const int n = (int)(ranges[2 * t + 1] - ranges[2 * t]);
+      c = (uint32_t)((n + 31) / 32);
+      bucket_count[t] = c;
+    }
+    uint32_t total;
+    const uint32_t ex = block_excl_scan(c, s_tmp, &total);
+    if (t < T) bucket_offsets[t] = carry + ex + c;
+    carry += total;
+  }
+}
+
 static int bits_for(int64_t count) {
   int b = 0;
   while (b < 32 && ((int64_t)1 << b) < count) ++b;
@@ -477,7 +612,7 @@ static int bits_for(int64_t count) {
 }
 
 struct BinningLayout {
-  size_t dkeys, dkeys_s, order, cnt, scanP, sortP, tkeys, tvals, tkeys_s, sortK, scanT, total;
+  size_t dkeys, dkeys_s, order, cnt, scanP, sortP, tkeys, tvals, tkeys_s, sortK, total;
 };
 
 static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -490,12 +625,11 @@ static BinningLayout binning_layout(int32_t P, int64_t K, int32_t T) {
   L.order = o; o += al((size_t)P * 4);
   L.cnt = o; o += al((size_t)P * 4);
   L.scanP = o; o += scan_ws_bytes(P);
-  L.sortP = o; o += sort_ws_bytes<uint32_t>(P);
+  L.sortP = o; o += sort_ws_bytes<uint32_t>(P, 4);
   L.tkeys = o; o += al((size_t)K * 4);
   L.tvals = o; o += al((size_t)K * 4);
   L.tkeys_s = o; o += al((size_t)K * 4);
-  L.sortK = o; o += sort_ws_bytes<uint32_t>(K);
-  L.scanT = o; o += scan_ws_bytes(T);
+  L.sortK = o; o += sort_ws_bytes<uint32_t>(K, (bits_for(T) + 7) / 8);
   L.total = o;
   return L;
 }
@@ -544,7 +678,7 @@ extern "C" int32_t fgs_duplicate_with_keys(int32_t P, const float* xys, const fl
   return check_launch("duplicate_keys_kernel");
 }
 
-extern "C" size_t fgs_sort_workspace_bytes(int64_t n) { return sort_ws_bytes<uint64_t>(n < 1 ? 1 : n); }
+extern "C" size_t fgs_sort_workspace_bytes(int64_t n) { return sort_ws_bytes<uint64_t>(n < 1 ? 1 : n, 8); }
 
 extern "C" int32_t fgs_sort_pairs_u64(const uint64_t* keys_in, const uint32_t* values_in,
                                       uint64_t* keys_out, uint32_t* values_out, int64_t n,
@@ -611,27 +745,28 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
         !io->point_list_keys || !io->point_list)
       return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
     const unsigned gP = ceil_div_u(P, 256);
-    hipLaunchKernelGGL(depth_keys_kernel, dim3(gP), dim3(256), 0, st, P, io->depths,
-                       io->tiles_touched, dkeys);
-    int32_t e = radix_sort_pairs<uint32_t>(dkeys, nullptr, dkeys_s, order, P, 0, 32,
-                                           ws + L.sortP, st);
+    // stage 1: Gaussians by depth bits (keys made inside the histogram kernel)
+    int32_t e = radix_sort_pairs<uint32_t, true>(nullptr, nullptr, dkeys_s, order, P, 0, 32,
+                                                 ws + L.sortP, st, io->depths, io->tiles_touched,
+                                                 dkeys);
     if (e != FGS_OK) return e;
-    hipLaunchKernelGGL(gather_counts_kernel, dim3(gP), dim3(256), 0, st, P, order,
-                       io->tiles_touched, cnt);
-    e = launch_scan(cnt, cnt, P, ws + L.scanP, false, st);
+    // duplicate offsets in depth order: exclusive scan of tiles_touched[order[i]]
+    e = launch_chained_scan<true>(io->tiles_touched, order, P, cnt, P, ws + L.scanP, false, false,
+                                  st);
     if (e != FGS_OK) return e;
     hipLaunchKernelGGL(duplicate_sorted_kernel, dim3(gP), dim3(256), 0, st, P, order, cnt, io->xys,
                        io->conic_opacity, io->tiles_touched, io->mult, io->grid_x, io->grid_y, K,
                        tkeys, tvals);
+    // stage 2: duplicates by tile id, stable
     e = radix_sort_pairs<uint32_t>(tkeys, tvals, tkeys_s, io->point_list, K, 0, bits_for(T),
                                    ws + L.sortK, st);
     if (e != FGS_OK) return e;
     hipLaunchKernelGGL(finalize_keys_ranges_kernel, dim3(ceil_div_u(K, 256)), dim3(256), 0, st, K,
-                       tkeys_s, io->point_list, io->depths, io->point_list_keys, io->ranges);
+                       T, P, tkeys_s, io->point_list, io->depths, io->point_list_keys,
+                       io->ranges);
   }
-  hipLaunchKernelGGL(bucket_count_kernel, dim3(ceil_div_u(T, 256)), dim3(256), 0, st, T,
-                     io->ranges, io->bucket_count);
-  const int32_t e = launch_scan(io->bucket_count, io->bucket_offsets, T, ws + L.scanT, true, st);
-  if (e != FGS_OK) return e;
+  if (T > 0)
+    hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, st, T, io->ranges,
+                       io->bucket_count, io->bucket_offsets);
   return check_launch("binning_sorted");
 }
