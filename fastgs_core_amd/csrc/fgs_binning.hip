@@ -605,6 +605,503 @@ bucket_scan_kernel(int32_t T, const uint32_t* __restrict__ ranges,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Two-level tile binning (grids of at most 256 super-tiles).
+//
+// The tiles are grouped into super-tiles of 8x8.  Level 1 lists, for every
+// super-tile, the Gaussians whose walk touches it, in depth order (a stable
+// partition of the depth-sorted Gaussians: per-workgroup counts, a scan, then
+// ranks by ballots).  Level 2 cuts each list into chunks of 512 and, per
+// entry, walks the Gaussian inside the super-tile window to get its 64-bit
+// tile mask; per-tile counts -> per-tile starts (ranges) -> every entry's
+// position = tile start + entries of that tile in earlier chunks + rank in
+// the chunk (ballots in list order).  A tile's entries therefore come out in
+// (depth bits, index) order and are written straight to point_list and
+// point_list_keys: no K-sized sort.
+// ---------------------------------------------------------------------------
+constexpr int kSt = 8;          // super-tile edge in tiles
+constexpr int kMaxSt = 256;     // super-tiles of the two-level path
+constexpr int kL1Group = 256;   // level-1 Gaussians per workgroup
+constexpr int kL1Segs = 64;     // level-1 row segments of the count scan
+constexpr int kL2Chunk = 512;   // level-2 entries per workgroup (4 wavefronts x 128)
+
+struct StGrid {
+  int gx, gy, sgx, sgy, S;
+};
+
+// Level 1: the set of super-tiles a Gaussian's walk touches (256 bits).
+struct EmitStSet {
+  uint64_t m[4];
+  int sgx;
+  __device__ __forceinline__ void set_bit(int b) { m[b >> 6] |= 1ull << (b & 63); }
+  __device__ __forceinline__ void set_range(int lo, int hi) {  // inclusive
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int a = imax(lo, 64 * w), z = imin(hi, 64 * w + 63);
+      if (z < a) continue;
+      const int n = z - a + 1;
+      const uint64_t bits = (n >= 64) ? ~0ull : ((1ull << n) - 1ull);
+      m[w] |= bits << (a - 64 * w);
+    }
+  }
+  __device__ __forceinline__ void operator()(int u, int vmin, int vmax, bool is_y) {
+    const int b = u / kSt;
+    const int c0 = vmin / kSt, c1 = (vmax - 1) / kSt;
+    if (is_y) {  // row u, columns [vmin, vmax): contiguous super-tile ids
+      set_range(b * sgx + c0, b * sgx + c1);
+    } else {  // column u, rows [vmin, vmax)
+      for (int c = c0; c <= c1; ++c) set_bit(c * sgx + b);
+    }
+  }
+};
+
+// Level 2: 64-bit mask of the tiles of one super-tile window (bit
+// (y - y0) * 8 + (x - x0)).  The walk is clipped to the window on its own
+// axis; spans are clipped here on the other.
+struct EmitTileMask {
+  uint64_t m;
+  int x0, y0;
+  __device__ __forceinline__ void operator()(int u, int vmin, int vmax, bool is_y) {
+    if (is_y) {
+      const int xs = imax(vmin, x0), xe = imin(vmax, x0 + kSt);
+      if (xe > xs) m |= ((1ull << (xe - xs)) - 1ull) << ((u - y0) * kSt + (xs - x0));
+    } else {
+      const int ys = imax(vmin, y0), ye = imin(vmax, y0 + kSt);
+      if (ye > ys) {
+        const uint64_t hi = (ye - y0 >= kSt) ? ~0ull : ((1ull << (kSt * (ye - y0))) - 1ull);
+        const uint64_t lo = (1ull << (kSt * (ys - y0))) - 1ull;
+        m |= (hi & ~lo) & (0x0101010101010101ull << (u - x0));
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ bool st_has(const uint64_t (&m)[4], int s) {
+  return (m[s >> 6] >> (s & 63)) & 1ull;
+}
+
+// Level 1a: per depth-ordered Gaussian its super-tile set (stored), and per
+// workgroup the number of its Gaussians touching each super-tile.
+__global__ void __launch_bounds__(kL1Group)
+l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ order,
+                const float* __restrict__ xys, const float* __restrict__ conic_opacity,
+                const uint32_t* __restrict__ tiles_touched, uint64_t* __restrict__ sets,
+                uint32_t* __restrict__ cnt1) {
+  __shared__ uint32_t s_cnt[kMaxSt];
+  const int t = (int)threadIdx.x;
+  const int i = (int)blockIdx.x * kL1Group + t;
+  s_cnt[t] = 0;
+  EmitStSet e;
+  e.m[0] = e.m[1] = e.m[2] = e.m[3] = 0ull;
+  e.sgx = sg.sgx;
+  if (i < P) {
+    const uint32_t g = order[i];
+    if (g < (uint32_t)P && tiles_touched[g] != 0u) {
+      const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
+      const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
+      tiles_walk(xy.x, xy.y, co, sg.gx, sg.gy, mult, e);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(sets + 4 * (size_t)i);
+    dst[0] = make_uint4((uint32_t)e.m[0], (uint32_t)(e.m[0] >> 32), (uint32_t)e.m[1],
+                        (uint32_t)(e.m[1] >> 32));
+    dst[1] = make_uint4((uint32_t)e.m[2], (uint32_t)(e.m[2] >> 32), (uint32_t)e.m[3],
+                        (uint32_t)(e.m[3] >> 32));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint64_t b = e.m[w];
+    while (b) {
+      const int k = __builtin_ctzll(b);
+      b &= b - 1ull;
+      atomicAdd(&s_cnt[64 * w + k], 1u);
+    }
+  }
+  __syncthreads();
+  if (t < sg.S) cnt1[(size_t)blockIdx.x * sg.S + t] = s_cnt[t];
+}
+
+// Level 1b: exclusive prefix of cnt1 over the workgroups of each of kL1Segs
+// row segments (in place), and each segment's totals.
+__global__ void __launch_bounds__(kMaxSt)
+l1_seg_scan_kernel(int nwg, int S, uint32_t* __restrict__ cnt1, uint32_t* __restrict__ segsum) {
+  const int s = (int)threadIdx.x;
+  if (s >= S) return;
+  const int rows = (nwg + kL1Segs - 1) / kL1Segs;
+  const int r0 = (int)blockIdx.x * rows, r1 = imin(nwg, r0 + rows);
+  uint32_t run = 0;
+  for (int r = r0; r < r1; ++r) {
+    const uint32_t v = cnt1[(size_t)r * S + s];
+    cnt1[(size_t)r * S + s] = run;
+    run += v;
+  }
+  segsum[(size_t)blockIdx.x * S + s] = run;
+}
+
+// Level 1c (one workgroup): segment prefixes, list starts st_start[0..S], the
+// level-2 chunk table (chunk_first[0..S], chunk_st[c]) and the chunk count.
+__global__ void __launch_bounds__(kMaxSt)
+l1_top_scan_kernel(int S, uint32_t* __restrict__ segsum, uint32_t* __restrict__ st_start,
+                   uint32_t* __restrict__ chunk_first, uint32_t* __restrict__ chunk_st,
+                   uint32_t* __restrict__ nchunks, int64_t max_chunks) {
+  __shared__ uint32_t s_tmp[kMaxSt / kWave + 1];
+  const int s = (int)threadIdx.x;
+  uint32_t run = 0;
+  if (s < S) {
+    for (int g = 0; g < kL1Segs; ++g) {
+      const uint32_t v = segsum[(size_t)g * S + s];
+      segsum[(size_t)g * S + s] = run;
+      run += v;
+    }
+  }
+  uint32_t total;
+  const uint32_t start = block_excl_scan(s < S ? run : 0u, s_tmp, &total);
+  const uint32_t nch = s < S ? (run + kL2Chunk - 1) / kL2Chunk : 0u;
+  uint32_t ctotal;
+  const uint32_t cfirst = block_excl_scan(nch, s_tmp, &ctotal);
+  if (s < S) {
+    st_start[s] = start;
+    chunk_first[s] = cfirst;
+    for (uint32_t k = 0; k < nch; ++k)
+      if ((int64_t)(cfirst + k) < max_chunks) chunk_st[cfirst + k] = (uint32_t)s;
+  }
+  if (s == 0) {
+    st_start[S] = total;
+    chunk_first[S] = ctotal;
+    nchunks[0] = (int64_t)ctotal < max_chunks ? ctotal : (uint32_t)max_chunks;
+  }
+}
+
+// Level 1d: each Gaussian written into the lists of its super-tiles.  The
+// workgroup's (Gaussian, super-tile) pairs are laid out in LDS in thread
+// order (a thread's super-tiles are distinct, so their order among
+// themselves is free) and ranked per super-tile in that order, 256 pairs at
+// a time: wave64 match-any over the 8 super-tile bits, then the four waves
+// through LDS counters, as in a radix pass.
+constexpr int kL1Pairs = 2048;  // LDS pair capacity per round
+__global__ void __launch_bounds__(kL1Group)
+l1_place_kernel(int32_t P, int S, const uint32_t* __restrict__ order,
+                const uint64_t* __restrict__ sets, const uint32_t* __restrict__ cnt1,
+                const uint32_t* __restrict__ segsum, const uint32_t* __restrict__ st_start,
+                int64_t cap, uint32_t* __restrict__ list, uint8_t* __restrict__ list_st) {
+  __shared__ uint32_t s_ps[kL1Pairs];  // super-tile of each pair
+  __shared__ uint32_t s_pg[kL1Pairs];  // Gaussian of each pair
+  __shared__ uint32_t s_wh[kWavesPerBlock][kMaxSt];
+  __shared__ uint32_t s_base[kMaxSt];
+  __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
+  const int t = (int)threadIdx.x;
+  const int w = t / kWave;
+  const int lane = lane_id();
+  const int i = (int)blockIdx.x * kL1Group + t;
+  uint64_t m[4] = {0ull, 0ull, 0ull, 0ull};
+  uint32_t g = 0;
+  if (i < P) {
+    const uint4* src = reinterpret_cast<const uint4*>(sets + 4 * (size_t)i);
+    const uint4 a = src[0], b = src[1];
+    m[0] = (uint64_t)a.x | ((uint64_t)a.y << 32);
+    m[1] = (uint64_t)a.z | ((uint64_t)a.w << 32);
+    m[2] = (uint64_t)b.x | ((uint64_t)b.y << 32);
+    m[3] = (uint64_t)b.z | ((uint64_t)b.w << 32);
+    g = order[i];
+  }
+  const int rows = (int)((gridDim.x + kL1Segs - 1) / kL1Segs);
+  const int seg = (int)blockIdx.x / rows;
+  if (t < S)
+    s_base[t] = st_start[t] + segsum[(size_t)seg * S + t] + cnt1[(size_t)blockIdx.x * S + t];
+  const uint32_t np = (uint32_t)(__popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]) + __popcll(m[3]));
+  uint32_t total;
+  const uint32_t off = block_excl_scan(np, s_tmp, &total);  // has barriers
+  const uint64_t lt = lanemask_lt();
+  for (uint32_t r0 = 0; r0 < total; r0 += kL1Pairs) {
+    // this round's pairs into LDS
+    uint32_t p = off;
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd) {
+      uint64_t b = m[wd];
+      while (b) {
+        const int k = __builtin_ctzll(b);
+        b &= b - 1ull;
+        if (p >= r0 && p < r0 + kL1Pairs) {
+          s_ps[p - r0] = (uint32_t)(64 * wd + k);
+          s_pg[p - r0] = g;
+        }
+        ++p;
+      }
+    }
+    __syncthreads();
+    const uint32_t rn = (total - r0) < (uint32_t)kL1Pairs ? (total - r0) : (uint32_t)kL1Pairs;
+    for (uint32_t q0 = 0; q0 < rn; q0 += kL1Group) {
+#pragma unroll
+      for (int k = 0; k < kWavesPerBlock; ++k) s_wh[k][t] = 0u;
+      __syncthreads();
+      const uint32_t q = q0 + (uint32_t)t;
+      const bool valid = q < rn;
+      const uint32_t d = valid ? s_ps[q] : 0u;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 8; ++bit) {
+        const bool on = (d >> bit) & 1u;
+        const uint64_t mb = __ballot(on);
+        peers &= on ? mb : ~mb;
+      }
+      const uint32_t rk = (uint32_t)__popcll(peers & lt);
+      if (valid && rk == 0) s_wh[w][d] = (uint32_t)__popcll(peers);
+      __syncthreads();
+      if (valid) {
+        uint32_t pos = s_base[d] + rk;
+        for (int k = 0; k < w; ++k) pos += s_wh[k][d];
+        if ((int64_t)pos < cap) {
+          list[pos] = s_pg[q];
+          list_st[pos] = (uint8_t)d;
+        }
+      }
+      __syncthreads();
+      if (t < S) s_base[t] += s_wh[0][t] + s_wh[1][t] + s_wh[2][t] + s_wh[3][t];
+      __syncthreads();
+    }
+  }
+}
+
+// Transpose of the 64x64 bit matrix whose row l is lane l's value: lane j
+// returns column j (bit i = bit j of lane i's value).  Blocks of 32, 16, ...,
+// 1 bits are exchanged with lane ^ d; each lane sends only the half of a
+// block that moves.
+__device__ __forceinline__ uint64_t transpose64(uint64_t row) {
+  const int l = lane_id();
+  uint32_t lo = (uint32_t)row, hi = (uint32_t)(row >> 32);
+  {
+    const bool up = (l & 32) != 0;
+    const uint32_t recv = (uint32_t)__shfl_xor((int)(up ? lo : hi), 32);
+    if (up) lo = recv;
+    else hi = recv;
+  }
+#pragma unroll
+  for (int d = 16; d >= 1; d >>= 1) {
+    const uint32_t m = d == 16 ? 0x0000FFFFu
+                     : d == 8  ? 0x00FF00FFu
+                     : d == 4  ? 0x0F0F0F0Fu
+                     : d == 2  ? 0x33333333u
+                               : 0x55555555u;
+    const bool up = (l & d) != 0;
+    const uint32_t rl = (uint32_t)__shfl_xor((int)(up ? (lo & m) : (lo & ~m)), d);
+    const uint32_t rh = (uint32_t)__shfl_xor((int)(up ? (hi & m) : (hi & ~m)), d);
+    lo = up ? ((lo & ~m) | (rl >> d)) : ((lo & m) | (rl << d));
+    hi = up ? ((hi & ~m) | (rh >> d)) : ((hi & m) | (rh << d));
+  }
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+// Level 2a: per list entry (one thread each), its 64-bit tile mask inside
+// its super-tile (the walk clipped to the super-tile window).
+__global__ void __launch_bounds__(256)
+l2_mask_kernel(StGrid sg, float mult, const uint32_t* __restrict__ list,
+               const uint8_t* __restrict__ list_st, const uint32_t* __restrict__ st_start,
+               int32_t P, const float* __restrict__ xys, const float* __restrict__ conic_opacity,
+               int64_t cap, uint64_t* __restrict__ masks) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t k1 = (int64_t)st_start[sg.S] < cap ? (int64_t)st_start[sg.S] : cap;
+  if (e >= k1) return;
+  const uint32_t s = list_st[e];
+  const uint32_t g = list[e];
+  EmitTileMask em;
+  em.m = 0ull;
+  em.x0 = (int)(s % (uint32_t)sg.sgx) * kSt;
+  em.y0 = (int)(s / (uint32_t)sg.sgx) * kSt;
+  if (g < (uint32_t)P && s < (uint32_t)sg.S) {
+    const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
+    const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
+    tiles_walk_window(xy.x, xy.y, co, sg.gx, sg.gy, mult, em.x0, em.x0 + kSt, em.y0,
+                      em.y0 + kSt, em);
+  }
+  masks[e] = em.m;
+}
+
+// Level 2b: per chunk of 512 entries of one super-tile list (four
+// wavefronts, 128 entries each), the number of entries per tile.
+__global__ void __launch_bounds__(kL1Group)
+l2_count_kernel(const uint32_t* __restrict__ st_start, const uint32_t* __restrict__ chunk_first,
+                const uint32_t* __restrict__ chunk_st, const uint32_t* __restrict__ nchunks,
+                int64_t cap, const uint64_t* __restrict__ masks, uint32_t* __restrict__ cnt2) {
+  __shared__ uint32_t s_wc[kWavesPerBlock][kWave];
+  const uint32_t c = blockIdx.x;
+  if (c >= nchunks[0]) return;
+  const int t = (int)threadIdx.x, w = t / kWave, l = lane_id();
+  const uint32_t s = chunk_st[c];
+  const uint32_t e0 = st_start[s] + (c - chunk_first[s]) * kL2Chunk;
+  const uint32_t e1 = (uint32_t)imin(imin((int)st_start[s + 1], (int)(e0 + kL2Chunk)), (int)cap);
+  uint32_t cnt = 0;
+  const uint32_t q0 = e0 + (uint32_t)w * (kL2Chunk / kWavesPerBlock);
+  const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
+  for (uint32_t base = q0; base < q1; base += kWave) {
+    const uint32_t e = base + (uint32_t)l;
+    const uint64_t m = e < q1 ? masks[e] : 0ull;
+    cnt += (uint32_t)__popcll(transpose64(m));  // lane j: entries with tile j
+  }
+  s_wc[w][l] = cnt;
+  __syncthreads();
+  if (t < kWave) cnt2[(size_t)c * kWave + t] = s_wc[0][t] + s_wc[1][t] + s_wc[2][t] + s_wc[3][t];
+}
+
+// Level 2c: per super-tile, each chunk's exclusive prefix per tile (base2)
+// and the tile totals.
+__global__ void __launch_bounds__(kWave)
+l2_st_scan_kernel(StGrid sg, const uint32_t* __restrict__ chunk_first,
+                  const uint32_t* __restrict__ cnt2, uint32_t* __restrict__ base2,
+                  uint32_t* __restrict__ tile_total, int64_t max_chunks) {
+  const int s = (int)blockIdx.x;
+  const int l = (int)threadIdx.x;
+  uint32_t run = 0;
+  const uint32_t c1 = (int64_t)chunk_first[s + 1] < max_chunks ? chunk_first[s + 1]
+                                                                 : (uint32_t)max_chunks;
+  for (uint32_t c = chunk_first[s]; c < c1; ++c) {
+    const uint32_t v = cnt2[(size_t)c * kWave + l];
+    base2[(size_t)c * kWave + l] = run;
+    run += v;
+  }
+  const int x = (s % sg.sgx) * kSt + (l % kSt), y = (s / sg.sgx) * kSt + (l / kSt);
+  if (x < sg.gx && y < sg.gy) tile_total[y * sg.gx + x] = run;
+}
+
+// Level 2d (one workgroup): tile starts, ranges (empty tiles [0,0], as the
+// reference's zero-filled ranges), bucket counts and their inclusive scan.
+__global__ void __launch_bounds__(1024)
+l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
+                    uint32_t* __restrict__ tile_start, uint32_t* __restrict__ ranges,
+                    uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets) {
+  __shared__ uint32_t s_tmp[1024 / kWave + 1];
+  uint32_t carry = 0, bcarry = 0;
+  for (int base = 0; base < T; base += 1024) {
+    const int t = base + (int)threadIdx.x;
+    const uint32_t n = t < T ? tile_total[t] : 0u;
+    uint32_t total;
+    const uint32_t ex = block_excl_scan(n, s_tmp, &total);
+    const uint32_t bc = (n + 31u) / 32u;
+    uint32_t btotal;
+    const uint32_t bex = block_excl_scan(bc, s_tmp, &btotal);
+    if (t < T) {
+      const uint32_t st = carry + ex;
+      tile_start[t] = st;
+      ranges[2 * (size_t)t] = n ? st : 0u;
+      ranges[2 * (size_t)t + 1] = n ? st + n : 0u;
+      bucket_count[t] = bc;
+      bucket_offsets[t] = bcarry + bex + bc;
+    }
+    carry += total;
+    bcarry += btotal;
+  }
+}
+
+// Level 2e: every entry's tiles written at tile start + entries of the tile
+// in earlier chunks + rank in this chunk (list order).  Four wavefronts take
+// 128 entries each; per round of 64 entries and per tile j (a uniform loop)
+// the ballot of the entries having tile j gives their ranks and lane j's
+// cursor (readlane) their base.  The chunk's output is staged in LDS grouped
+// by tile and written run by run (consecutive lanes, consecutive positions;
+// wavefront w writes tiles j = w mod 4); a chunk with more than kL2Stage
+// outputs writes straight to its positions.
+constexpr int kL2Stage = 4608;
+__global__ void __launch_bounds__(kL1Group)
+l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
+               const uint32_t* __restrict__ st_start, const uint32_t* __restrict__ chunk_first,
+               const uint32_t* __restrict__ chunk_st, const uint32_t* __restrict__ nchunks,
+               const uint64_t* __restrict__ masks, const uint32_t* __restrict__ cnt2,
+               const uint32_t* __restrict__ base2, const uint32_t* __restrict__ tile_start,
+               int32_t P, const float* __restrict__ depths, int64_t K,
+               uint64_t* __restrict__ keys, uint32_t* __restrict__ point_list) {
+  __shared__ uint32_t s_g[kL2Stage];
+  __shared__ uint32_t s_db[kL2Stage];
+  __shared__ uint32_t s_wc[kWavesPerBlock][kWave];
+  const uint32_t c = blockIdx.x;
+  if (c >= nchunks[0]) return;
+  const int t = (int)threadIdx.x, w = t / kWave, l = lane_id();
+  const uint32_t s = chunk_st[c];
+  const uint32_t e0 = st_start[s] + (c - chunk_first[s]) * kL2Chunk;
+  const uint32_t e1 = (uint32_t)imin(imin((int)st_start[s + 1], (int)(e0 + kL2Chunk)), (int)K);
+  const uint32_t q0 = e0 + (uint32_t)w * (kL2Chunk / kWavesPerBlock);
+  const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
+  const int x0 = (int)(s % (uint32_t)sg.sgx) * kSt, y0 = (int)(s / (uint32_t)sg.sgx) * kSt;
+  // this wavefront's entries per tile (lane j)
+  {
+    uint32_t cnt = 0;
+    for (uint32_t base = q0; base < q1; base += kWave) {
+      const uint32_t e = base + (uint32_t)l;
+      cnt += (uint32_t)__popcll(transpose64(e < q1 ? masks[e] : 0ull));
+    }
+    s_wc[w][l] = cnt;
+  }
+  // lane j: tile j's chunk count, staging offset and global base
+  const uint32_t cj = cnt2[(size_t)c * kWave + l];
+  const uint32_t ci = wave_incl_scan(cj);
+  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)ci, kWave - 1);
+  const bool staged = total <= (uint32_t)kL2Stage;
+  uint32_t gbase = 0;
+  {
+    const int x = x0 + (l % kSt), y = y0 + (l / kSt);
+    if (x < sg.gx && y < sg.gy) gbase = tile_start[y * sg.gx + x] + base2[(size_t)c * kWave + l];
+  }
+  const uint32_t soff = ci - cj;
+  __syncthreads();
+  uint32_t cur = staged ? soff : gbase;
+  for (int k = 0; k < w; ++k) cur += s_wc[k][l];
+  const uint64_t lt = lanemask_lt();
+  for (uint32_t base = q0; base < q1; base += kWave) {
+    const uint32_t e = base + (uint32_t)l;
+    uint64_t m = 0ull;
+    uint32_t g = 0, db = 0;
+    if (e < q1) {
+      m = masks[e];
+      g = list[e];
+      db = g < (uint32_t)P ? __float_as_uint(depths[g]) : 0xFFFFFFFFu;
+    }
+    for (int j = 0; j < kWave; ++j) {
+      const bool has = (m >> j) & 1ull;
+      const uint64_t b = __ballot(has);
+      if (b == 0ull) continue;  // uniform
+      const uint32_t at =
+          (uint32_t)__builtin_amdgcn_readlane((int)cur, j) + (uint32_t)__popcll(b & lt);
+      if (has) {
+        if (staged) {
+          if (at < (uint32_t)kL2Stage) {
+            s_g[at] = g;
+            s_db[at] = db;
+          }
+        } else if ((int64_t)at < K) {
+          const uint32_t tile = (uint32_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt));
+          keys[at] = ((uint64_t)tile << 32) | (uint64_t)db;
+          point_list[at] = g;
+        }
+      }
+      if (l == j) cur += (uint32_t)__popcll(b);
+    }
+  }
+  if (!staged) return;  // uniform
+  __syncthreads();
+  for (int j = w; j < kWave; j += kWavesPerBlock) {
+    const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
+    if (nj == 0u) continue;
+    const uint32_t oj = (uint32_t)__builtin_amdgcn_readlane((int)soff, j);
+    const uint32_t gj = (uint32_t)__builtin_amdgcn_readlane((int)gbase, j);
+    const uint64_t tile = (uint64_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt)) << 32;
+    for (uint32_t k = (uint32_t)l; k < nj; k += kWave) {
+      const uint32_t pos = gj + k;
+      if ((int64_t)pos < K && oj + k < (uint32_t)kL2Stage) {
+        keys[pos] = tile | (uint64_t)s_db[oj + k];
+        point_list[pos] = s_g[oj + k];
+      }
+    }
+  }
+}
+
+static StGrid st_grid(int gx, int gy) {
+  StGrid g;
+  g.gx = gx;
+  g.gy = gy;
+  g.sgx = (gx + kSt - 1) / kSt;
+  g.sgy = (gy + kSt - 1) / kSt;
+  g.S = g.sgx * g.sgy;
+  return g;
+}
+
 static int bits_for(int64_t count) {
   int b = 0;
   while (b < 32 && ((int64_t)1 << b) < count) ++b;
@@ -632,6 +1129,44 @@ static BinningLayout binning_layout(int32_t P, int64_t K, int32_t T) {
   L.sortK = o; o += sort_ws_bytes<uint32_t>(K, (bits_for(T) + 7) / 8);
   L.total = o;
   return L;
+}
+
+// Workspace of the two-level path (sized for kMaxSt super-tiles).
+struct TwoLevelLayout {
+  size_t dkeys, dkeys_s, order, sortP, sets, cnt1, segsum, st_start, chunk_first, nchunks,
+      chunk_st, list, list_st, masks, cnt2, base2, tile_total, tile_start, total;
+  int64_t max_chunks;
+};
+
+static TwoLevelLayout two_level_layout(int32_t P, int64_t K, int32_t T) {
+  TwoLevelLayout L;
+  const int64_t nwg1 = (P + kL1Group - 1) / kL1Group;
+  L.max_chunks = K / kL2Chunk + kMaxSt + 1;
+  size_t o = 0;
+  L.dkeys = o; o += al((size_t)P * 4);
+  L.dkeys_s = o; o += al((size_t)P * 4);
+  L.order = o; o += al((size_t)P * 4);
+  L.sortP = o; o += sort_ws_bytes<uint32_t>(P, 4);
+  L.sets = o; o += al((size_t)P * 32);
+  L.cnt1 = o; o += al((size_t)nwg1 * kMaxSt * 4);
+  L.segsum = o; o += al((size_t)kL1Segs * kMaxSt * 4);
+  L.st_start = o; o += al((kMaxSt + 1) * 4);
+  L.chunk_first = o; o += al((kMaxSt + 1) * 4);
+  L.nchunks = o; o += al(4);
+  L.chunk_st = o; o += al((size_t)L.max_chunks * 4);
+  L.list = o; o += al((size_t)K * 4);
+  L.list_st = o; o += al((size_t)K);
+  L.masks = o; o += al((size_t)K * 8);
+  L.cnt2 = o; o += al((size_t)L.max_chunks * kWave * 4);
+  L.base2 = o; o += al((size_t)L.max_chunks * kWave * 4);
+  L.tile_total = o; o += al((size_t)T * 4);
+  L.tile_start = o; o += al((size_t)T * 4);
+  L.total = o;
+  return L;
+}
+
+static bool use_two_level(const StGrid& sg, int64_t K) {
+  return sg.S <= kMaxSt && K < (int64_t)0x7FFFFFFF;
 }
 
 }  // namespace fgs
@@ -713,8 +1248,10 @@ extern "C" int32_t fgs_tile_ranges(const uint64_t* keys, int64_t num_rendered, i
 }
 
 extern "C" size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, int32_t num_tiles) {
-  return binning_layout(P < 1 ? 1 : P, num_rendered < 1 ? 1 : num_rendered,
-                        num_tiles < 1 ? 1 : num_tiles).total;
+  const int32_t p = P < 1 ? 1 : P, t = num_tiles < 1 ? 1 : num_tiles;
+  const int64_t k = num_rendered < 1 ? 1 : num_rendered;
+  const size_t a = binning_layout(p, k, t).total, b = two_level_layout(p, k, t).total;
+  return a > b ? a : b;
 }
 
 extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
@@ -730,6 +1267,58 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
   if (!io->ranges || !io->bucket_count || !io->bucket_offsets || !io->workspace)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
   hipStream_t st = (hipStream_t)stream;
+  const StGrid sg = st_grid(io->grid_x, io->grid_y);
+  if (K > 0 && P > 0 && use_two_level(sg, K)) {
+    if (!io->xys || !io->depths || !io->conic_opacity || !io->tiles_touched ||
+        !io->point_list_keys || !io->point_list)
+      return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
+    const TwoLevelLayout L = two_level_layout(P, K, T);
+    char* ws = (char*)io->workspace;
+    uint32_t* dkeys = (uint32_t*)(ws + L.dkeys);
+    uint32_t* dkeys_s = (uint32_t*)(ws + L.dkeys_s);
+    uint32_t* order = (uint32_t*)(ws + L.order);
+    uint64_t* sets = (uint64_t*)(ws + L.sets);
+    uint32_t* cnt1 = (uint32_t*)(ws + L.cnt1);
+    uint32_t* segsum = (uint32_t*)(ws + L.segsum);
+    uint32_t* st_start = (uint32_t*)(ws + L.st_start);
+    uint32_t* chunk_first = (uint32_t*)(ws + L.chunk_first);
+    uint32_t* nchunks = (uint32_t*)(ws + L.nchunks);
+    uint32_t* chunk_st = (uint32_t*)(ws + L.chunk_st);
+    uint32_t* list = (uint32_t*)(ws + L.list);
+    uint8_t* list_st = (uint8_t*)(ws + L.list_st);
+    uint64_t* masks = (uint64_t*)(ws + L.masks);
+    uint32_t* cnt2 = (uint32_t*)(ws + L.cnt2);
+    uint32_t* base2 = (uint32_t*)(ws + L.base2);
+    uint32_t* tile_total = (uint32_t*)(ws + L.tile_total);
+    uint32_t* tile_start = (uint32_t*)(ws + L.tile_start);
+    // Gaussians by depth bits (keys made inside the histogram kernel)
+    int32_t e = radix_sort_pairs<uint32_t, true>(nullptr, nullptr, dkeys_s, order, P, 0, 32,
+                                                 ws + L.sortP, st, io->depths, io->tiles_touched,
+                                                 dkeys);
+    if (e != FGS_OK) return e;
+    const unsigned nwg1 = ceil_div_u(P, kL1Group);
+    hipLaunchKernelGGL(l1_count_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, io->mult, order,
+                       io->xys, io->conic_opacity, io->tiles_touched, sets, cnt1);
+    hipLaunchKernelGGL(l1_seg_scan_kernel, dim3(kL1Segs), dim3(kMaxSt), 0, st, (int)nwg1, sg.S,
+                       cnt1, segsum);
+    hipLaunchKernelGGL(l1_top_scan_kernel, dim3(1), dim3(kMaxSt), 0, st, sg.S, segsum, st_start,
+                       chunk_first, chunk_st, nchunks, L.max_chunks);
+    hipLaunchKernelGGL(l1_place_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg.S, order, sets,
+                       cnt1, segsum, st_start, K, list, list_st);
+    hipLaunchKernelGGL(l2_mask_kernel, dim3(ceil_div_u(K, 256)), dim3(256), 0, st, sg, io->mult,
+                       list, list_st, st_start, P, io->xys, io->conic_opacity, K, masks);
+    const unsigned nch = (unsigned)L.max_chunks;
+    hipLaunchKernelGGL(l2_count_kernel, dim3(nch), dim3(kL1Group), 0, st, st_start, chunk_first,
+                       chunk_st, nchunks, K, masks, cnt2);
+    hipLaunchKernelGGL(l2_st_scan_kernel, dim3(sg.S), dim3(kWave), 0, st, sg, chunk_first, cnt2,
+                       base2, tile_total, L.max_chunks);
+    hipLaunchKernelGGL(l2_tile_scan_kernel, dim3(1), dim3(1024), 0, st, T, tile_total, tile_start,
+                       io->ranges, io->bucket_count, io->bucket_offsets);
+    hipLaunchKernelGGL(l2_emit_kernel, dim3(nch), dim3(kL1Group), 0, st, sg, list, st_start,
+                       chunk_first, chunk_st, nchunks, masks, cnt2, base2, tile_start, P,
+                       io->depths, K, io->point_list_keys, io->point_list);
+    return check_launch("binning_sorted (two-level)");
+  }
   const BinningLayout L = binning_layout(P < 1 ? 1 : P, K < 1 ? 1 : K, T);
   char* ws = (char*)io->workspace;
   uint32_t* dkeys = (uint32_t*)(ws + L.dkeys);

@@ -101,9 +101,16 @@ __device__ __forceinline__ void ellipse_isect(float4 co, float disc, float t, fl
   hi = (-co.y * h + sq) / coeff + p_v;
 }
 
+// The walk restricted to the tile window [wx0, wx1) x [wy0, wy1): lines u
+// outside the window's range on the walked axis are not visited, and the
+// line state at the first visited line is the one the full walk reaches
+// there (the previous line's far edge, u*16, is always intersected), so every
+// emitted span is bit-identical to the full walk's.  Spans are not clipped on
+// the other axis.
 template <typename Emit>
-__device__ __forceinline__ uint32_t tiles_walk(float px, float py, float4 co, int gx, int gy,
-                                               float mult, Emit&& emit) {
+__device__ __forceinline__ uint32_t tiles_walk_window(float px, float py, float4 co, int gx, int gy,
+                                                      float mult, int wx0, int wx1, int wy0,
+                                                      int wy1, Emit&& emit) {
   const float disc = co.y * co.y - co.x * co.z;
   if (co.x <= 0.0f || co.z <= 0.0f || disc >= 0.0f) return 0u;
   float t = 2.0f * det_logf(co.w * 255.0f);
@@ -142,17 +149,30 @@ __device__ __forceinline__ uint32_t tiles_walk(float px, float py, float4 co, in
     tf = am0; am0 = am1; am1 = tf;
     tf = aM0; aM0 = aM1; aM1 = tf;
   }
+  int u0 = rmin0, u1 = rmax0;
+  if (is_y) {
+    u0 = imax(u0, wy0);
+    u1 = imin(u1, wy1);
+  } else {
+    u0 = imax(u0, wx0);
+    u1 = imin(u1, wx1);
+  }
   uint32_t count = 0;
   float il0, il1;            // intersect_min_line
   float iM0 = bmax1, iM1 = bmin1;  // intersect_max_line
-  float min_line = (float)rmin0 * 16.0f;
-  if (bmin0 <= min_line) {
+  float min_line = (float)u0 * 16.0f;
+  if (u0 > rmin0) {
+    // the full walk's line u0-1 intersected its far edge u0*16 (u0*16 <= bmax0)
+    ellipse_isect(co, disc, t, px, py, is_y, min_line, il0, il1);
+    iM0 = il0;
+    iM1 = il1;
+  } else if (bmin0 <= min_line) {
     ellipse_isect(co, disc, t, px, py, is_y, (float)rmin0 * 16.0f, il0, il1);
   } else {
     il0 = iM0;
     il1 = iM1;
   }
-  for (int u = rmin0; u < rmax0; ++u) {
+  for (int u = u0; u < u1; ++u) {
     const float max_line = min_line + 16.0f;
     if (max_line <= bmax0) ellipse_isect(co, disc, t, px, py, is_y, max_line, iM0, iM1);
     float e_min, e_max;
@@ -175,6 +195,12 @@ __device__ __forceinline__ uint32_t tiles_walk(float px, float py, float4 co, in
     min_line = max_line;
   }
   return count;
+}
+
+template <typename Emit>
+__device__ __forceinline__ uint32_t tiles_walk(float px, float py, float4 co, int gx, int gy,
+                                               float mult, Emit&& emit) {
+  return tiles_walk_window(px, py, co, gx, gy, mult, 0, gx, 0, gy, emit);
 }
 
 struct NoEmit {

@@ -35,13 +35,20 @@ def _render_both(oracle, sc, cam, get_flag=False, metric_map=None, bg=(0.0, 0.0,
     return inp, ref, out
 
 
-@pytest.mark.parametrize("case", ["cfg1", "sh3_small", "sh3_close"])
+@pytest.mark.parametrize("case", ["cfg1", "sh3_small", "sh3_close", "hd_grid", "wide_grid",
+                                  "uhd_grid"])
 def test_forward_pipeline_parity(oracle, case):
     if case == "cfg1":
         sc = syn.scene_config1(0, 4096)
         cam = syn.config1_camera(96, 80)
     elif case == "sh3_small":
         sc, cam = scene_small(1, 3000, 3, 160, 112)
+    elif case == "hd_grid":  # 120 x 68 tiles: 135 super-tiles of 8 x 8
+        sc, cam = scene_small(3, 6000, 1, 1920, 1080)
+    elif case == "wide_grid":  # 272 x 8 tiles: 34 x 1 super-tiles (two-level path)
+        sc, cam = scene_small(8, 3000, 1, 4352, 128)
+    elif case == "uhd_grid":  # 272 x 136 tiles: 578 super-tiles (one-level path)
+        sc, cam = scene_small(9, 2000, 1, 4352, 2176)
     else:
         sc, cam = scene_small(2, 1500, 2, 128, 128, eye=(0.3, 0.5, -1.6))
     _say("forward pipeline", case, "P", sc["means3d"].shape[0], cam.width, cam.height)
