@@ -54,19 +54,22 @@ __device__ __forceinline__ void status_store(uint64_t* p, uint32_t flag, uint32_
 }
 
 // Exclusive prefix for chunk `chunk` of one counter whose status words are
-// `stride` apart (status[c * stride], c < chunk): predecessors are read from
-// the nearest back, adding aggregates until an inclusive prefix is met; an
-// unpublished predecessor is polled after a short sleep.
+// `stride` apart (status[c * stride], c < chunk).  The nearest unread
+// predecessor is polled alone (with a short sleep) until it has published;
+// the 16 predecessors below it are then read at once (independent loads in
+// flight) and walked from the nearest, adding aggregates until an inclusive
+// prefix is met or an unpublished one is reached.
 __device__ __forceinline__ uint32_t look_back(const uint64_t* status, int64_t chunk,
                                               int64_t stride, uint32_t* err) {
+  constexpr int kWin = 16;
   uint32_t excl = 0;
   uint32_t spins = 0;
   int64_t c = chunk - 1;
   while (c >= 0) {
-    const uint64_t w = __hip_atomic_load(status + c * stride, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t flag = (uint32_t)(w >> 32);
-    if (flag == 0u) {
+    const uint64_t w0 = __hip_atomic_load(status + c * stride, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t f0 = (uint32_t)(w0 >> 32);
+    if (f0 == 0u) {
       if (++spins > kSpinLimit) {
         __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
@@ -74,9 +77,34 @@ __device__ __forceinline__ uint32_t look_back(const uint64_t* status, int64_t ch
       __builtin_amdgcn_s_sleep(1);
       continue;
     }
-    excl += (uint32_t)w;
-    if (flag == kFlagPrefix) break;
+    excl += (uint32_t)w0;
+    if (f0 == kFlagPrefix) break;
     --c;
+    if (c < 0) break;
+    const int64_t lo = c >= kWin - 1 ? c - (kWin - 1) : 0;
+    uint64_t w[kWin];
+#pragma unroll
+    for (int i = 0; i < kWin; ++i)
+      w[i] = (lo + i <= c) ? __hip_atomic_load(status + (lo + i) * stride, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)
+                           : 0ull;
+    bool stop = false, done = false;
+#pragma unroll
+    for (int i = kWin - 1; i >= 0; --i) {
+      if (stop || lo + i > c) continue;
+      const uint32_t flag = (uint32_t)(w[i] >> 32);
+      if (flag == 0u) {  // not published yet: poll it alone next
+        stop = true;
+        continue;
+      }
+      excl += (uint32_t)w[i];
+      --c;
+      if (flag == kFlagPrefix) {
+        stop = true;
+        done = true;
+      }
+    }
+    if (done) break;
   }
   return excl;
 }
