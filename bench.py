@@ -6,7 +6,8 @@ N(0,1)^3 clipped to [-2,2], log-scales N(-4.5,0.7), opacity logits N(0,1.5),
 DC U(0,1), higher-order SH N(0,0.05), SH degree 3), 1920x1080, 20 seeded
 poses on a radius-4 sphere looking at the origin, 60 degree horizontal FoV.
 A step is one training iteration without the optimizer: parameter
-activations (sigmoid / exp / quaternion normalise) -> rasterize_gaussians
+activations (sigmoid / exp / quaternion normalise; fastgs_core_amd.activate,
+one HIP kernel each way) -> rasterize_gaussians
 forward -> L1 + 0.2*(1 - SSIM) against a seeded U(0,1) target (11x11
 Gaussian window, sigma 1.5; fastgs_core_amd.l1_ssim_loss, one HIP kernel
 each way) -> backward to every Gaussian parameter and the viewspace_points
@@ -266,10 +267,9 @@ def main():
     def render(i, train=True):
         c = cam_t[i % len(cam_t)]
         vsp = torch.zeros((P, 4), device=dev, requires_grad=train)
-        opac = torch.sigmoid(raw["opacity_logits"])
-        scales = torch.exp(raw["log_scales"])
-        q = raw["quats"]
-        rots = q / (q.norm(dim=1, keepdim=True) + 1e-8)
+        # activations (sigmoid / exp / quaternion normalise): one fused kernel each way
+        scales, rots, opac = fastgs_core_amd.activate(raw["log_scales"], raw["quats"],
+                                                      raw["opacity_logits"])
         inputs = {"means3d": raw["means3d"], "scales": scales, "rotations": rots,
                   "opacities": opac, "dc": raw["dc"], "sh": raw["sh"], "background": background,
                   "metric_map": metric_map, "viewmatrix": c["viewmatrix"],

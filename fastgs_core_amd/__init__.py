@@ -6,6 +6,13 @@ same functions, signatures, dict keys and autograd routes, computed by the
 hand-written HIP kernels in ``libfastgs_hip.so``.
 """
 from .loss import l1_ssim_loss  # noqa: F401
+from .train import (  # noqa: F401
+    FastGSOptimizerPolicy,
+    FusedAdam,
+    OptimizerPolicyConfig,
+    activate,
+    expon_lr_func,
+)
 from .rasterizer import (  # noqa: F401
     binning_forward,
     dummy_add,

@@ -282,6 +282,37 @@ int32_t fgs_l1_ssim_bwd(const float* img, const float* tgt, const float* dmaps,
                         const float* grad_out, int32_t C, int32_t H, int32_t W, float w_l1,
                         float w_ssim, float* dimg, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Training-step glue.  No counterpart in the reference library: the         */
+/* reference's training scripts do these in MLX (activations                 */
+/* scripts/train_scanner_fixed.py:523-536; optimizer                          */
+/* scripts/train_scanner_fastgs.py:77-182).                                   */
+/* ------------------------------------------------------------------------ */
+
+/* scales = exp(log_scales) [P,3], rotations = q / (|q| + 1e-8) [P,4],
+ * opacities = sigmoid(opacity_logits) [P].  Each input may be NULL (its output
+ * is then not written). */
+int32_t fgs_activations_fwd(int32_t P, const float* log_scales, const float* quats,
+                            const float* opacity_logits, float* scales, float* rotations,
+                            float* opacities, void* stream);
+
+/* Backward of fgs_activations_fwd from the gradients of the activated
+ * tensors (NULL = zero): d_log_scales needs scales, d_quats needs quats,
+ * d_logits needs opacities (the forward's outputs / inputs).  A NULL output
+ * is not written. */
+int32_t fgs_activations_bwd(int32_t P, const float* quats, const float* scales,
+                            const float* opacities, const float* d_scales,
+                            const float* d_rotations, const float* d_opacities,
+                            float* d_log_scales, float* d_quats, float* d_logits, void* stream);
+
+/* One in-place Adam step over n floats (step >= 1 counts this update):
+ * m = b1 m + (1-b1) g; v = b2 v + (1-b2) g^2;
+ * bias_correction == 0 (MLX's Adam default): p -= lr m / (sqrt(v) + eps);
+ * bias_correction != 0: p -= lr/(1-b1^step) m / (sqrt(v)/sqrt(1-b2^step) + eps). */
+int32_t fgs_adam_step(float* param, const float* grad, float* exp_avg, float* exp_avg_sq,
+                      int64_t n, float lr, float beta1, float beta2, float eps, int32_t step,
+                      int32_t bias_correction, void* stream);
+
 /* Fill a u32 buffer with a value on the stream (a kernel, graph-safe). */
 int32_t fgs_fill_u32(uint32_t* dst, uint32_t value, int64_t n, void* stream);
 
