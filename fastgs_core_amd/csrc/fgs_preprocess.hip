@@ -110,24 +110,69 @@ __device__ __forceinline__ void cov2d_eval(const Mat16& V, float mx, float my, f
   o.cov11 = U[1][0] * o.T[1][0] + U[1][1] * o.T[1][1] + U[1][2] * o.T[1][2];
 }
 
-// Block-cooperative copy of the SH rows of Gaussians [b0, b0+256) into LDS
-// (coalesced 4-byte loads across the block; rows are 180 B apart at degree 3).
-__device__ __forceinline__ void stage_sh_rows(const float* __restrict__ sh, int P, int row,
+// Block-cooperative copy of the SH rows of Gaussians [b0, b0+256) into LDS.
+// The block's rows are one contiguous range of 256*kRow floats that starts on
+// a 16-byte boundary (b0*kRow*4 is a multiple of 1024 and the base is 16-byte
+// aligned), so it moves as 16-byte loads, all in flight before the first LDS
+// write, then a tail of fewer than 4 floats.
+template <int kRow>
+__device__ __forceinline__ void stage_sh_rows(const float* __restrict__ sh, int P,
                                               float* __restrict__ s_sh) {
+  constexpr int kIters = (kRow + 3) / 4;  // ceil(256*kRow/4 / 256)
   const int b0 = (int)blockIdx.x * 256;
   const int nb = (P - b0) < 256 ? (P - b0) : 256;
-  const float* __restrict__ src = sh + (size_t)b0 * row;
-  for (int e = (int)threadIdx.x; e < nb * row; e += 256) s_sh[e] = src[e];
+  const int n = nb * kRow;
+  const int n4 = n >> 2;
+  const float* __restrict__ src = sh + (size_t)b0 * kRow;
+  // n4 >= 2 (nb >= 1, kRow >= 9). Indexes past the range are clamped to its
+  // last element (several lanes then copy the same value), so the copy is
+  // branch-free and every load issues before the first wait.
+  const int t = 4 * n4 + (int)threadIdx.x;  // tail float of this thread
+  const float tv = src[t < n ? t : n - 1];
+  float4 v[kIters];
+#pragma unroll
+  for (int j = 0; j < kIters; ++j) {
+    const int e = (int)threadIdx.x + 256 * j;
+    v[j] = reinterpret_cast<const float4*>(src)[e < n4 ? e : n4 - 1];
+  }
+#pragma unroll
+  for (int j = 0; j < kIters; ++j) {
+    const int e = (int)threadIdx.x + 256 * j;
+    reinterpret_cast<float4*>(s_sh)[e < n4 ? e : n4 - 1] = v[j];
+  }
+  if (t < n) s_sh[t] = tv;
   __syncthreads();
 }
 
-template <bool kStageSH>
+// The reverse copy: LDS rows of the block's Gaussians to global memory.
+template <int kRow>
+__device__ __forceinline__ void store_sh_rows(const float* __restrict__ s_sh, int P,
+                                              float* __restrict__ dst_base) {
+  constexpr int kIters = (kRow + 3) / 4;
+  const int b0 = (int)blockIdx.x * 256;
+  const int nb = (P - b0) < 256 ? (P - b0) : 256;
+  const int n = nb * kRow;
+  const int n4 = n >> 2;
+  float* __restrict__ dst = dst_base + (size_t)b0 * kRow;
+#pragma unroll
+  for (int j = 0; j < kIters; ++j) {
+    const int e = (int)threadIdx.x + 256 * j;
+    if (e < n4) reinterpret_cast<float4*>(dst)[e] = reinterpret_cast<const float4*>(s_sh)[e];
+  }
+  const int t = 4 * n4 + (int)threadIdx.x;
+  if (t < n) dst[t] = s_sh[t];
+}
+
+// kRow = 0: SH rows are read from global memory where needed; kRow > 0: the
+// rows (kRow = 3 * max_sh_coeffs floats) of the block are staged through LDS.
+template <int kRow>
 __global__ void __launch_bounds__(256)
 preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_io io,
                       float focal_x, float focal_y) {
-  extern __shared__ float s_sh[];
-  const int row = prm.max_sh_coeffs * 3;
-  if (kStageSH) stage_sh_rows(io.sh, prm.P, row, s_sh);
+  extern __shared__ float4 s_sh4[];
+  float* __restrict__ s_sh = reinterpret_cast<float*>(s_sh4);
+  const int row = kRow > 0 ? kRow : prm.max_sh_coeffs * 3;
+  if constexpr (kRow > 0) stage_sh_rows<kRow>(io.sh, prm.P, s_sh);
   const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= prm.P) return;
   const size_t I = (size_t)i;
@@ -188,7 +233,7 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
           const float len = __builtin_sqrtf(v0 * v0 + v1 * v1 + v2 * v2);
           const float x = v0 / len, y = v1 / len, z = v2 / len;
           const float* __restrict__ s =
-              kStageSH ? s_sh + threadIdx.x * row : io.sh + I * (size_t)row;
+              kRow > 0 ? s_sh + threadIdx.x * kRow : io.sh + I * (size_t)row;
           const float* __restrict__ d = io.dc + 3 * I;
           const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
 #pragma unroll
@@ -244,23 +289,27 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   }
 }
 
-template <bool kStageSH>
+// kRow as in preprocess_fwd_kernel. Staged, the SH coefficients are copied
+// into registers so the LDS rows can be reused for the gradient rows, which
+// leave as one coalesced block store at the end.
+template <int kRow>
 __global__ void __launch_bounds__(256)
 preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_io io,
                       float focal_x, float focal_y) {
-  extern __shared__ float s_sh[];
-  const int msh = prm.max_sh_coeffs;
-  const int row = msh * 3;
-  if (kStageSH) stage_sh_rows(io.sh, prm.P, row, s_sh);
+  extern __shared__ float4 s_sh4[];
+  float* __restrict__ s_sh = reinterpret_cast<float*>(s_sh4);
+  constexpr bool kStaged = kRow > 0;
+  const int msh = kStaged ? kRow / 3 : prm.max_sh_coeffs;
+  if constexpr (kStaged) stage_sh_rows<kRow>(io.sh, prm.P, s_sh);
   const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   const bool valid = i < prm.P;
   const size_t I = valid ? (size_t)i : 0;
-  // SH coefficients in registers, so the LDS rows can be reused for the
-  // gradient rows (written back coalesced at the end)
   float shv[45];
-  if (kStageSH) {
+  float dsv[45];
 #pragma unroll
-    for (int k = 0; k < 45; ++k) shv[k] = (k < row) ? s_sh[threadIdx.x * row + k] : 0.0f;
+  for (int k = 0; k < 45; ++k) {
+    shv[k] = (kStaged && k < kRow) ? s_sh[threadIdx.x * kRow + k] : 0.0f;
+    dsv[k] = 0.0f;
   }
   float dm[3] = {0.f, 0.f, 0.f};
   float ddc[3] = {0.f, 0.f, 0.f};
@@ -269,10 +318,7 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
   float dsc[3] = {0.f, 0.f, 0.f};
   float dq[4] = {0.f, 0.f, 0.f, 0.f};
   float4 dvsp = make_float4(0.f, 0.f, 0.f, 0.f);
-  float dsv[45];
-#pragma unroll
-  for (int k = 0; k < 45; ++k) dsv[k] = 0.0f;
-  float* __restrict__ ds = kStageSH ? dsv : (io.dL_dsh ? io.dL_dsh + I * (size_t)msh * 3 : nullptr);
+  float* __restrict__ ds = kStaged ? dsv : (io.dL_dsh ? io.dL_dsh + I * (size_t)msh * 3 : nullptr);
   int sh_written = 0;  // number of rest coefficients written below
   if (valid && io.radii[I] > 0) {
     const float px = io.means3d[3 * I + 0], py = io.means3d[3 * I + 1], pz = io.means3d[3 * I + 2];
@@ -388,7 +434,7 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
         const float d0 = px - io.campos[0], d1 = py - io.campos[1], d2 = pz - io.campos[2];
         const float len = __builtin_sqrtf(d0 * d0 + d1 * d1 + d2 * d2);
         const float x = d0 / len, y = d1 / len, z = d2 / len;
-        const float* __restrict__ s = kStageSH ? shv : io.sh + I * (size_t)msh * 3;
+        const float* __restrict__ s = kStaged ? shv : io.sh + I * (size_t)msh * 3;
         float dRGBdx[3], dRGBdy[3], dRGBdz[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
@@ -510,17 +556,12 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
     }
     if (io.dL_dviewspace_out) dvsp = *reinterpret_cast<const float4*>(io.dL_dviewspace_out + 4 * I);
   }
-  if (kStageSH) {
-    // gradient rows through LDS, then one coalesced block store
+  if constexpr (kStaged) {
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 45; ++k)
-      if (k < row) s_sh[threadIdx.x * row + k] = dsv[k];
+    for (int k = 0; k < kRow; ++k) s_sh[threadIdx.x * kRow + k] = dsv[k];
     __syncthreads();
-    const int b0 = (int)blockIdx.x * 256;
-    const int nb = (prm.P - b0) < 256 ? (prm.P - b0) : 256;
-    float* __restrict__ dst = io.dL_dsh + (size_t)b0 * row;
-    for (int e = (int)threadIdx.x; e < nb * row; e += 256) dst[e] = s_sh[e];
+    store_sh_rows<kRow>(s_sh, prm.P, io.dL_dsh);
   }
   if (!valid) return;
   // Write every element of every gradient row.
@@ -539,7 +580,7 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
   if (io.dL_drotations)
     *reinterpret_cast<float4*>(io.dL_drotations + 4 * I) = make_float4(dq[0], dq[1], dq[2], dq[3]);
   *reinterpret_cast<float4*>(io.dL_dviewspace_in + 4 * I) = dvsp;
-  if (!kStageSH && ds) {
+  if (!kStaged && ds) {
     for (int k = sh_written * 3; k < msh * 3; ++k) ds[k] = 0.0f;
   }
 }
@@ -548,11 +589,16 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
 
 using namespace fgs;
 
-// SH rows are staged through LDS when the SH colour path is active and a row
-// has at most 15 rest coefficients (45 floats: 45 KB of LDS per workgroup).
-static bool stage_sh(const fgs_preprocess_params* p) {
-  return !p->use_colors_precomp && p->degree > 0 && p->max_sh_coeffs > 0 &&
-         p->max_sh_coeffs <= 15;
+// Row length (floats) of the LDS-staged SH path, or 0 for direct reads. Rows
+// are staged when the SH colour path is active, the row is one of the three
+// sizes of degrees 1-3 with 3, 8 or 15 rest coefficients (at most 45 floats:
+// 45 KB of LDS per workgroup) and the arrays are 16-byte aligned.
+// (The forward passes sh as both arrays.)
+static int staged_sh_row(const fgs_preprocess_params* p, const float* sh, const float* dsh) {
+  if (p->use_colors_precomp || p->degree <= 0 || !sh || !dsh) return 0;
+  if ((reinterpret_cast<uintptr_t>(sh) | reinterpret_cast<uintptr_t>(dsh)) & 15u) return 0;
+  const int m = p->max_sh_coeffs;
+  return (m == 3 || m == 8 || m == 15) ? 3 * m : 0;
 }
 
 extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
@@ -579,11 +625,26 @@ extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
   const float fx = (float)p->image_width / (2.0f * p->tan_fovx);
   const float fy = (float)p->image_height / (2.0f * p->tan_fovy);
   const unsigned blocks = (unsigned)((p->P + 255) / 256);
-  // The forward reads SH rows only for visible Gaussians, directly: staging
-  // every row of the block through LDS measured slower (more bytes, lower
-  // occupancy) than the strided reads, which the L2 serves.
-  hipLaunchKernelGGL(preprocess_fwd_kernel<false>, dim3(blocks), dim3(256), 0,
-                     (hipStream_t)stream, *p, *io, fx, fy);
+  // Staging moves every row of the block, visible or not, but as coalesced
+  // 16-byte loads; the direct path reads 4-byte elements 180 bytes apart.
+  const hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(blocks), block(256);
+  switch (staged_sh_row(p, io->sh, io->sh)) {
+    case 9:
+      hipLaunchKernelGGL(preprocess_fwd_kernel<9>, grid, block, 256 * 9 * sizeof(float), st, *p,
+                         *io, fx, fy);
+      break;
+    case 24:
+      hipLaunchKernelGGL(preprocess_fwd_kernel<24>, grid, block, 256 * 24 * sizeof(float), st,
+                         *p, *io, fx, fy);
+      break;
+    case 45:
+      hipLaunchKernelGGL(preprocess_fwd_kernel<45>, grid, block, 256 * 45 * sizeof(float), st,
+                         *p, *io, fx, fy);
+      break;
+    default:
+      hipLaunchKernelGGL(preprocess_fwd_kernel<0>, grid, block, 0, st, *p, *io, fx, fy);
+  }
   return check_launch("preprocess_fwd_kernel");
 }
 
@@ -603,13 +664,23 @@ extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
   const float fx = 0.5f * (float)p->image_width / fmaxf(p->tan_fovx, 1e-6f);
   const float fy = 0.5f * (float)p->image_height / fmaxf(p->tan_fovy, 1e-6f);
   const unsigned blocks = (unsigned)((p->P + 255) / 256);
-  if (stage_sh(p) && io->dL_dsh) {
-    const size_t lds = (size_t)256 * p->max_sh_coeffs * 3 * sizeof(float);
-    hipLaunchKernelGGL(preprocess_bwd_kernel<true>, dim3(blocks), dim3(256), lds,
-                       (hipStream_t)stream, *p, *io, fx, fy);
-  } else {
-    hipLaunchKernelGGL(preprocess_bwd_kernel<false>, dim3(blocks), dim3(256), 0,
-                       (hipStream_t)stream, *p, *io, fx, fy);
+  const hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(blocks), block(256);
+  switch (staged_sh_row(p, io->sh, io->dL_dsh)) {
+    case 9:
+      hipLaunchKernelGGL(preprocess_bwd_kernel<9>, grid, block, 256 * 9 * sizeof(float), st, *p,
+                         *io, fx, fy);
+      break;
+    case 24:
+      hipLaunchKernelGGL(preprocess_bwd_kernel<24>, grid, block, 256 * 24 * sizeof(float), st,
+                         *p, *io, fx, fy);
+      break;
+    case 45:
+      hipLaunchKernelGGL(preprocess_bwd_kernel<45>, grid, block, 256 * 45 * sizeof(float), st,
+                         *p, *io, fx, fy);
+      break;
+    default:
+      hipLaunchKernelGGL(preprocess_bwd_kernel<0>, grid, block, 0, st, *p, *io, fx, fy);
   }
   return check_launch("preprocess_bwd_kernel");
 }
