@@ -109,12 +109,15 @@ def ssim(torch, F, img, tgt, win):
 
 
 class StageTimer:
-    """Event pairs recorded on the launch stream around each C-ABI stage."""
+    """Event pairs recorded on the launch stream around each C-ABI stage.
+    A stage entered more than once in one step (binning: the depth order, then
+    the rest) is reported as the sum of its intervals in that step."""
 
     def __init__(self, torch):
         self.torch = torch
         self.open = {}
         self.done = []
+        self.step_index = 0
 
     def begin(self, name):
         e = self.torch.cuda.Event(enable_timing=True)
@@ -124,15 +127,20 @@ class StageTimer:
     def end(self, name):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
-        self.done.append((name, self.open.pop(name), e))
+        self.done.append((self.step_index, name, self.open.pop(name), e))
+
+    def mark_step(self):
+        self.step_index += 1
 
     def collect(self):
+        """{stage: [ms per step]}"""
         self.torch.cuda.synchronize()
-        out = {}
-        for name, a, b in self.done:
-            out.setdefault(name, []).append(a.elapsed_time(b))
+        acc = {}
+        for step, name, a, b in self.done:
+            per_step = acc.setdefault(name, {})
+            per_step[step] = per_step.get(step, 0.0) + a.elapsed_time(b)
         self.done = []
-        return out
+        return {name: list(v.values()) for name, v in acc.items()}
 
 
 # ---------------------------------------------------------------------------
@@ -333,6 +341,7 @@ def main():
         stats = []
         for i in range(len(cam_t)):
             out = step(i)
+            timer.mark_step()
             nc = out["img_n_contrib"]
             stats.append((out["rendered"], out["num_buckets"], int((out["radii"] > 0).sum()),
                           int(nc.to(torch.int64).sum()) if nc.numel() else 0))

@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class PreprocessParams(Structure):
@@ -53,7 +53,7 @@ class BinningIO(Structure):
         ("mult", c_float),
     ] + [(n, c_void_p) for n in (
         "xys", "depths", "conic_opacity", "tiles_touched", "point_list_keys", "point_list",
-        "ranges", "bucket_count", "bucket_offsets", "workspace")]
+        "ranges", "bucket_count", "bucket_offsets", "workspace", "depth_order")]
 
 
 class RasterParams(Structure):
@@ -97,6 +97,8 @@ SIGNATURES = {
     "fgs_tile_ranges": (c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p]),
     "fgs_binning_workspace_bytes": (c_size_t, [c_int32, c_int64, c_int32]),
     "fgs_binning_sorted": (c_int32, [POINTER(BinningIO), c_void_p]),
+    "fgs_depth_order_workspace_bytes": (c_size_t, [c_int32]),
+    "fgs_depth_order": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fgs_rasterize_fwd": (c_int32, [POINTER(RasterParams), POINTER(RasterFwdIO), c_void_p]),
     "fgs_rasterize_bwd": (c_int32, [POINTER(RasterParams), POINTER(RasterBwdIO), c_void_p]),
     "fgs_fill_u32": (c_int32, [c_void_p, c_uint32, c_int64, c_void_p]),

@@ -1136,21 +1136,44 @@ static int bits_for(int64_t count) {
   return b;
 }
 
-struct BinningLayout {
-  size_t dkeys, dkeys_s, order, cnt, scanP, sortP, tkeys, tvals, tkeys_s, sortK, total;
+static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Depth-order state (depth keys, sorted keys, the order and the sort's own
+// state): a depth workspace, and the first part of every binning workspace.
+struct DepthLayout {
+  size_t dkeys, dkeys_s, order, sort, total;
 };
 
-static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+static DepthLayout depth_layout(int32_t P) {
+  DepthLayout D;
+  size_t o = 0;
+  D.dkeys = o; o += al((size_t)P * 4);
+  D.dkeys_s = o; o += al((size_t)P * 4);
+  D.order = o; o += al((size_t)P * 4);
+  D.sort = o; o += sort_ws_bytes<uint32_t>(P, 4);
+  D.total = o;
+  return D;
+}
+
+// The P Gaussians by depth bits, culled ones last (keys made inside the
+// histogram kernel); the order lands at D.order of dws.
+static int32_t run_depth_order(int32_t P, const float* depths, const uint32_t* tiles_touched,
+                               char* dws, hipStream_t st) {
+  const DepthLayout D = depth_layout(P);
+  return radix_sort_pairs<uint32_t, true>(nullptr, nullptr, (uint32_t*)(dws + D.dkeys_s),
+                                          (uint32_t*)(dws + D.order), P, 0, 32, dws + D.sort, st,
+                                          depths, tiles_touched, (uint32_t*)(dws + D.dkeys));
+}
+
+struct BinningLayout {
+  size_t cnt, scanP, tkeys, tvals, tkeys_s, sortK, total;
+};
 
 static BinningLayout binning_layout(int32_t P, int64_t K, int32_t T) {
   BinningLayout L;
-  size_t o = 0;
-  L.dkeys = o; o += al((size_t)P * 4);
-  L.dkeys_s = o; o += al((size_t)P * 4);
-  L.order = o; o += al((size_t)P * 4);
+  size_t o = depth_layout(P).total;
   L.cnt = o; o += al((size_t)P * 4);
   L.scanP = o; o += scan_ws_bytes(P);
-  L.sortP = o; o += sort_ws_bytes<uint32_t>(P, 4);
   L.tkeys = o; o += al((size_t)K * 4);
   L.tvals = o; o += al((size_t)K * 4);
   L.tkeys_s = o; o += al((size_t)K * 4);
@@ -1161,8 +1184,8 @@ static BinningLayout binning_layout(int32_t P, int64_t K, int32_t T) {
 
 // Workspace of the two-level path (sized for kMaxSt super-tiles).
 struct TwoLevelLayout {
-  size_t dkeys, dkeys_s, order, sortP, sets, cnt1, segsum, st_start, chunk_first, nchunks,
-      chunk_st, list, list_st, masks, cnt2, base2, tile_total, tile_start, total;
+  size_t sets, cnt1, segsum, st_start, chunk_first, nchunks, chunk_st, list, list_st, masks, cnt2,
+      base2, tile_total, tile_start, total;
   int64_t max_chunks;
 };
 
@@ -1170,11 +1193,7 @@ static TwoLevelLayout two_level_layout(int32_t P, int64_t K, int32_t T) {
   TwoLevelLayout L;
   const int64_t nwg1 = (P + kL1Group - 1) / kL1Group;
   L.max_chunks = K / kL2Chunk + kMaxSt + 1;
-  size_t o = 0;
-  L.dkeys = o; o += al((size_t)P * 4);
-  L.dkeys_s = o; o += al((size_t)P * 4);
-  L.order = o; o += al((size_t)P * 4);
-  L.sortP = o; o += sort_ws_bytes<uint32_t>(P, 4);
+  size_t o = depth_layout(P).total;
   L.sets = o; o += al((size_t)P * 32);
   L.cnt1 = o; o += al((size_t)nwg1 * kMaxSt * 4);
   L.segsum = o; o += al((size_t)kL1Segs * kMaxSt * 4);
@@ -1282,6 +1301,22 @@ extern "C" size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, i
   return a > b ? a : b;
 }
 
+extern "C" size_t fgs_depth_order_workspace_bytes(int32_t P) {
+  return depth_layout(P < 1 ? 1 : P).total;
+}
+
+extern "C" int32_t fgs_depth_order(int32_t P, const float* depths, const uint32_t* tiles_touched,
+                                   void* depth_workspace, void* stream) {
+  if (P < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_depth_order: P < 0");
+  if (P == 0) return FGS_OK;
+  if (!depths || !tiles_touched || !depth_workspace)
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_depth_order: null pointer");
+  const int32_t e = run_depth_order(P, depths, tiles_touched, (char*)depth_workspace,
+                                    (hipStream_t)stream);
+  if (e != FGS_OK) return e;
+  return check_launch("depth_order");
+}
+
 extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
   if (!io) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null io");
   const int32_t P = io->P;
@@ -1296,15 +1331,22 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
   hipStream_t st = (hipStream_t)stream;
   const StGrid sg = st_grid(io->grid_x, io->grid_y);
-  if (K > 0 && P > 0 && use_two_level(sg, K)) {
+  char* ws = (char*)io->workspace;
+  // Gaussians by depth bits: from the caller's depth workspace, or sorted here
+  // into the front of the binning workspace
+  const char* dws = io->depth_order ? (const char*)io->depth_order : ws;
+  const uint32_t* order = (const uint32_t*)(dws + depth_layout(P).order);
+  if (K > 0 && P > 0) {
     if (!io->xys || !io->depths || !io->conic_opacity || !io->tiles_touched ||
         !io->point_list_keys || !io->point_list)
       return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
+    if (!io->depth_order) {
+      const int32_t e = run_depth_order(P, io->depths, io->tiles_touched, ws, st);
+      if (e != FGS_OK) return e;
+    }
+  }
+  if (K > 0 && P > 0 && use_two_level(sg, K)) {
     const TwoLevelLayout L = two_level_layout(P, K, T);
-    char* ws = (char*)io->workspace;
-    uint32_t* dkeys = (uint32_t*)(ws + L.dkeys);
-    uint32_t* dkeys_s = (uint32_t*)(ws + L.dkeys_s);
-    uint32_t* order = (uint32_t*)(ws + L.order);
     uint64_t* sets = (uint64_t*)(ws + L.sets);
     uint32_t* cnt1 = (uint32_t*)(ws + L.cnt1);
     uint32_t* segsum = (uint32_t*)(ws + L.segsum);
@@ -1319,11 +1361,6 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     uint32_t* base2 = (uint32_t*)(ws + L.base2);
     uint32_t* tile_total = (uint32_t*)(ws + L.tile_total);
     uint32_t* tile_start = (uint32_t*)(ws + L.tile_start);
-    // Gaussians by depth bits (keys made inside the histogram kernel)
-    int32_t e = radix_sort_pairs<uint32_t, true>(nullptr, nullptr, dkeys_s, order, P, 0, 32,
-                                                 ws + L.sortP, st, io->depths, io->tiles_touched,
-                                                 dkeys);
-    if (e != FGS_OK) return e;
     const unsigned nwg1 = ceil_div_u(P, kL1Group);
     hipLaunchKernelGGL(l1_count_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, io->mult, order,
                        io->xys, io->conic_opacity, io->tiles_touched, sets, cnt1);
@@ -1348,10 +1385,6 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     return check_launch("binning_sorted (two-level)");
   }
   const BinningLayout L = binning_layout(P < 1 ? 1 : P, K < 1 ? 1 : K, T);
-  char* ws = (char*)io->workspace;
-  uint32_t* dkeys = (uint32_t*)(ws + L.dkeys);
-  uint32_t* dkeys_s = (uint32_t*)(ws + L.dkeys_s);
-  uint32_t* order = (uint32_t*)(ws + L.order);
   uint32_t* cnt = (uint32_t*)(ws + L.cnt);
   uint32_t* tkeys = (uint32_t*)(ws + L.tkeys);
   uint32_t* tvals = (uint32_t*)(ws + L.tvals);
@@ -1362,13 +1395,8 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
         !io->point_list_keys || !io->point_list)
       return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
     const unsigned gP = ceil_div_u(P, 256);
-    // stage 1: Gaussians by depth bits (keys made inside the histogram kernel)
-    int32_t e = radix_sort_pairs<uint32_t, true>(nullptr, nullptr, dkeys_s, order, P, 0, 32,
-                                                 ws + L.sortP, st, io->depths, io->tiles_touched,
-                                                 dkeys);
-    if (e != FGS_OK) return e;
     // duplicate offsets in depth order: exclusive scan of tiles_touched[order[i]]
-    e = launch_chained_scan<true>(io->tiles_touched, order, P, cnt, P, ws + L.scanP, false, false,
+    int32_t e = launch_chained_scan<true>(io->tiles_touched, order, P, cnt, P, ws + L.scanP, false, false,
                                   st);
     if (e != FGS_OK) return e;
     hipLaunchKernelGGL(duplicate_sorted_kernel, dim3(gP), dim3(256), 0, st, P, order, cnt, io->xys,

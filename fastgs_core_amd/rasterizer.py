@@ -189,6 +189,8 @@ class _Preprocess(torch.autograd.Function):
         ctx.save_for_backward(means3d, sh, scales, rotations, cov3d_precomp, viewmatrix,
                               projmatrix, campos, cov3d, radii, clamped)
         ctx.mark_non_differentiable(radii, tiles, clamped)
+        # outputs the loss does not reach arrive as None (no zero tensors)
+        ctx.set_materialize_grads(False)
         return radii, xys, depths, cov3d, rgb, conic, tiles, clamped, vsp_out
 
     @staticmethod
@@ -275,6 +277,7 @@ class _Rasterize(torch.autograd.Function):
                               final_t, n_contrib, max_contrib)
         ctx.mark_non_differentiable(bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib,
                                     max_contrib, mc)
+        ctx.set_materialize_grads(False)
         return (bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib, max_contrib,
                 pixel_colors, out_color, mc)
 
@@ -323,7 +326,8 @@ def _inclusive_scan_i32(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: float):
+def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: float,
+                    depth_ws: Optional[torch.Tensor] = None):
     lib = _lib.load()
     dev = xys.device
     P = xys.shape[0]
@@ -335,7 +339,8 @@ def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: f
     bucket_offsets = torch.empty(T, dtype=torch.int32, device=dev)
     ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
     io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
-                        _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws))
+                        _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws),
+                        _p(depth_ws))
     with _stage("binning"):
         _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
     return keys, plist, ranges, bucket_count, bucket_offsets
@@ -346,6 +351,39 @@ def _last_u32(t: torch.Tensor) -> int:
     if t.numel() == 0:
         return 0
     return int(t[-1].item()) & 0xFFFFFFFF
+
+
+def _last_u32_async(t: torch.Tensor):
+    """read_last_u32 split in two: the 4-byte copy to pinned host memory and an
+    event are queued now, the value is read by _wait_u32. Work queued in
+    between runs on the GPU while the host waits."""
+    host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    host.copy_(t[-1:], non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(t.device))
+    return host, ev
+
+
+def _wait_u32(pending) -> int:
+    host, ev = pending
+    ev.synchronize()
+    return int(host[0]) & 0xFFFFFFFF
+
+
+def _count_and_depth_order(point_offsets, depths, tiles):
+    """K = point_offsets[P-1] (binding.cpp:153-154) and the depth order of the
+    Gaussians, the first stage of the binning. The depth sort needs only P, so
+    it is queued between the copy of K and the wait for it."""
+    P = tiles.numel()
+    if P == 0:
+        return 0, None
+    lib = _lib.load()
+    dev = tiles.device
+    pending = _last_u32_async(point_offsets)
+    dws = torch.empty(int(lib.fgs_depth_order_workspace_bytes(P)), dtype=torch.uint8, device=dev)
+    with _stage("binning"):
+        _lib.check(lib.fgs_depth_order(P, _p(depths), _p(tiles), _p(dws), _stream(dev)))
+    return _wait_u32(pending), dws
 
 
 # ---------------------------------------------------------------------------
@@ -454,7 +492,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     gx, gy = cfg["gx"], cfg["gy"]
     T = gx * gy
     point_offsets = _inclusive_scan_i32(tiles)
-    K = _last_u32(point_offsets)
+    K, depth_ws = _count_and_depth_order(point_offsets, depths.detach(), tiles)
     i32 = dict(dtype=torch.int32, device=dev)
     f32 = dict(dtype=torch.float32, device=dev)
     point_list_keys = torch.zeros(0, dtype=torch.int64, device=dev)
@@ -475,18 +513,31 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     if K > 0:
         with torch.no_grad():
             point_list_keys, point_list, ranges, bucket_count, bucket_offsets = _binning_sorted(
-                xys.detach(), depths.detach(), conic.detach(), tiles, K, gx, gy, float(mult))
-        B = _last_u32(bucket_offsets)
+                xys.detach(), depths.detach(), conic.detach(), tiles, K, gx, gy, float(mult),
+                depth_ws)
+        ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
+        if ws:
+            # the sampled state is B * 256 entries: B is needed before the launch
+            B = _last_u32(bucket_offsets)
+            pending_b = None
+        else:
+            # B = sum over tiles of ceil(n_t / 32) <= (K + 31 T) / 32: bucket_to_tile
+            # is sized by that bound and cut to B once the value arrives, which
+            # is waited for after the rasterize launch
+            pending_b = _last_u32_async(bucket_offsets)
+            B = (K + 31 * T) // 32
         if B > 0:
             background = _to(inputs["background"], dev, torch.float32)
             metric_map = _to(inputs["metric_map"], dev, torch.int32)
-            ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
             rcfg = dict(W=cfg["W"], H=cfg["H"], C=3, T=T, B=B, get_flag=bool(get_flag),
                         write_sampled=ws)
             (bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib, max_contrib,
              pixel_colors, out_color, metric_count) = _Rasterize.apply(
                 rcfg, ranges, point_list, bucket_offsets, xys, rgb, conic, background, radii,
                 metric_map, metric_count, vsp_out)
+        if pending_b is not None:
+            B = _wait_u32(pending_b)
+            bucket_to_tile = bucket_to_tile[:B]
     return {
         "rendered": K, "num_buckets": B, "out_color": out_color, "radii": radii,
         "point_offsets": point_offsets, "ranges": ranges, "bucket_count": bucket_count,

@@ -192,10 +192,26 @@ typedef struct {
   uint32_t* bucket_count;     /* [T] */
   uint32_t* bucket_offsets;   /* [T] inclusive */
   void* workspace;            /* fgs_binning_workspace_bytes(P, K, T) */
+  /* NULL (the Gaussians are sorted by depth here), or the depth workspace of
+   * an fgs_depth_order call on the same P, depths and tiles_touched that is
+   * ordered before this call (same stream, or an event). */
+  const void* depth_order;
 } fgs_binning_io;
 
 size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, int32_t num_tiles);
 int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream);
+
+/* The first stage of fgs_binning_sorted on its own: the P Gaussians ordered
+ * by depth bits (stable; culled ones, tiles_touched == 0, last).  It needs
+ * only P, so a caller can enqueue it before the blocking read of
+ * K = point_offsets[P-1] (binding.cpp:25-31,153-154) and the GPU sorts while
+ * the host waits; the result is passed as fgs_binning_io.depth_order.  No
+ * reference counterpart of its own: it is the depth half of the argsort at
+ * binding.cpp:195-197.  depth_workspace: fgs_depth_order_workspace_bytes(P),
+ * 256-byte aligned, no initial contents required. */
+size_t fgs_depth_order_workspace_bytes(int32_t P);
+int32_t fgs_depth_order(int32_t P, const float* depths, const uint32_t* tiles_touched,
+                        void* depth_workspace, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Rasterize.                                                                */

@@ -119,32 +119,44 @@ def test_metric_count_parity(oracle):
     assert int(ref["metric_count"].sum()) > 0
 
 
-@pytest.mark.parametrize("case", ["cfg1", "sh3", "bg"])
+@pytest.mark.parametrize("case", ["cfg1", "sh3", "bg", "sh1", "sh3_deg1", "sh_rows10"])
 def test_backward_parity(oracle, case):
+    """Gradients of every input against the oracle. The SH cases cover each
+    LDS-staged row length (3, 8 and 15 rest coefficients), a degree below the
+    buffer's (progressive SH training) and a row of 10 coefficients, which the
+    library reads directly instead of staging."""
     import fastgs_core
     import torch
 
+    bg = (0.0, 0.0, 0.0)
     if case == "cfg1":
         sc = syn.scene_config1(1, 3000)
         cam = syn.config1_camera(80, 64)
-        bg = (0.0, 0.0, 0.0)
     elif case == "sh3":
         sc, cam = scene_small(4, 2500, 3, 128, 96)
-        bg = (0.0, 0.0, 0.0)
+    elif case == "sh1":
+        sc, cam = scene_small(12, 2000, 1, 96, 80)
+    elif case == "sh3_deg1":
+        sc, cam = scene_small(13, 2000, 3, 96, 80)
+    elif case == "sh_rows10":
+        sc, cam = scene_small(14, 1999, 3, 112, 80)
+        sc["sh"] = np.ascontiguousarray(sc["sh"][:, :10])
+        sc["degree"] = 2
     else:
         sc, cam = scene_small(5, 2000, 2, 96, 112)
         bg = (0.2, 0.5, 0.9)
+    degree = 1 if case == "sh3_deg1" else sc["degree"]
     _say("backward", case)
     inp = syn.make_inputs(sc, cam, background=bg)
-    ref = oracle.render(inp, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, sc["degree"])
+    ref = oracle.render(inp, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, degree)
     rng = np.random.default_rng(11)
     dL = rng.standard_normal((3, cam.width * cam.height)).astype(np.float32)
     rg = oracle.render_backward(inp, ref, dL, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy,
-                                sc["degree"])
+                                degree)
     req = ("means3d", "scales", "rotations", "opacities", "dc", "sh", "viewspace_points")
     tin = to_torch(inp, requires_grad=req)
     out = fastgs_core.rasterize_gaussians(tin, cam.width, cam.height, 16, 16, cam.tan_fovx,
-                                          cam.tan_fovy, sc["degree"])
+                                          cam.tan_fovy, degree)
     loss = (out["out_color"] * torch.from_numpy(dL).cuda()).sum()
     loss.backward()
     for k, rk in (("means3d", "means3d"), ("scales", "scales"), ("rotations", "rotations"),
