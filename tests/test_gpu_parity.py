@@ -284,6 +284,48 @@ def test_binning_forward_matches_oracle(oracle):
     np.testing.assert_array_equal(to_np(tp["bucket_count"]).view(np.uint32), ref["bucket_count"])
 
 
+@pytest.mark.parametrize("grid", ["two_level", "one_level"])
+def test_binning_sorted_depth_order_entry(oracle, grid):
+    """fgs_binning_sorted with the depth order sorted inside the call
+    (depth_order NULL) and with it from a separate fgs_depth_order call: both
+    give the oracle's sorted keys, values, ranges and bucket arrays bit for
+    bit, on a grid of at most 256 super-tiles (two-level binning) and on one
+    of 578 (the one-level fallback)."""
+    import torch
+
+    from fastgs_core_amd import _lib, rasterizer
+
+    if grid == "two_level":
+        sc, cam = scene_small(15, 2500, 0, 320, 176)
+    else:
+        sc, cam = scene_small(9, 2000, 0, 4352, 2176)
+    _say("binning_sorted depth order", grid)
+    inp = syn.make_inputs(sc, cam)
+    ref = oracle.render(inp, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, 0)
+    K = int(ref["rendered"])
+    assert K > 0
+    gx, gy = (cam.width + 15) // 16, (cam.height + 15) // 16
+    dev = torch.device("cuda")
+    g = {k: torch.from_numpy(np.ascontiguousarray(ref[k])).to(dev)
+         for k in ("geom_means2d", "geom_depths", "geom_conic_opacity")}
+    tiles = torch.from_numpy(ref["geom_tiles_touched"].view(np.int32)).to(dev)
+    P = tiles.numel()
+    lib = _lib.load()
+    dws = torch.empty(int(lib.fgs_depth_order_workspace_bytes(P)), dtype=torch.uint8, device=dev)
+    _lib.check(lib.fgs_depth_order(P, g["geom_depths"].data_ptr(), tiles.data_ptr(),
+                                   dws.data_ptr(), rasterizer._stream(dev)))
+    for depth_ws in (None, dws):
+        keys, plist, ranges, bcount, boffs = rasterizer._binning_sorted(
+            g["geom_means2d"], g["geom_depths"], g["geom_conic_opacity"], tiles, K, gx, gy, 1.0,
+            depth_ws)
+        np.testing.assert_array_equal(to_np(keys).view(np.uint64), ref["point_list_keys"])
+        np.testing.assert_array_equal(to_np(plist).view(np.uint32), ref["point_list"])
+        np.testing.assert_array_equal(to_np(ranges).view(np.uint32).reshape(-1, 2),
+                                      np.asarray(ref["ranges"]).reshape(-1, 2))
+        np.testing.assert_array_equal(to_np(bcount).view(np.uint32), ref["bucket_count"])
+        np.testing.assert_array_equal(to_np(boffs).view(np.uint32), ref["bucket_offsets"])
+
+
 def test_empty_scene():
     import fastgs_core
 
