@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class PreprocessParams(Structure):
@@ -35,7 +35,8 @@ class PreprocessFwdIO(Structure):
     _fields_ = [(n, c_void_p) for n in (
         "means3d", "dc", "sh", "colors_precomp", "opacities", "scales", "rotations",
         "cov3d_precomp", "viewmatrix", "projmatrix", "campos", "viewspace_in", "radii", "xys",
-        "depths", "cov3d", "rgb", "conic_opacity", "tiles_touched", "clamped", "viewspace_out")]
+        "depths", "cov3d", "rgb", "conic_opacity", "tiles_touched", "clamped", "viewspace_out",
+        "st_base", "st_masks")]
 
 
 class PreprocessBwdIO(Structure):
@@ -53,7 +54,8 @@ class BinningIO(Structure):
         ("mult", c_float),
     ] + [(n, c_void_p) for n in (
         "xys", "depths", "conic_opacity", "tiles_touched", "point_list_keys", "point_list",
-        "ranges", "bucket_count", "bucket_offsets", "workspace", "depth_order")]
+        "ranges", "bucket_count", "bucket_offsets", "workspace", "depth_order", "st_base",
+        "st_masks")]
 
 
 class RasterParams(Structure):

@@ -708,41 +708,76 @@ __device__ __forceinline__ bool st_has(const uint64_t (&m)[4], int s) {
   return (m[s >> 6] >> (s & 63)) & 1ull;
 }
 
-// Level 1a: per depth-ordered Gaussian its super-tile set (stored), and per
-// workgroup the number of its Gaussians touching each super-tile.
+// Super-tile of mask k of record word w; a record made for another grid can
+// give ids >= S, which both level-1 kernels skip.
+__device__ __forceinline__ int rec_st(uint32_t w, int k, const StGrid& sg) {
+  const int bx = (int)(w & 0xFFFu) + (k & 1), by = (int)((w >> 12) & 0xFFFu) + (k >> 1);
+  return (bx < sg.sgx && by < sg.sgy) ? by * sg.sgx + bx : kMaxSt;
+}
+
+// Level 1a: per depth-ordered Gaussian its super-tiles, and per workgroup
+// the number of its Gaussians touching each super-tile.  A Gaussian with a
+// preprocess record (st_base word != 0) takes its four super-tile masks from
+// it; any other walks its tiles into its 256-bit super-tile set.  Stored in
+// depth order for l1_place: recw[i] (the record word, 0 for a set) and
+// sets[4i..4i+3] (the masks, or the set).
 __global__ void __launch_bounds__(kL1Group)
 l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ order,
                 const float* __restrict__ xys, const float* __restrict__ conic_opacity,
-                const uint32_t* __restrict__ tiles_touched, uint64_t* __restrict__ sets,
-                uint32_t* __restrict__ cnt1) {
+                const uint32_t* __restrict__ tiles_touched, const uint32_t* __restrict__ st_base,
+                const uint64_t* __restrict__ st_masks, uint32_t* __restrict__ recw,
+                uint64_t* __restrict__ sets, uint32_t* __restrict__ cnt1) {
   __shared__ uint32_t s_cnt[kMaxSt];
   const int t = (int)threadIdx.x;
   const int i = (int)blockIdx.x * kL1Group + t;
   s_cnt[t] = 0;
-  EmitStSet e;
-  e.m[0] = e.m[1] = e.m[2] = e.m[3] = 0ull;
-  e.sgx = sg.sgx;
+  uint64_t m[4] = {0ull, 0ull, 0ull, 0ull};
+  uint32_t w = 0u;
   if (i < P) {
     const uint32_t g = order[i];
     if (g < (uint32_t)P && tiles_touched[g] != 0u) {
-      const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
-      const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
-      tiles_walk(xy.x, xy.y, co, sg.gx, sg.gy, mult, e);
+      w = st_base ? st_base[g] : 0u;
+      if (w != 0u) {
+        const uint4* src = reinterpret_cast<const uint4*>(st_masks + 4 * (size_t)g);
+        const uint4 a = src[0], b = src[1];
+        m[0] = (uint64_t)a.x | ((uint64_t)a.y << 32);
+        m[1] = (uint64_t)a.z | ((uint64_t)a.w << 32);
+        m[2] = (uint64_t)b.x | ((uint64_t)b.y << 32);
+        m[3] = (uint64_t)b.z | ((uint64_t)b.w << 32);
+      } else {
+        EmitStSet e;
+        e.m[0] = e.m[1] = e.m[2] = e.m[3] = 0ull;
+        e.sgx = sg.sgx;
+        const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
+        const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
+        tiles_walk(xy.x, xy.y, co, sg.gx, sg.gy, mult, e);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) m[k] = e.m[k];
+      }
     }
+    recw[i] = w;
     uint4* dst = reinterpret_cast<uint4*>(sets + 4 * (size_t)i);
-    dst[0] = make_uint4((uint32_t)e.m[0], (uint32_t)(e.m[0] >> 32), (uint32_t)e.m[1],
-                        (uint32_t)(e.m[1] >> 32));
-    dst[1] = make_uint4((uint32_t)e.m[2], (uint32_t)(e.m[2] >> 32), (uint32_t)e.m[3],
-                        (uint32_t)(e.m[3] >> 32));
+    dst[0] = make_uint4((uint32_t)m[0], (uint32_t)(m[0] >> 32), (uint32_t)m[1],
+                        (uint32_t)(m[1] >> 32));
+    dst[1] = make_uint4((uint32_t)m[2], (uint32_t)(m[2] >> 32), (uint32_t)m[3],
+                        (uint32_t)(m[3] >> 32));
   }
   __syncthreads();
+  if (w != 0u) {
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    uint64_t b = e.m[w];
-    while (b) {
-      const int k = __builtin_ctzll(b);
-      b &= b - 1ull;
-      atomicAdd(&s_cnt[64 * w + k], 1u);
+    for (int k = 0; k < 4; ++k) {
+      const int sid = rec_st(w, k, sg);
+      if (m[k] != 0ull && sid < sg.S) atomicAdd(&s_cnt[sid], 1u);
+    }
+  } else {
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd) {
+      uint64_t b = m[wd];
+      while (b) {
+        const int k = __builtin_ctzll(b);
+        b &= b - 1ull;
+        atomicAdd(&s_cnt[64 * wd + k], 1u);
+      }
     }
   }
   __syncthreads();
@@ -800,29 +835,34 @@ l1_top_scan_kernel(int S, uint32_t* __restrict__ segsum, uint32_t* __restrict__ 
   }
 }
 
-// Level 1d: each Gaussian written into the lists of its super-tiles.  The
-// workgroup's (Gaussian, super-tile) pairs are laid out in LDS in thread
-// order (a thread's super-tiles are distinct, so their order among
-// themselves is free) and ranked per super-tile in that order, 256 pairs at
-// a time: wave64 match-any over the 8 super-tile bits, then the four waves
-// through LDS counters, as in a radix pass.
+// Level 1d: each Gaussian written into the lists of its super-tiles, with
+// its 64-bit tile mask there.  The workgroup's (Gaussian, super-tile, mask)
+// triples are laid out in LDS in thread order (a thread's super-tiles are
+// distinct, so their order among themselves is free) and ranked per
+// super-tile in that order, 256 at a time: wave64 match-any over the 8
+// super-tile bits, then the four waves through LDS counters, as in a radix
+// pass.  The mask comes from the record, or, for a Gaussian without one, from
+// its walk clipped to the super-tile's window.
 constexpr int kL1Pairs = 2048;  // LDS pair capacity per round
 __global__ void __launch_bounds__(kL1Group)
-l1_place_kernel(int32_t P, int S, const uint32_t* __restrict__ order,
-                const uint64_t* __restrict__ sets, const uint32_t* __restrict__ cnt1,
-                const uint32_t* __restrict__ segsum, const uint32_t* __restrict__ st_start,
-                int64_t cap, uint32_t* __restrict__ list, uint8_t* __restrict__ list_st) {
-  __shared__ uint32_t s_ps[kL1Pairs];  // super-tile of each pair
+l1_place_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ order,
+                const uint32_t* __restrict__ recw, const uint64_t* __restrict__ sets,
+                const uint32_t* __restrict__ cnt1, const uint32_t* __restrict__ segsum,
+                const uint32_t* __restrict__ st_start, const float* __restrict__ xys,
+                const float* __restrict__ conic_opacity, int64_t cap,
+                uint32_t* __restrict__ list, uint64_t* __restrict__ masks) {
+  __shared__ uint64_t s_pm[kL1Pairs];  // mask of each pair (0: walk it)
   __shared__ uint32_t s_pg[kL1Pairs];  // Gaussian of each pair
+  __shared__ uint8_t s_ps[kL1Pairs];   // super-tile of each pair
   __shared__ uint32_t s_wh[kWavesPerBlock][kMaxSt];
   __shared__ uint32_t s_base[kMaxSt];
   __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
+  const int S = sg.S;
   const int t = (int)threadIdx.x;
   const int w = t / kWave;
-  const int lane = lane_id();
   const int i = (int)blockIdx.x * kL1Group + t;
   uint64_t m[4] = {0ull, 0ull, 0ull, 0ull};
-  uint32_t g = 0;
+  uint32_t g = 0, rw = 0;
   if (i < P) {
     const uint4* src = reinterpret_cast<const uint4*>(sets + 4 * (size_t)i);
     const uint4 a = src[0], b = src[1];
@@ -831,29 +871,51 @@ l1_place_kernel(int32_t P, int S, const uint32_t* __restrict__ order,
     m[2] = (uint64_t)b.x | ((uint64_t)b.y << 32);
     m[3] = (uint64_t)b.z | ((uint64_t)b.w << 32);
     g = order[i];
+    rw = recw[i];
   }
   const int rows = (int)((gridDim.x + kL1Segs - 1) / kL1Segs);
   const int seg = (int)blockIdx.x / rows;
   if (t < S)
     s_base[t] = st_start[t] + segsum[(size_t)seg * S + t] + cnt1[(size_t)blockIdx.x * S + t];
-  const uint32_t np = (uint32_t)(__popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]) + __popcll(m[3]));
+  uint32_t np = 0;
+  if (rw != 0u) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) np += (m[k] != 0ull && rec_st(rw, k, sg) < S) ? 1u : 0u;
+  } else {
+    np = (uint32_t)(__popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]) + __popcll(m[3]));
+  }
   uint32_t total;
   const uint32_t off = block_excl_scan(np, s_tmp, &total);  // has barriers
   const uint64_t lt = lanemask_lt();
   for (uint32_t r0 = 0; r0 < total; r0 += kL1Pairs) {
     // this round's pairs into LDS
     uint32_t p = off;
+    if (rw != 0u) {
 #pragma unroll
-    for (int wd = 0; wd < 4; ++wd) {
-      uint64_t b = m[wd];
-      while (b) {
-        const int k = __builtin_ctzll(b);
-        b &= b - 1ull;
+      for (int k = 0; k < 4; ++k) {
+        const int sid = rec_st(rw, k, sg);
+        if (m[k] == 0ull || sid >= S) continue;
         if (p >= r0 && p < r0 + kL1Pairs) {
-          s_ps[p - r0] = (uint32_t)(64 * wd + k);
+          s_ps[p - r0] = (uint8_t)sid;
           s_pg[p - r0] = g;
+          s_pm[p - r0] = m[k];
         }
         ++p;
+      }
+    } else {
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        uint64_t b = m[wd];
+        while (b) {
+          const int k = __builtin_ctzll(b);
+          b &= b - 1ull;
+          if (p >= r0 && p < r0 + kL1Pairs) {
+            s_ps[p - r0] = (uint8_t)(64 * wd + k);
+            s_pg[p - r0] = g;
+            s_pm[p - r0] = 0ull;
+          }
+          ++p;
+        }
       }
     }
     __syncthreads();
@@ -879,8 +941,21 @@ l1_place_kernel(int32_t P, int S, const uint32_t* __restrict__ order,
         uint32_t pos = s_base[d] + rk;
         for (int k = 0; k < w; ++k) pos += s_wh[k][d];
         if ((int64_t)pos < cap) {
-          list[pos] = s_pg[q];
-          list_st[pos] = (uint8_t)d;
+          const uint32_t gq = s_pg[q];
+          uint64_t mk = s_pm[q];
+          if (mk == 0ull && gq < (uint32_t)P) {
+            EmitTileMask em;
+            em.m = 0ull;
+            em.x0 = (int)(d % (uint32_t)sg.sgx) * kSt;
+            em.y0 = (int)(d / (uint32_t)sg.sgx) * kSt;
+            const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)gq);
+            const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)gq);
+            tiles_walk_window(xy.x, xy.y, co, sg.gx, sg.gy, mult, em.x0, em.x0 + kSt, em.y0,
+                              em.y0 + kSt, em);
+            mk = em.m;
+          }
+          list[pos] = gq;
+          masks[pos] = mk;
         }
       }
       __syncthreads();
@@ -917,31 +992,6 @@ __device__ __forceinline__ uint64_t transpose64(uint64_t row) {
     hi = up ? ((hi & ~m) | (rh >> d)) : ((hi & m) | (rh << d));
   }
   return (uint64_t)lo | ((uint64_t)hi << 32);
-}
-
-// Level 2a: per list entry (one thread each), its 64-bit tile mask inside
-// its super-tile (the walk clipped to the super-tile window).
-__global__ void __launch_bounds__(256)
-l2_mask_kernel(StGrid sg, float mult, const uint32_t* __restrict__ list,
-               const uint8_t* __restrict__ list_st, const uint32_t* __restrict__ st_start,
-               int32_t P, const float* __restrict__ xys, const float* __restrict__ conic_opacity,
-               int64_t cap, uint64_t* __restrict__ masks) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t k1 = (int64_t)st_start[sg.S] < cap ? (int64_t)st_start[sg.S] : cap;
-  if (e >= k1) return;
-  const uint32_t s = list_st[e];
-  const uint32_t g = list[e];
-  EmitTileMask em;
-  em.m = 0ull;
-  em.x0 = (int)(s % (uint32_t)sg.sgx) * kSt;
-  em.y0 = (int)(s / (uint32_t)sg.sgx) * kSt;
-  if (g < (uint32_t)P && s < (uint32_t)sg.S) {
-    const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
-    const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
-    tiles_walk_window(xy.x, xy.y, co, sg.gx, sg.gy, mult, em.x0, em.x0 + kSt, em.y0,
-                      em.y0 + kSt, em);
-  }
-  masks[e] = em.m;
 }
 
 // Level 2b: per chunk of 512 entries of one super-tile list (four
@@ -1184,7 +1234,7 @@ static BinningLayout binning_layout(int32_t P, int64_t K, int32_t T) {
 
 // Workspace of the two-level path (sized for kMaxSt super-tiles).
 struct TwoLevelLayout {
-  size_t sets, cnt1, segsum, st_start, chunk_first, nchunks, chunk_st, list, list_st, masks, cnt2,
+  size_t recw, sets, cnt1, segsum, st_start, chunk_first, nchunks, chunk_st, list, masks, cnt2,
       base2, tile_total, tile_start, total;
   int64_t max_chunks;
 };
@@ -1194,6 +1244,7 @@ static TwoLevelLayout two_level_layout(int32_t P, int64_t K, int32_t T) {
   const int64_t nwg1 = (P + kL1Group - 1) / kL1Group;
   L.max_chunks = K / kL2Chunk + kMaxSt + 1;
   size_t o = depth_layout(P).total;
+  L.recw = o; o += al((size_t)P * 4);
   L.sets = o; o += al((size_t)P * 32);
   L.cnt1 = o; o += al((size_t)nwg1 * kMaxSt * 4);
   L.segsum = o; o += al((size_t)kL1Segs * kMaxSt * 4);
@@ -1202,7 +1253,6 @@ static TwoLevelLayout two_level_layout(int32_t P, int64_t K, int32_t T) {
   L.nchunks = o; o += al(4);
   L.chunk_st = o; o += al((size_t)L.max_chunks * 4);
   L.list = o; o += al((size_t)K * 4);
-  L.list_st = o; o += al((size_t)K);
   L.masks = o; o += al((size_t)K * 8);
   L.cnt2 = o; o += al((size_t)L.max_chunks * kWave * 4);
   L.base2 = o; o += al((size_t)L.max_chunks * kWave * 4);
@@ -1329,6 +1379,10 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
   const int32_t T = (int32_t)T64;
   if (!io->ranges || !io->bucket_count || !io->bucket_offsets || !io->workspace)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
+  if (!io->st_base != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u))
+    return set_error(FGS_ERR_INVALID_ARGUMENT,
+                     "fgs_binning_sorted: st_base and st_masks must both be set (st_masks "
+                     "16-byte aligned) or both NULL");
   hipStream_t st = (hipStream_t)stream;
   const StGrid sg = st_grid(io->grid_x, io->grid_y);
   char* ws = (char*)io->workspace;
@@ -1355,23 +1409,23 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     uint32_t* nchunks = (uint32_t*)(ws + L.nchunks);
     uint32_t* chunk_st = (uint32_t*)(ws + L.chunk_st);
     uint32_t* list = (uint32_t*)(ws + L.list);
-    uint8_t* list_st = (uint8_t*)(ws + L.list_st);
     uint64_t* masks = (uint64_t*)(ws + L.masks);
     uint32_t* cnt2 = (uint32_t*)(ws + L.cnt2);
     uint32_t* base2 = (uint32_t*)(ws + L.base2);
     uint32_t* tile_total = (uint32_t*)(ws + L.tile_total);
     uint32_t* tile_start = (uint32_t*)(ws + L.tile_start);
     const unsigned nwg1 = ceil_div_u(P, kL1Group);
+    uint32_t* recw = (uint32_t*)(ws + L.recw);
     hipLaunchKernelGGL(l1_count_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, io->mult, order,
-                       io->xys, io->conic_opacity, io->tiles_touched, sets, cnt1);
+                       io->xys, io->conic_opacity, io->tiles_touched, io->st_base, io->st_masks,
+                       recw, sets, cnt1);
     hipLaunchKernelGGL(l1_seg_scan_kernel, dim3(kL1Segs), dim3(kMaxSt), 0, st, (int)nwg1, sg.S,
                        cnt1, segsum);
     hipLaunchKernelGGL(l1_top_scan_kernel, dim3(1), dim3(kMaxSt), 0, st, sg.S, segsum, st_start,
                        chunk_first, chunk_st, nchunks, L.max_chunks);
-    hipLaunchKernelGGL(l1_place_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg.S, order, sets,
-                       cnt1, segsum, st_start, K, list, list_st);
-    hipLaunchKernelGGL(l2_mask_kernel, dim3(ceil_div_u(K, 256)), dim3(256), 0, st, sg, io->mult,
-                       list, list_st, st_start, P, io->xys, io->conic_opacity, K, masks);
+    hipLaunchKernelGGL(l1_place_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, io->mult, order,
+                       recw, sets, cnt1, segsum, st_start, io->xys, io->conic_opacity, K, list,
+                       masks);
     const unsigned nch = (unsigned)L.max_chunks;
     hipLaunchKernelGGL(l2_count_kernel, dim3(nch), dim3(kL1Group), 0, st, st_start, chunk_first,
                        chunk_st, nchunks, K, masks, cnt2);

@@ -12,6 +12,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace fgs {
 
 constexpr int kTile = 16;
@@ -101,6 +104,14 @@ __device__ __forceinline__ void ellipse_isect(float4 co, float disc, float t, fl
   hi = (-co.y * h + sq) / coeff + p_v;
 }
 
+// Walk consumers may define rect(x0, x1, y0, y1): it is called once, before
+// any span, with the walk's tile rectangle [x0, x1) x [y0, y1), which holds
+// every span the walk emits.
+template <typename E, typename = void>
+struct HasRect : std::false_type {};
+template <typename E>
+struct HasRect<E, std::void_t<decltype(std::declval<E&>().rect(0, 0, 0, 0))>> : std::true_type {};
+
 // The walk restricted to the tile window [wx0, wx1) x [wy0, wy1): lines u
 // outside the window's range on the walked axis are not visited, and the
 // line state at the first visited line is the one the full walk reaches
@@ -138,6 +149,7 @@ __device__ __forceinline__ uint32_t tiles_walk_window(float px, float py, float4
   const int y_span = rmax1 - rmin1;
   const int x_span = rmax0 - rmin0;
   if (y_span * x_span == 0) return 0u;
+  if constexpr (HasRect<std::remove_reference_t<Emit>>::value) emit.rect(rmin0, rmax0, rmin1, rmax1);
   const bool is_y = y_span < x_span;
   if (is_y) {
     int ti;
@@ -205,6 +217,73 @@ __device__ __forceinline__ uint32_t tiles_walk(float px, float py, float4 co, in
 
 struct NoEmit {
   __device__ __forceinline__ void operator()(int, int, int, bool) const {}
+};
+
+// ---------------------------------------------------------------------------
+// Super-tile record of a Gaussian, built during the exact walk for the
+// two-level tile binning.  Super-tiles are 8x8 tiles.  Mask k (k = 0..3)
+// holds the Gaussian's tiles in super-tile (bx + (k & 1), by + (k >> 1)),
+// where (bx, by) is the super-tile of the walk rectangle's corner; bit
+// (y mod 8) * 8 + (x mod 8) is tile (x, y).  The record word is
+// bx | by << 12 | kStRecFits; a rectangle that reaches a third super-tile on
+// either axis (or a grid past 4096 super-tiles an axis) does not fit and has
+// record word 0 and no masks.
+// ---------------------------------------------------------------------------
+constexpr int kStTiles = 8;
+constexpr uint32_t kStRecFits = 1u << 31;
+
+// bits [a, b) of one 8-bit mask row (0 <= a, b <= 8)
+__device__ __forceinline__ uint64_t st_row_bits(int a, int b) {
+  return b > a ? (((1ull << (b - a)) - 1ull) << a) : 0ull;
+}
+
+// rows [a, b) of mask column c (0 <= a, b <= 8)
+__device__ __forceinline__ uint64_t st_col_bits(int a, int b, int c) {
+  if (b <= a) return 0ull;
+  const uint64_t hi = (b >= 8) ? ~0ull : ((1ull << (8 * b)) - 1ull);
+  const uint64_t lo = (1ull << (8 * a)) - 1ull;
+  return (hi & ~lo) & (0x0101010101010101ull << c);
+}
+
+struct EmitStMasks {
+  uint64_t m0 = 0ull, m1 = 0ull, m2 = 0ull, m3 = 0ull;
+  int bx = 0, by = 0;
+  bool fits = false;
+  __device__ __forceinline__ void rect(int x0, int x1, int y0, int y1) {
+    bx = x0 / kStTiles;
+    by = y0 / kStTiles;
+    fits = (x1 - 1) / kStTiles - bx <= 1 && (y1 - 1) / kStTiles - by <= 1 && bx < 4096 &&
+           by < 4096;
+  }
+  __device__ __forceinline__ void operator()(int u, int vmin, int vmax, bool is_y) {
+    if (!fits) return;
+    if (is_y) {  // tile row u, columns [vmin, vmax)
+      const int r = u - kStTiles * by;
+      const int c0 = vmin - kStTiles * bx, c1 = vmax - kStTiles * bx;
+      const int sh = (r & 7) * 8;
+      const uint64_t a = st_row_bits(c0, imin(c1, 8)) << sh;
+      const uint64_t b = st_row_bits(imax(c0, 8) - 8, c1 - 8) << sh;
+      // selects on every mask: a branch here becomes an indexed (scratch) access
+      const bool top = r < 8;
+      m0 |= top ? a : 0ull;
+      m1 |= top ? b : 0ull;
+      m2 |= top ? 0ull : a;
+      m3 |= top ? 0ull : b;
+    } else {  // tile column u, rows [vmin, vmax)
+      const int c = u - kStTiles * bx;
+      const int r0 = vmin - kStTiles * by, r1 = vmax - kStTiles * by;
+      const uint64_t a = st_col_bits(r0, imin(r1, 8), c & 7);
+      const uint64_t b = st_col_bits(imax(r0, 8) - 8, r1 - 8, c & 7);
+      const bool left = c < 8;
+      m0 |= left ? a : 0ull;
+      m2 |= left ? b : 0ull;
+      m1 |= left ? 0ull : a;
+      m3 |= left ? 0ull : b;
+    }
+  }
+  __device__ __forceinline__ uint32_t word() const {
+    return fits ? ((uint32_t)bx | ((uint32_t)by << 12) | kStRecFits) : 0u;
+  }
 };
 
 // ---------------------------------------------------------------------------

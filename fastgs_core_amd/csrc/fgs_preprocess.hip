@@ -188,6 +188,7 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   uint8_t clamp[3] = {0, 0, 0};
   float4 vsp = make_float4(0.f, 0.f, 0.f, 0.f);
   float c3[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  EmitStMasks st;  // super-tile record, built by the tile walk
   // p_view (in_frustum, :96-115)
   const float pv0 = V.m[0] * mx + V.m[4] * my + V.m[8] * mz + V.m[12];
   const float pv1 = V.m[1] * mx + V.m[5] * my + V.m[9] * mz + V.m[13];
@@ -223,7 +224,7 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
       const float px = ((pp0 + 1.0f) * (float)prm.image_width - 1.0f) * 0.5f;
       const float py = ((pp1 + 1.0f) * (float)prm.image_height - 1.0f) * 0.5f;
       const float4 con_o = make_float4(conic0, conic1, conic2, io.opacities[I]);
-      const uint32_t n = tiles_walk(px, py, con_o, prm.grid_x, prm.grid_y, prm.mult, NoEmit{});
+      const uint32_t n = tiles_walk(px, py, con_o, prm.grid_x, prm.grid_y, prm.mult, st);
       if (n != 0u) {
         if (prm.use_colors_precomp) {
 #pragma unroll
@@ -286,6 +287,17 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   for (int c = 0; c < 3; ++c) {
     io.rgb[3 * I + c] = col[c];
     io.clamped[3 * I + c] = clamp[c];
+  }
+  if (io.st_base) {
+    const uint32_t w = cnt != 0u ? st.word() : 0u;
+    io.st_base[I] = w;
+    if (w != 0u) {
+      uint4* dst = reinterpret_cast<uint4*>(io.st_masks + 4 * I);
+      dst[0] = make_uint4((uint32_t)st.m0, (uint32_t)(st.m0 >> 32), (uint32_t)st.m1,
+                          (uint32_t)(st.m1 >> 32));
+      dst[1] = make_uint4((uint32_t)st.m2, (uint32_t)(st.m2 >> 32), (uint32_t)st.m3,
+                          (uint32_t)(st.m3 >> 32));
+    }
   }
 }
 
@@ -622,6 +634,10 @@ extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
   }
   if (p->image_width <= 0 || p->image_height <= 0 || p->grid_x <= 0 || p->grid_y <= 0)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: bad image size");
+  if (!io->st_base != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u))
+    return set_error(FGS_ERR_INVALID_ARGUMENT,
+                     "fgs_preprocess_fwd: st_base and st_masks must both be set (st_masks "
+                     "16-byte aligned) or both NULL");
   const float fx = (float)p->image_width / (2.0f * p->tan_fovx);
   const float fy = (float)p->image_height / (2.0f * p->tan_fovy);
   const unsigned blocks = (unsigned)((p->P + 255) / 256);

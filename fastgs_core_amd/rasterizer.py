@@ -178,12 +178,12 @@ class _Preprocess(torch.autograd.Function):
             _p(means3d), _p(dc), _p(sh), _p(colors_precomp), _p(opacities), _p(scales),
             _p(rotations), _p(cov3d_precomp), _p(viewmatrix), _p(projmatrix), _p(campos),
             _p(viewspace_in), _p(radii), _p(xys), _p(depths), _p(cov3d), _p(rgb), _p(conic),
-            _p(tiles), _p(clamped), _p(vsp_out))
+            _p(tiles), _p(clamped), _p(vsp_out), _p(cfg["st_base"]), _p(cfg["st_masks"]))
         if P > 0:
             with _stage("preprocess_fwd"):
                 _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io),
                                                   _stream(dev)))
-        ctx.cfg = cfg
+        ctx.cfg = dict(cfg, st_base=None, st_masks=None)  # the records are forward-only
         ctx.opacity_shape = opacities.shape
         ctx.sh_shape = None if sh is None else sh.shape
         ctx.save_for_backward(means3d, sh, scales, rotations, cov3d_precomp, viewmatrix,
@@ -327,7 +327,9 @@ def _inclusive_scan_i32(x: torch.Tensor) -> torch.Tensor:
 
 
 def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: float,
-                    depth_ws: Optional[torch.Tensor] = None):
+                    depth_ws: Optional[torch.Tensor] = None,
+                    st_base: Optional[torch.Tensor] = None,
+                    st_masks: Optional[torch.Tensor] = None):
     lib = _lib.load()
     dev = xys.device
     P = xys.shape[0]
@@ -340,7 +342,7 @@ def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: f
     ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
     io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
                         _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws),
-                        _p(depth_ws))
+                        _p(depth_ws), _p(st_base), _p(st_masks))
     with _stage("binning"):
         _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
     return keys, plist, ranges, bucket_count, bucket_offsets
@@ -420,8 +422,11 @@ def _colour_and_geometry(inputs: Dict[str, Any], fn: str, col_keys, rot_key: str
 
 
 def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block_y, tan_fovx,
-                    tan_fovy, degree, scale_modifier, mult, default_vsp: bool):
-    """Shared body of preprocess_forward / rasterize_gaussians (binding.cpp:61-153, 424-492)."""
+                    tan_fovy, degree, scale_modifier, mult, default_vsp: bool,
+                    st_records: bool = False):
+    """Shared body of preprocess_forward / rasterize_gaussians (binding.cpp:61-153, 424-492).
+    st_records: also write the super-tile records the fused binning reads
+    (grids of at most 256 super-tiles of 8x8 tiles)."""
     def req(k):
         if k not in inputs:
             raise RuntimeError(f"{fn} missing required input tensor: {k}")
@@ -451,7 +456,11 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     gx, gy, _ = _tile_bounds(image_width, image_height, block_x, block_y)
     cfg = dict(degree=int(degree), max_sh=max_sh, W=int(image_width), H=int(image_height), gx=gx,
                gy=gy, use_cov=has_cov, use_col=has_col, scale_modifier=float(scale_modifier),
-               mult=float(mult), tan_fovx=float(tan_fovx), tan_fovy=float(tan_fovy))
+               mult=float(mult), tan_fovx=float(tan_fovx), tan_fovy=float(tan_fovy),
+               st_base=None, st_masks=None)
+    if st_records and ((gx + 7) // 8) * ((gy + 7) // 8) <= 256:
+        cfg["st_base"] = torch.empty(P, dtype=torch.int32, device=dev)
+        cfg["st_masks"] = torch.empty((P, 4), dtype=torch.int64, device=dev)
     dc = f(inputs["dc"]) if sh_path else None
     sh = f(inputs["sh"]) if sh_path else None
     if sh is not None and sh.numel() == 0:
@@ -481,12 +490,12 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
                                 prefiltered: bool = False, get_flag: bool = False,
                                 *, write_sampled: Optional[bool] = None) -> Dict[str, Any]:
     """Full forward (binding.cpp:33-282): preprocess -> scan -> binning/sort ->
-    tile ranges -> bucket offsets -> rasterize.  Two blocking 4-byte reads
-    (K and B), as in the reference."""
+    tile ranges -> bucket offsets -> rasterize.  The two 4-byte reads of the
+    reference (K and B) are waited for while the GPU has queued work."""
     fn = "rasterize_gaussians_forward"
     outs, cfg, dev = _run_preprocess(inputs, fn, _RG_NAMES, image_width, image_height, block_x,
                                      block_y, tan_fovx, tan_fovy, degree, scale_modifier, mult,
-                                     default_vsp=True)
+                                     default_vsp=True, st_records=True)
     radii, xys, depths, cov3d, rgb, conic, tiles, clamped, vsp_out = outs
     P = xys.shape[0]
     gx, gy = cfg["gx"], cfg["gy"]
@@ -514,7 +523,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
         with torch.no_grad():
             point_list_keys, point_list, ranges, bucket_count, bucket_offsets = _binning_sorted(
                 xys.detach(), depths.detach(), conic.detach(), tiles, K, gx, gy, float(mult),
-                depth_ws)
+                depth_ws, cfg["st_base"], cfg["st_masks"])
         ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
         if ws:
             # the sampled state is B * 256 entries: B is needed before the launch

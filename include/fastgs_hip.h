@@ -85,6 +85,16 @@ typedef struct {
   uint32_t* tiles_touched;     /* [P] */
   uint8_t* clamped;            /* [P,3] bool */
   float* viewspace_out;        /* [P,4] */
+  /* Optional (NULL: not written) super-tile records for fgs_binning_sorted,
+   * no reference counterpart: the Gaussian's tiles in the 2x2 super-tiles
+   * (8x8 tiles each) from the super-tile (bx, by) of its tile rectangle's
+   * corner.  st_base[i] = bx | by << 12 | 1u << 31, or 0 when the rectangle
+   * reaches a third super-tile on an axis or nothing is touched;
+   * st_masks[4i + k] = tiles of super-tile (bx + (k & 1), by + (k >> 1)),
+   * bit (y mod 8) * 8 + (x mod 8), written only where st_base[i] != 0.
+   * Both set or both NULL. */
+  uint32_t* st_base;           /* [P] */
+  uint64_t* st_masks;          /* [P,4], 16-byte aligned */
 } fgs_preprocess_fwd_io;
 
 /* Replaces FastGSPreprocess::eval_gpu (fastgs_preprocess.cpp:81-169) /
@@ -196,6 +206,10 @@ typedef struct {
    * an fgs_depth_order call on the same P, depths and tiles_touched that is
    * ordered before this call (same stream, or an event). */
   const void* depth_order;
+  /* NULL, or the super-tile records fgs_preprocess_fwd wrote for these
+   * Gaussians (same grid): Gaussians with a record skip their tile walks. */
+  const uint32_t* st_base;
+  const uint64_t* st_masks;
 } fgs_binning_io;
 
 size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, int32_t num_tiles);
