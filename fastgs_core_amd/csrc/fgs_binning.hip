@@ -652,6 +652,7 @@ constexpr int kMaxSt = 256;     // super-tiles of the two-level path
 constexpr int kL1Group = 256;   // level-1 Gaussians per workgroup
 constexpr int kL1Segs = 64;     // level-1 row segments of the count scan
 constexpr int kL2Chunk = 512;   // level-2 entries per workgroup (4 wavefronts x 128)
+constexpr int kWideGroups = 512;  // grid of l1_wide_masks_kernel
 
 struct StGrid {
   int gx, gy, sgx, sgy, S;
@@ -716,11 +717,11 @@ __device__ __forceinline__ int rec_st(uint32_t w, int k, const StGrid& sg) {
 }
 
 // Level 1a: per depth-ordered Gaussian its super-tiles, and per workgroup
-// the number of its Gaussians touching each super-tile.  A Gaussian with a
-// preprocess record (st_base word != 0) takes its four super-tile masks from
-// it; any other walks its tiles into its 256-bit super-tile set.  Stored in
-// depth order for l1_place: recw[i] (the record word, 0 for a set) and
-// sets[4i..4i+3] (the masks, or the set).
+// the number of its Gaussians touching each super-tile.  The preprocess
+// record (st_base word != 0) gives either four super-tile masks (fits) or the
+// 256-bit super-tile set; a Gaussian without one walks its tiles into the
+// set.  Stored in depth order for l1_place: recw[i] (the record word; 0 or
+// kStRecSet mean a set) and sets[4i..4i+3] (the masks, or the set).
 __global__ void __launch_bounds__(kL1Group)
 l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ order,
                 const float* __restrict__ xys, const float* __restrict__ conic_opacity,
@@ -735,7 +736,7 @@ l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
   uint32_t w = 0u;
   if (i < P) {
     const uint32_t g = order[i];
-    if (g < (uint32_t)P && tiles_touched[g] != 0u) {
+    if (g < (uint32_t)P) {
       w = st_base ? st_base[g] : 0u;
       if (w != 0u) {
         const uint4* src = reinterpret_cast<const uint4*>(st_masks + 4 * (size_t)g);
@@ -744,7 +745,7 @@ l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
         m[1] = (uint64_t)a.z | ((uint64_t)a.w << 32);
         m[2] = (uint64_t)b.x | ((uint64_t)b.y << 32);
         m[3] = (uint64_t)b.z | ((uint64_t)b.w << 32);
-      } else {
+      } else if (tiles_touched[g] != 0u) {
         EmitStSet e;
         e.m[0] = e.m[1] = e.m[2] = e.m[3] = 0ull;
         e.sgx = sg.sgx;
@@ -763,7 +764,7 @@ l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
                         (uint32_t)(m[3] >> 32));
   }
   __syncthreads();
-  if (w != 0u) {
+  if (w & kStRecFits) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int sid = rec_st(w, k, sg);
@@ -773,6 +774,7 @@ l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
 #pragma unroll
     for (int wd = 0; wd < 4; ++wd) {
       uint64_t b = m[wd];
+      if (64 * (wd + 1) > sg.S) b &= (64 * wd >= sg.S) ? 0ull : ((1ull << (sg.S - 64 * wd)) - 1ull);
       while (b) {
         const int k = __builtin_ctzll(b);
         b &= b - 1ull;
@@ -841,16 +843,16 @@ l1_top_scan_kernel(int S, uint32_t* __restrict__ segsum, uint32_t* __restrict__ 
 // distinct, so their order among themselves is free) and ranked per
 // super-tile in that order, 256 at a time: wave64 match-any over the 8
 // super-tile bits, then the four waves through LDS counters, as in a radix
-// pass.  The mask comes from the record, or, for a Gaussian without one, from
-// its walk clipped to the super-tile's window.
+// pass.  A record's masks are written as they are; a Gaussian given by its
+// super-tile set gets mask 0, filled in by l1_wide_masks_kernel (every real
+// pair has at least one tile, so 0 marks exactly those).
 constexpr int kL1Pairs = 2048;  // LDS pair capacity per round
 __global__ void __launch_bounds__(kL1Group)
-l1_place_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ order,
+l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
                 const uint32_t* __restrict__ recw, const uint64_t* __restrict__ sets,
                 const uint32_t* __restrict__ cnt1, const uint32_t* __restrict__ segsum,
-                const uint32_t* __restrict__ st_start, const float* __restrict__ xys,
-                const float* __restrict__ conic_opacity, int64_t cap,
-                uint32_t* __restrict__ list, uint64_t* __restrict__ masks) {
+                const uint32_t* __restrict__ st_start, int64_t cap, uint32_t* __restrict__ list,
+                uint64_t* __restrict__ masks) {
   __shared__ uint64_t s_pm[kL1Pairs];  // mask of each pair (0: walk it)
   __shared__ uint32_t s_pg[kL1Pairs];  // Gaussian of each pair
   __shared__ uint8_t s_ps[kL1Pairs];   // super-tile of each pair
@@ -877,11 +879,15 @@ l1_place_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
   const int seg = (int)blockIdx.x / rows;
   if (t < S)
     s_base[t] = st_start[t] + segsum[(size_t)seg * S + t] + cnt1[(size_t)blockIdx.x * S + t];
+  const bool fits = (rw & kStRecFits) != 0u;
   uint32_t np = 0;
-  if (rw != 0u) {
+  if (fits) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) np += (m[k] != 0ull && rec_st(rw, k, sg) < S) ? 1u : 0u;
   } else {
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd)  // super-tile ids >= S are never set; clear them anyway
+      if (64 * (wd + 1) > S) m[wd] &= (64 * wd >= S) ? 0ull : ((1ull << (S - 64 * wd)) - 1ull);
     np = (uint32_t)(__popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]) + __popcll(m[3]));
   }
   uint32_t total;
@@ -890,7 +896,7 @@ l1_place_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
   for (uint32_t r0 = 0; r0 < total; r0 += kL1Pairs) {
     // this round's pairs into LDS
     uint32_t p = off;
-    if (rw != 0u) {
+    if (fits) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int sid = rec_st(rw, k, sg);
@@ -941,27 +947,69 @@ l1_place_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
         uint32_t pos = s_base[d] + rk;
         for (int k = 0; k < w; ++k) pos += s_wh[k][d];
         if ((int64_t)pos < cap) {
-          const uint32_t gq = s_pg[q];
-          uint64_t mk = s_pm[q];
-          if (mk == 0ull && gq < (uint32_t)P) {
-            EmitTileMask em;
-            em.m = 0ull;
-            em.x0 = (int)(d % (uint32_t)sg.sgx) * kSt;
-            em.y0 = (int)(d / (uint32_t)sg.sgx) * kSt;
-            const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)gq);
-            const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)gq);
-            tiles_walk_window(xy.x, xy.y, co, sg.gx, sg.gy, mult, em.x0, em.x0 + kSt, em.y0,
-                              em.y0 + kSt, em);
-            mk = em.m;
-          }
-          list[pos] = gq;
-          masks[pos] = mk;
+          list[pos] = s_pg[q];
+          masks[pos] = s_pm[q];
         }
       }
       __syncthreads();
       if (t < S) s_base[t] += s_wh[0][t] + s_wh[1][t] + s_wh[2][t] + s_wh[3][t];
       __syncthreads();
     }
+  }
+}
+
+// Level 1e: the mask of every list entry l1_place left 0 (a Gaussian given
+// by its super-tile set; every real pair has at least one tile, so 0 marks
+// exactly those): its walk clipped to the super-tile window.  A workgroup
+// takes 4096 entries at a time, collects the chunk's zero masks in LDS, then
+// walks them one per thread, so the few walks run side by side.  The
+// super-tile of entry e is the list holding it (binary search over the list
+// starts, staged in LDS).
+constexpr int kWideChunk = 4096;
+__global__ void __launch_bounds__(256)
+l1_wide_masks_kernel(StGrid sg, float mult, const uint32_t* __restrict__ st_start, int32_t P,
+                     const float* __restrict__ xys, const float* __restrict__ conic_opacity,
+                     const uint32_t* __restrict__ list, int64_t cap,
+                     uint64_t* __restrict__ masks) {
+  __shared__ uint32_t s_ss[kMaxSt + 1];
+  __shared__ uint32_t s_e[kWideChunk];
+  __shared__ uint32_t s_n;
+  const int t = (int)threadIdx.x;
+  for (int k = t; k <= sg.S; k += 256) s_ss[k] = st_start[k];
+  __syncthreads();
+  const int64_t k1 = (int64_t)s_ss[sg.S] < cap ? (int64_t)s_ss[sg.S] : cap;
+  for (int64_t c0 = (int64_t)blockIdx.x * kWideChunk; c0 < k1;
+       c0 += (int64_t)gridDim.x * kWideChunk) {
+    if (t == 0) s_n = 0u;
+    __syncthreads();
+#pragma unroll 4
+    for (int k = 0; k < kWideChunk / 256; ++k) {
+      const int64_t e = c0 + k * 256 + t;
+      if (e < k1 && masks[e] == 0ull) s_e[atomicAdd(&s_n, 1u)] = (uint32_t)(e - c0);
+    }
+    __syncthreads();
+    const uint32_t n = s_n;
+    for (uint32_t j = (uint32_t)t; j < n; j += 256) {
+      const int64_t e = c0 + s_e[j];
+      int lo = 0, hi = sg.S;  // largest s with st_start[s] <= e
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if ((int64_t)s_ss[mid] <= e) lo = mid; else hi = mid;
+      }
+      const uint32_t g = list[e];
+      EmitTileMask em;
+      em.m = 0ull;
+      em.x0 = (lo % sg.sgx) * kSt;
+      em.y0 = (lo / sg.sgx) * kSt;
+      if (g < (uint32_t)P) {
+        const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
+        const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
+        tiles_walk_window(xy.x, xy.y, co, sg.gx, sg.gy, mult, em.x0, em.x0 + kSt, em.y0,
+                          em.y0 + kSt, em);
+      }
+      masks[e] = em.m;
+    }
+    __syncthreads();
   }
 }
 
@@ -1423,9 +1471,10 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
                        cnt1, segsum);
     hipLaunchKernelGGL(l1_top_scan_kernel, dim3(1), dim3(kMaxSt), 0, st, sg.S, segsum, st_start,
                        chunk_first, chunk_st, nchunks, L.max_chunks);
-    hipLaunchKernelGGL(l1_place_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, io->mult, order,
-                       recw, sets, cnt1, segsum, st_start, io->xys, io->conic_opacity, K, list,
-                       masks);
+    hipLaunchKernelGGL(l1_place_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order, recw,
+                       sets, cnt1, segsum, st_start, K, list, masks);
+    hipLaunchKernelGGL(l1_wide_masks_kernel, dim3(kWideGroups), dim3(256), 0, st, sg, io->mult,
+                       st_start, P, io->xys, io->conic_opacity, list, K, masks);
     const unsigned nch = (unsigned)L.max_chunks;
     hipLaunchKernelGGL(l2_count_kernel, dim3(nch), dim3(kL1Group), 0, st, st_start, chunk_first,
                        chunk_st, nchunks, K, masks, cnt2);

@@ -221,16 +221,22 @@ struct NoEmit {
 
 // ---------------------------------------------------------------------------
 // Super-tile record of a Gaussian, built during the exact walk for the
-// two-level tile binning.  Super-tiles are 8x8 tiles.  Mask k (k = 0..3)
-// holds the Gaussian's tiles in super-tile (bx + (k & 1), by + (k >> 1)),
-// where (bx, by) is the super-tile of the walk rectangle's corner; bit
-// (y mod 8) * 8 + (x mod 8) is tile (x, y).  The record word is
-// bx | by << 12 | kStRecFits; a rectangle that reaches a third super-tile on
-// either axis (or a grid past 4096 super-tiles an axis) does not fit and has
-// record word 0 and no masks.
+// two-level tile binning.  Super-tiles are 8x8 tiles, numbered row-major on a
+// grid sgx wide.  Two forms share four 64-bit words m0..m3:
+//  - fits: the walk rectangle lies in the 2x2 super-tiles from (bx, by), the
+//    super-tile of its corner.  m_k holds the tiles in super-tile
+//    (bx + (k & 1), by + (k >> 1)), bit (y mod 8) * 8 + (x mod 8) for tile
+//    (x, y).  Record word bx | by << 12 | kStRecFits.
+//  - set: any other rectangle, on grids of at most 256 super-tiles: bit s of
+//    m0..m3 (m_k holding s = 64k..64k+63) marks each super-tile s holding at
+//    least one of the Gaussian's tiles.  Record word kStRecSet.
+// A Gaussian that touches no tile, or a wide one on a larger grid, has record
+// word 0.
 // ---------------------------------------------------------------------------
 constexpr int kStTiles = 8;
+constexpr int kStMaxSet = 256;
 constexpr uint32_t kStRecFits = 1u << 31;
+constexpr uint32_t kStRecSet = 1u << 30;
 
 // bits [a, b) of one 8-bit mask row (0 <= a, b <= 8)
 __device__ __forceinline__ uint64_t st_row_bits(int a, int b) {
@@ -245,10 +251,25 @@ __device__ __forceinline__ uint64_t st_col_bits(int a, int b, int c) {
   return (hi & ~lo) & (0x0101010101010101ull << c);
 }
 
-struct EmitStMasks {
+// bits [lo, hi] of the 256-bit word lo..hi <= 255, as four 64-bit words:
+// word k gets the part of the range inside [64k, 64k + 63]
+__device__ __forceinline__ uint64_t st_set_word(int lo, int hi, int k) {
+  const int a = imax(lo, 64 * k), z = imin(hi, 64 * k + 63);
+  if (z < a) return 0ull;
+  const int n = z - a + 1;
+  return ((n >= 64) ? ~0ull : ((1ull << n) - 1ull)) << (a - 64 * k);
+}
+
+struct EmitStRecord {
   uint64_t m0 = 0ull, m1 = 0ull, m2 = 0ull, m3 = 0ull;
   int bx = 0, by = 0;
+  int sgx = 0;           // super-tile grid width
+  bool set_ok = false;   // the grid has at most kStMaxSet super-tiles
   bool fits = false;
+  __device__ __forceinline__ EmitStRecord(int gx, int gy) {
+    sgx = (gx + kStTiles - 1) / kStTiles;
+    set_ok = sgx * ((gy + kStTiles - 1) / kStTiles) <= kStMaxSet;
+  }
   __device__ __forceinline__ void rect(int x0, int x1, int y0, int y1) {
     bx = x0 / kStTiles;
     by = y0 / kStTiles;
@@ -256,33 +277,56 @@ struct EmitStMasks {
            by < 4096;
   }
   __device__ __forceinline__ void operator()(int u, int vmin, int vmax, bool is_y) {
-    if (!fits) return;
-    if (is_y) {  // tile row u, columns [vmin, vmax)
-      const int r = u - kStTiles * by;
-      const int c0 = vmin - kStTiles * bx, c1 = vmax - kStTiles * bx;
-      const int sh = (r & 7) * 8;
-      const uint64_t a = st_row_bits(c0, imin(c1, 8)) << sh;
-      const uint64_t b = st_row_bits(imax(c0, 8) - 8, c1 - 8) << sh;
-      // selects on every mask: a branch here becomes an indexed (scratch) access
-      const bool top = r < 8;
-      m0 |= top ? a : 0ull;
-      m1 |= top ? b : 0ull;
-      m2 |= top ? 0ull : a;
-      m3 |= top ? 0ull : b;
-    } else {  // tile column u, rows [vmin, vmax)
-      const int c = u - kStTiles * bx;
-      const int r0 = vmin - kStTiles * by, r1 = vmax - kStTiles * by;
-      const uint64_t a = st_col_bits(r0, imin(r1, 8), c & 7);
-      const uint64_t b = st_col_bits(imax(r0, 8) - 8, r1 - 8, c & 7);
-      const bool left = c < 8;
-      m0 |= left ? a : 0ull;
-      m2 |= left ? b : 0ull;
-      m1 |= left ? 0ull : a;
-      m3 |= left ? 0ull : b;
+    // every update is a select on all four words: a branch or an index here
+    // becomes a scratch access
+    if (fits) {
+      if (is_y) {  // tile row u, columns [vmin, vmax)
+        const int r = u - kStTiles * by;
+        const int c0 = vmin - kStTiles * bx, c1 = vmax - kStTiles * bx;
+        const int sh = (r & 7) * 8;
+        const uint64_t a = st_row_bits(c0, imin(c1, 8)) << sh;
+        const uint64_t b = st_row_bits(imax(c0, 8) - 8, c1 - 8) << sh;
+        const bool top = r < 8;
+        m0 |= top ? a : 0ull;
+        m1 |= top ? b : 0ull;
+        m2 |= top ? 0ull : a;
+        m3 |= top ? 0ull : b;
+      } else {  // tile column u, rows [vmin, vmax)
+        const int c = u - kStTiles * bx;
+        const int r0 = vmin - kStTiles * by, r1 = vmax - kStTiles * by;
+        const uint64_t a = st_col_bits(r0, imin(r1, 8), c & 7);
+        const uint64_t b = st_col_bits(imax(r0, 8) - 8, r1 - 8, c & 7);
+        const bool left = c < 8;
+        m0 |= left ? a : 0ull;
+        m2 |= left ? b : 0ull;
+        m1 |= left ? 0ull : a;
+        m3 |= left ? 0ull : b;
+      }
+    } else if (set_ok) {
+      const int b = u / kStTiles;
+      const int c0 = vmin / kStTiles, c1 = (vmax - 1) / kStTiles;
+      if (is_y) {  // row u: super-tiles b*sgx + c0 .. b*sgx + c1
+        const int lo = b * sgx + c0, hi = b * sgx + c1;
+        m0 |= st_set_word(lo, hi, 0);
+        m1 |= st_set_word(lo, hi, 1);
+        m2 |= st_set_word(lo, hi, 2);
+        m3 |= st_set_word(lo, hi, 3);
+      } else {  // column u: super-tiles c*sgx + b, c = c0..c1
+        for (int c = c0; c <= c1; ++c) {
+          const int sb = c * sgx + b;
+          const uint64_t bit = 1ull << (sb & 63);
+          const int k = sb >> 6;
+          m0 |= k == 0 ? bit : 0ull;
+          m1 |= k == 1 ? bit : 0ull;
+          m2 |= k == 2 ? bit : 0ull;
+          m3 |= k == 3 ? bit : 0ull;
+        }
+      }
     }
   }
   __device__ __forceinline__ uint32_t word() const {
-    return fits ? ((uint32_t)bx | ((uint32_t)by << 12) | kStRecFits) : 0u;
+    if (fits) return (uint32_t)bx | ((uint32_t)by << 12) | kStRecFits;
+    return set_ok ? kStRecSet : 0u;
   }
 };
 

@@ -188,7 +188,7 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   uint8_t clamp[3] = {0, 0, 0};
   float4 vsp = make_float4(0.f, 0.f, 0.f, 0.f);
   float c3[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  EmitStMasks st;  // super-tile record, built by the tile walk
+  EmitStRecord st(prm.grid_x, prm.grid_y);  // super-tile record, built by the tile walk
   // p_view (in_frustum, :96-115)
   const float pv0 = V.m[0] * mx + V.m[4] * my + V.m[8] * mz + V.m[12];
   const float pv1 = V.m[1] * mx + V.m[5] * my + V.m[9] * mz + V.m[13];

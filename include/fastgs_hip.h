@@ -86,12 +86,17 @@ typedef struct {
   uint8_t* clamped;            /* [P,3] bool */
   float* viewspace_out;        /* [P,4] */
   /* Optional (NULL: not written) super-tile records for fgs_binning_sorted,
-   * no reference counterpart: the Gaussian's tiles in the 2x2 super-tiles
-   * (8x8 tiles each) from the super-tile (bx, by) of its tile rectangle's
-   * corner.  st_base[i] = bx | by << 12 | 1u << 31, or 0 when the rectangle
-   * reaches a third super-tile on an axis or nothing is touched;
-   * st_masks[4i + k] = tiles of super-tile (bx + (k & 1), by + (k >> 1)),
-   * bit (y mod 8) * 8 + (x mod 8), written only where st_base[i] != 0.
+   * no reference counterpart.  Super-tiles are 8x8 tiles, numbered row-major
+   * on a grid ceil(grid_x/8) wide.  Two forms:
+   *  - st_base[i] = bx | by << 12 | 1u << 31: the Gaussian's tile rectangle
+   *    lies in the 2x2 super-tiles from (bx, by), the super-tile of its
+   *    corner; st_masks[4i + k] = its tiles in super-tile
+   *    (bx + (k & 1), by + (k >> 1)), bit (y mod 8) * 8 + (x mod 8);
+   *  - st_base[i] = 1u << 30 (other rectangles, grids of at most 256
+   *    super-tiles): bit s of the 256-bit st_masks[4i..4i+3] marks each
+   *    super-tile s holding one of its tiles;
+   *  - st_base[i] = 0: no tile touched (or a wide Gaussian on a larger
+   *    grid); st_masks[4i..] not written.
    * Both set or both NULL. */
   uint32_t* st_base;           /* [P] */
   uint64_t* st_masks;          /* [P,4], 16-byte aligned */
