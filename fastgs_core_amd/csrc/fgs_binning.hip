@@ -1119,12 +1119,14 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
 
 // Level 2e: every entry's tiles written at tile start + entries of the tile
 // in earlier chunks + rank in this chunk (list order).  Four wavefronts take
-// 128 entries each; per round of 64 entries and per tile j (a uniform loop)
-// the ballot of the entries having tile j gives their ranks and lane j's
-// cursor (readlane) their base.  The chunk's output is staged in LDS grouped
-// by tile and written run by run (consecutive lanes, consecutive positions;
-// wavefront w writes tiles j = w mod 4); a chunk with more than kL2Stage
-// outputs writes straight to its positions.
+// 128 entries each.  Per round of 64 entries, a 64x64 bit transpose gives
+// lane j the ballot of the entries having tile j; each lane then walks the
+// set bits of its own mask, fetching tile j's ballot (its rank: the entries
+// below it) and lane j's cursor (its base) with ds_bpermute.  The chunk's
+// output is staged in LDS grouped by tile and written run by run
+// (consecutive lanes, consecutive positions; wavefront w writes tiles
+// j = w mod 4); a chunk with more than kL2Stage outputs writes straight to
+// its positions.
 constexpr int kL2Stage = 4608;
 __global__ void __launch_bounds__(kL1Group)
 l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
@@ -1179,13 +1181,23 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
       g = list[e];
       db = g < (uint32_t)P ? __float_as_uint(depths[g]) : 0xFFFFFFFFu;
     }
-    for (int j = 0; j < kWave; ++j) {
-      const bool has = (m >> j) & 1ull;
-      const uint64_t b = __ballot(has);
-      if (b == 0ull) continue;  // uniform
-      const uint32_t at =
-          (uint32_t)__builtin_amdgcn_readlane((int)cur, j) + (uint32_t)__popcll(b & lt);
-      if (has) {
+    // lane j: the round's entries having tile j (bit i = entry i)
+    const uint64_t bt = transpose64(m);
+    const int bt_lo = (int)(uint32_t)bt, bt_hi = (int)(uint32_t)(bt >> 32);
+    // each lane walks its own tiles; the loop is uniform so every lane
+    // takes part in the permutes that fetch tile j's ballot and cursor
+    uint64_t mm = m;
+    while (__ballot(mm != 0ull) != 0ull) {
+      const bool act = mm != 0ull;
+      const int j = act ? (int)__builtin_ctzll(mm) : 0;
+      mm &= mm - 1ull;
+      const int src = j << 2;
+      const uint32_t blo = (uint32_t)__builtin_amdgcn_ds_bpermute(src, bt_lo);
+      const uint32_t bhi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, bt_hi);
+      const uint32_t cur_j = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)cur);
+      if (act) {
+        const uint64_t bj = (uint64_t)blo | ((uint64_t)bhi << 32);
+        const uint32_t at = cur_j + (uint32_t)__popcll(bj & lt);
         if (staged) {
           if (at < (uint32_t)kL2Stage) {
             s_g[at] = g;
@@ -1197,8 +1209,8 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
           point_list[at] = g;
         }
       }
-      if (l == j) cur += (uint32_t)__popcll(b);
     }
+    cur += (uint32_t)__popcll(bt);  // lane j: tile j's entries in this round
   }
   if (!staged) return;  // uniform
   __syncthreads();
