@@ -316,26 +316,27 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
 
 // Splats lo+cnt-1 .. lo of the staged batch, back to front: per splat the
 // gradient terms of the lane's pixels, then (when any pixel blends it) the
-// wave reduction into the splat's LDS record.  kSafe is fixed per batch, so
-// the accumulators stay in one set of registers through the loop.
+// wave reduction into the splat's LDS record.  The accumulators live for one
+// splat and start at -0.0 (-0 + x == x exactly, so the first add folds away
+// and nothing is carried or cleared between splats).
 template <int NCH, bool kSafe>
 __device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, const float4* s_h,
                                           const float4* s_cull, float* s_rec, const int lo,
                                           const int cnt, const int l, const float pxf,
                                           const float pyf0, const float ty0, const int (&nc)[4],
                                           float (&T)[4], float (&SdL)[4],
-                                          const float (&dL)[4][3], float (&v)[kGradTerms]) {
+                                          const float (&dL)[4][3]) {
   for (int j = cnt - 1; j >= 0; --j) {
     const float4 a = s_a[j];
     const float4 b = s_b[j];
     const float4 hh = s_h[j];
     const float4 cu = s_cull[j];
-    if (bwd_splat_terms<NCH, kSafe>(a, b, cu.w, hh, make_float2(cu.x, cu.y), lo + j, pxf, pyf0,
-                                    ty0, nc, T, SdL, dL, v)) {
-      wave_reduce_terms(v, s_rec + j * kRec, l);
+    float v[kGradTerms];
 #pragma unroll
-      for (int k = 0; k < kGradTerms; ++k) v[k] = 0.0f;
-    }
+    for (int k = 0; k < kGradTerms; ++k) v[k] = -0.0f;
+    if (bwd_splat_terms<NCH, kSafe>(a, b, cu.w, hh, make_float2(cu.x, cu.y), lo + j, pxf, pyf0,
+                                    ty0, nc, T, SdL, dL, v))
+      wave_reduce_terms(v, s_rec + j * kRec, l);
   }
 }
 
@@ -391,9 +392,6 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
   const float ty0 = (float)(ty * kTile);
   const float hx = 0.5f * (float)sh.W;
   const float hy = 0.5f * (float)sh.H;
-  float v[kGradTerms];
-#pragma unroll
-  for (int k = 0; k < kGradTerms; ++k) v[k] = 0.0f;
   const int rounds = (last + kBwdBatch - 1) / kBwdBatch;
   for (int r = 0; r < rounds; ++r) {
     const int hi = last - r * kBwdBatch;
@@ -432,10 +430,10 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
     __syncthreads();
     if (fast)
       bwd_batch<NCH, false>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, T, SdL,
-                            dL, v);
+                            dL);
     else
       bwd_batch<NCH, true>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, T, SdL,
-                           dL, v);
+                           dL);
     __syncthreads();
     // Flush: item q = (splat q/12, term q%12), so the lanes of one atomic
     // instruction cover the consecutive terms of about five splats.
