@@ -72,9 +72,12 @@ __device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c,
   return make_float2(y - hy, y + hy);
 }
 
-template <int NCH, bool kSampled>
+// kMode bit 0: write the sampled state; bit 1: count metric hits (get_flag).
+template <int NCH, int kMode>
 __global__ void __launch_bounds__(256)
 raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, RasterShape sh) {
+  constexpr bool kSampled = (kMode & 1) != 0;
+  constexpr bool kMetric = (kMode & 2) != 0;
   __shared__ float4 s_a[256];
   __shared__ float4 s_b[256];
   __shared__ float s_c[256];
@@ -99,10 +102,10 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
     for (int b = t; b < nb; b += 256)
       if ((int64_t)bbm0 + b < prm.bucket_sum) io.bucket_to_tile[bbm0 + b] = (uint32_t)tile;
   }
-  const bool count_metric = prm.get_flag && inside && io.metric_map[pix] == 1;
+  const bool count_metric = kMetric && inside && io.metric_map[pix] == 1;
   const float pxf = (float)px, pyf = (float)py;
   float T = 1.0f;
-  uint32_t contributor = 0, last = 0;
+  uint32_t last = 0;
   float acc[3] = {0.0f, 0.0f, 0.0f};
   int done = inside ? 0 : 1;
   const int rounds = (n + 255) / 256;
@@ -121,10 +124,15 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
     }
     __syncthreads();
     const int cnt = (n - base) < 256 ? (n - base) : 256;
-    if (!done) {
+    // Branch-free per splat: blend / stop / take are lane predicates and the
+    // state moves by selects, so the wave runs one straight path; it leaves
+    // the batch once no lane is live.  A lane that stops takes nothing more,
+    // as the reference loop's break.
+    bool live = !done;
+    if (__ballot(live) != 0ull) {  // wave-uniform
       for (int j = 0; j < cnt; ++j) {
         const int jj = base + j;
-        if (kSampled && (jj & 31) == 0) {
+        if (kSampled && (jj & 31) == 0 && live) {
           const size_t bk = (size_t)bbm0 + (size_t)(jj >> 5);
           if ((int64_t)bk < prm.bucket_sum) {
             io.sampled_t[bk * 256 + t] = T;
@@ -133,31 +141,33 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
               io.sampled_ar[bk * (size_t)prm.num_channels * 256 + (size_t)c * 256 + t] = acc[c];
           }
         }
-        contributor++;
         const float4 a = s_a[j];
         const float4 b = s_b[j];
         const float dx = a.x - pxf;
         const float dy = a.y - pyf;
         const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-        if (power > 0.0f) continue;
         const float alpha = fminf(0.99f, b.y * det_expf(power));
-        if (alpha < 1.0f / 255.0f) continue;
         const float test_t = T * (1.0f - alpha);
-        if (test_t < 0.0001f) {
-          done = 1;
-          break;
-        }
-        // colour by fused multiply-adds (no decision depends on it)
-        const float aT = alpha * T;
-        acc[0] = __builtin_fmaf(b.z, aT, acc[0]);
-        if (NCH > 1) acc[1] = __builtin_fmaf(b.w, aT, acc[1]);
-        if (NCH > 2) acc[2] = __builtin_fmaf(s_c[j], aT, acc[2]);
-        if (count_metric && s_g[j] < (uint32_t)prm.num_points)
+        const bool blend = live && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
+        const bool stop = blend && test_t < 0.0001f;
+        const bool take = blend && !stop;
+        live = live && !stop;
+        // colour by fused multiply-adds (no decision depends on it); both
+        // factors are selected to 0 where the pixel does not take the splat,
+        // so a non-finite colour stays out of it (0 * 0 adds nothing)
+        const float aT = take ? alpha * T : 0.0f;
+        const float c2 = NCH > 2 ? s_c[j] : 0.0f;
+        acc[0] = __builtin_fmaf(take ? b.z : 0.0f, aT, acc[0]);
+        if (NCH > 1) acc[1] = __builtin_fmaf(take ? b.w : 0.0f, aT, acc[1]);
+        if (NCH > 2) acc[2] = __builtin_fmaf(take ? c2 : 0.0f, aT, acc[2]);
+        if (kMetric && take && count_metric && s_g[j] < (uint32_t)prm.num_points)
           atomicAdd(&io.metric_count[s_g[j]], 1);
-        T = test_t;
-        last = contributor;
+        T = take ? test_t : T;
+        last = take ? (uint32_t)(jj + 1) : last;
+        if ((j & 7) == 7 && __ballot(live) == 0ull) break;  // uniform
       }
     }
+    done = live ? 0 : 1;
     __syncthreads();
   }
   if (inside) {
@@ -471,6 +481,17 @@ copy_means2d_grad_kernel(const float* __restrict__ vsp, float* __restrict__ dmea
 
 using namespace fgs;
 
+template <int NCH>
+static void launch_fwd(int mode, dim3 grid, dim3 block, hipStream_t st,
+                       const fgs_raster_params& p, const fgs_raster_fwd_io& io, RasterShape sh) {
+  switch (mode) {
+    case 0: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 0>), grid, block, 0, st, p, io, sh); break;
+    case 1: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 1>), grid, block, 0, st, p, io, sh); break;
+    case 2: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 2>), grid, block, 0, st, p, io, sh); break;
+    default: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 3>), grid, block, 0, st, p, io, sh);
+  }
+}
+
 static int32_t raster_check(const fgs_raster_params* p, const char* who) {
   if (!p) return set_error(FGS_ERR_INVALID_ARGUMENT, who);
   if (p->image_width <= 0 || p->image_height <= 0 || p->num_channels <= 0 || p->num_tiles < 0 ||
@@ -521,18 +542,11 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
     fgs_fill_u32(io->max_contrib + tiles, 0u, p->num_tiles - tiles, stream);
   if (tiles == 0) return check_launch("rasterize_fwd");
   RasterShape sh{W, H, gx, gy};
-  const bool smp = p->write_sampled && p->bucket_sum > 0;
+  const int mode = (p->write_sampled && p->bucket_sum > 0 ? 1 : 0) | (p->get_flag ? 2 : 0);
   const dim3 grid(tiles), block(256);
-  if (NCH == 3) {
-    if (smp) hipLaunchKernelGGL((raster_fwd_kernel<3, true>), grid, block, 0, st, *p, *io, sh);
-    else hipLaunchKernelGGL((raster_fwd_kernel<3, false>), grid, block, 0, st, *p, *io, sh);
-  } else if (NCH == 2) {
-    if (smp) hipLaunchKernelGGL((raster_fwd_kernel<2, true>), grid, block, 0, st, *p, *io, sh);
-    else hipLaunchKernelGGL((raster_fwd_kernel<2, false>), grid, block, 0, st, *p, *io, sh);
-  } else {
-    if (smp) hipLaunchKernelGGL((raster_fwd_kernel<1, true>), grid, block, 0, st, *p, *io, sh);
-    else hipLaunchKernelGGL((raster_fwd_kernel<1, false>), grid, block, 0, st, *p, *io, sh);
-  }
+  if (NCH == 3) launch_fwd<3>(mode, grid, block, st, *p, *io, sh);
+  else if (NCH == 2) launch_fwd<2>(mode, grid, block, st, *p, *io, sh);
+  else launch_fwd<1>(mode, grid, block, st, *p, *io, sh);
   return check_launch("raster_fwd_kernel");
 }
 
