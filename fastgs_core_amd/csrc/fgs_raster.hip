@@ -112,6 +112,8 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
   for (int r = 0; r < rounds; ++r) {
     if (__syncthreads_count(done) == 256) break;
     const int base = r * 256;
+    const int cnt = (n - base) < 256 ? (n - base) : 256;
+    const int cnt8 = (cnt + 7) & ~7;  // padded with splats of opacity 0 (never blended)
     if (base + t < n) {
       const uint32_t g = io.point_list[start + base + t];
       float4 a, b;
@@ -121,18 +123,25 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
       s_b[t] = b;
       s_c[t] = c;
       s_g[t] = g;
+    } else if (t < cnt8) {
+      s_a[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+      s_b[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+      s_c[t] = 0.0f;
+      s_g[t] = 0xFFFFFFFFu;
     }
     __syncthreads();
-    const int cnt = (n - base) < 256 ? (n - base) : 256;
     // Branch-free per splat: blend / stop / take are lane predicates and the
-    // state moves by selects, so the wave runs one straight path; it leaves
-    // the batch once no lane is live.  A lane that stops takes nothing more,
-    // as the reference loop's break.
+    // state moves by selects, so the wave runs one straight path, eight
+    // splats at a time; it leaves the batch once no lane is live.  A lane
+    // that stops takes nothing more, as the reference loop's break.
     bool live = !done;
     if (__ballot(live) != 0ull) {  // wave-uniform
-      for (int j = 0; j < cnt; ++j) {
+      for (int j0 = 0; j0 < cnt8; j0 += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u;
         const int jj = base + j;
-        if (kSampled && (jj & 31) == 0 && live) {
+        if (kSampled && (jj & 31) == 0 && jj < n && live) {
           const size_t bk = (size_t)bbm0 + (size_t)(jj >> 5);
           if ((int64_t)bk < prm.bucket_sum) {
             io.sampled_t[bk * 256 + t] = T;
@@ -164,7 +173,8 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           atomicAdd(&io.metric_count[s_g[j]], 1);
         T = take ? test_t : T;
         last = take ? (uint32_t)(jj + 1) : last;
-        if ((j & 7) == 7 && __ballot(live) == 0ull) break;  // uniform
+      }
+        if (__ballot(live) == 0ull) break;  // uniform
       }
     }
     done = live ? 0 : 1;
