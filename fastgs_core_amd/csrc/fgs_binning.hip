@@ -109,6 +109,32 @@ __device__ __forceinline__ uint32_t look_back(const uint64_t* status, int64_t ch
   return excl;
 }
 
+// Exclusive prefix of chunk `chunk` of a single counter from the aggregates
+// its predecessors publish (status[c], flag kFlagAggregate): the threads of
+// the workgroup take predecessors t, t + blockDim, ... (polling each until
+// published), then one block reduction.  All loads are in flight at once, so
+// there is no chain of waits.  Called by every thread of the workgroup.
+__device__ __forceinline__ uint32_t block_sum_predecessors(const uint64_t* status, int64_t chunk,
+                                                           uint32_t* err, uint32_t* s_tmp) {
+  uint32_t acc = 0;
+  for (int64_t c = threadIdx.x; c < chunk; c += blockDim.x) {
+    uint64_t w = __hip_atomic_load(status + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t spins = 0;
+    while ((uint32_t)(w >> 32) == 0u) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      w = __hip_atomic_load(status + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    acc += (uint32_t)w;
+  }
+  uint32_t total;
+  block_excl_scan(acc, s_tmp, &total);
+  return total;
+}
+
 __device__ __forceinline__ int64_t take_ticket(uint32_t* ticket, uint32_t* s_slot) {
   if (threadIdx.x == 0) *s_slot = atomicAdd(ticket, 1u);
   __syncthreads();
@@ -116,7 +142,8 @@ __device__ __forceinline__ int64_t take_ticket(uint32_t* ticket, uint32_t* s_slo
 }
 
 // ---------------------------------------------------------------------------
-// Scan (u32, wrapping): one pass, chunk prefixes by look-back.
+// Scan (u32, wrapping): one pass; each chunk publishes its sum and adds up
+// its predecessors' sums (block_sum_predecessors).
 // kGather: the input element i is tiles_touched[order[i]].
 // ---------------------------------------------------------------------------
 template <bool kGather>
@@ -127,7 +154,6 @@ chained_scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict_
   __shared__ uint32_t s_data[kChunk + kChunk / 16];
   __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
   __shared__ uint32_t s_slot;
-  __shared__ uint32_t s_excl;
   const int64_t chunk = take_ticket(ticket, &s_slot);
   const int64_t base = chunk * kChunk;
 #pragma unroll
@@ -155,19 +181,9 @@ chained_scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict_
   }
   uint32_t total;
   const uint32_t texcl = block_excl_scan(tsum, s_tmp, &total);
-  if (threadIdx.x == 0) {
-    uint32_t excl = 0;
-    if (chunk == 0) {
-      status_store(status, kFlagPrefix, total);
-    } else {
-      status_store(status + chunk, kFlagAggregate, total);
-      excl = look_back(status, chunk, 1, err);
-      status_store(status + chunk, kFlagPrefix, excl + total);
-    }
-    s_excl = excl;
-  }
-  __syncthreads();
-  uint32_t run = texcl + s_excl;
+  if (threadIdx.x == 0) status_store(status + chunk, kFlagAggregate, total);
+  const uint32_t excl = block_sum_predecessors(status, chunk, err, s_tmp);
+  uint32_t run = texcl + excl;
 #pragma unroll
   for (int k = 0; k < kItems; ++k) {
     const uint32_t x = v[k];
@@ -301,27 +317,30 @@ radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* 
   }
 }
 
-template <typename K>
-__global__ void __launch_bounds__(kThreads)
+// kT threads per workgroup, kT * kItems keys per chunk.  Digit-wise steps
+// (histograms, offsets, look-back) run on the first 256 threads.
+template <typename K, int kT>
+__global__ void __launch_bounds__(kT)
 radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                   K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift,
                   int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
                   int64_t nchunks, uint32_t* ticket, uint32_t* err) {
-  __shared__ uint32_t s_wh[kWavesPerBlock][256];
+  constexpr int kW = kT / kWave;
+  constexpr int kC = kT * kItems;
+  __shared__ uint32_t s_wh[kW][256];
   __shared__ uint32_t s_dstart[256];
   __shared__ uint32_t s_goff[256];
-  __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
+  __shared__ uint32_t s_tmp[kW + 1];
   __shared__ uint32_t s_slot;
-  __shared__ K s_keys[kChunk];
-  __shared__ uint32_t s_vals[kChunk];
+  __shared__ K s_keys[kC];
+  __shared__ uint32_t s_vals[kC];
   const int t = (int)threadIdx.x;
   const int w = t / kWave;
   const int lane = lane_id();
   const uint32_t mask = (1u << nbits) - 1u;
-#pragma unroll
-  for (int k = 0; k < kWavesPerBlock; ++k) s_wh[k][t] = 0;
+  for (int i = t; i < kW * 256; i += kT) (&s_wh[0][0])[i] = 0;
   const int64_t chunk = take_ticket(ticket, &s_slot);  // includes a barrier
-  const int64_t base = chunk * kChunk + (int64_t)w * (kChunk / kWavesPerBlock);
+  const int64_t base = chunk * kC + (int64_t)w * (kC / kW);
   const uint64_t lt = lanemask_lt();
   K key[kItems];
   uint32_t val[kItems];
@@ -347,25 +366,28 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   }
   __syncthreads();
   {
-    uint32_t c[kWavesPerBlock];
+    const bool dig = (uint32_t)t <= mask;  // t < 256 as nbits <= 8
+    uint32_t c[kW];
     uint32_t tot = 0;
 #pragma unroll
-    for (int k = 0; k < kWavesPerBlock; ++k) {
-      c[k] = ((uint32_t)t <= mask) ? s_wh[k][t] : 0u;
+    for (int k = 0; k < kW; ++k) {
+      c[k] = dig ? s_wh[k][t] : 0u;
       tot += c[k];
     }
-    const uint32_t g = ((uint32_t)t <= mask) ? hist[t] : 0u;
+    const uint32_t g = dig ? hist[t] : 0u;
     const uint32_t gbase = block_excl_scan(g, s_tmp, nullptr);
     uint32_t total;
     const uint32_t ds = block_excl_scan(tot, s_tmp, &total);
-    uint32_t run = ds;
+    if (t < 256) {
+      uint32_t run = ds;
 #pragma unroll
-    for (int k = 0; k < kWavesPerBlock; ++k) {
-      s_wh[k][t] = run;
-      run += c[k];
+      for (int k = 0; k < kW; ++k) {
+        s_wh[k][t] = run;
+        run += c[k];
+      }
+      s_dstart[t] = ds;
     }
-    s_dstart[t] = ds;
-    if ((uint32_t)t <= mask) {
+    if (dig) {
       uint32_t excl = 0;
       uint64_t* st = status + (size_t)t;  // chunk-major: [chunk][digit]
       if (chunk == 0) {
@@ -390,9 +412,9 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     }
   }
   __syncthreads();
-  const int64_t rem = n - chunk * kChunk;
-  const int cnt = rem < kChunk ? (int)rem : kChunk;
-  for (int j = t; j < cnt; j += kThreads) {
+  const int64_t rem = n - chunk * kC;
+  const int cnt = rem < kC ? (int)rem : kC;
+  for (int j = t; j < cnt; j += kT) {
     const K k = s_keys[j];
     const uint32_t d = (uint32_t)(k >> shift) & mask;
     const uint32_t g = s_goff[d] + ((uint32_t)j - s_dstart[d]);
@@ -401,10 +423,14 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   }
 }
 
+// Radix passes run kSortT threads per workgroup (kSortChunk keys per chunk).
+constexpr int kSortT = 512;
+constexpr int kSortChunk = kSortT * kItems;
+
 // Zero-initialised state of one sort: histograms (8 x 256), tickets (8),
 // error word, then the status words of every pass.
 static size_t sort_state_bytes(int64_t n, int passes) {
-  const int64_t nc = (n + kChunk - 1) / kChunk;
+  const int64_t nc = (n + kSortChunk - 1) / kSortChunk;
   return (size_t)((8 * 256 * 4 + 64 + (int64_t)passes * (nc < 1 ? 1 : nc) * 256 * 8 + 255) &
                   ~(int64_t)255);
 }
@@ -436,7 +462,7 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
                        vals_in, keys_out, vals_out, n);
     return check_launch("copy_pairs");
   }
-  const int64_t nc = (n + kChunk - 1) / kChunk;
+  const int64_t nc = (n + kSortChunk - 1) / kSortChunk;
   char* p = (char*)ws;
   K* tk = (K*)p;
   p += ((size_t)n * sizeof(K) + 255) & ~(size_t)255;
@@ -447,7 +473,8 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   uint32_t* err = tickets + 8;
   uint64_t* status = (uint64_t*)(p + 8 * 256 * 4 + 64);
   launch_fill(hist, 0u, (int64_t)(sort_state_bytes(n, pl.passes) / 4), st);
-  int64_t hb = nc < 1024 ? nc : 1024;
+  const int64_t hn = (n + kChunk - 1) / kChunk;  // histogram workgroups: 4096 keys each
+  const int64_t hb = hn < 1024 ? hn : 1024;
   hipLaunchKernelGGL((radix_hist_kernel<K, kDepthKeys>), dim3((unsigned)hb), dim3(kThreads), 0, st,
                      keys_in, n, pl, hist, depths, tiles_touched, dkeys_out);
   const K* src_k = kDepthKeys ? (const K*)dkeys_out : keys_in;
@@ -457,7 +484,7 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
     const bool to_out = ((pl.passes - 1 - pass) % 2) == 0;
     K* dk = to_out ? keys_out : tk;
     uint32_t* dv = to_out ? vals_out : tv;
-    hipLaunchKernelGGL(radix_pass_kernel<K>, dim3((unsigned)nc), dim3(kThreads), 0, st, src_k,
+    hipLaunchKernelGGL((radix_pass_kernel<K, kSortT>), dim3((unsigned)nc), dim3(kSortT), 0, st, src_k,
                        src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
                        status + (size_t)pass * nc * 256, nc, tickets + pass, err);
     const int32_t e2 = check_launch("radix_pass");
@@ -653,6 +680,7 @@ constexpr int kL1Group = 256;   // level-1 Gaussians per workgroup
 constexpr int kL1Segs = 64;     // level-1 row segments of the count scan
 constexpr int kL2Chunk = 512;   // level-2 entries per workgroup (4 wavefronts x 128)
 constexpr int kWideGroups = 512;  // grid of l1_wide_masks_kernel
+constexpr int kScanBatch = 32;    // loads in flight per serial-scan batch
 
 struct StGrid {
   int gx, gy, sgx, sgy, S;
@@ -795,10 +823,16 @@ l1_seg_scan_kernel(int nwg, int S, uint32_t* __restrict__ cnt1, uint32_t* __rest
   const int rows = (nwg + kL1Segs - 1) / kL1Segs;
   const int r0 = (int)blockIdx.x * rows, r1 = imin(nwg, r0 + rows);
   uint32_t run = 0;
-  for (int r = r0; r < r1; ++r) {
-    const uint32_t v = cnt1[(size_t)r * S + s];
-    cnt1[(size_t)r * S + s] = run;
-    run += v;
+  for (int r = r0; r < r1; r += kScanBatch) {
+    // the batch's loads are all issued before its first store
+    uint32_t v[kScanBatch];
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) v[i] = r + i < r1 ? cnt1[(size_t)(r + i) * S + s] : 0u;
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) {
+      if (r + i < r1) cnt1[(size_t)(r + i) * S + s] = run;
+      run += v[i];
+    }
   }
   segsum[(size_t)blockIdx.x * S + s] = run;
 }
@@ -813,10 +847,15 @@ l1_top_scan_kernel(int S, uint32_t* __restrict__ segsum, uint32_t* __restrict__ 
   const int s = (int)threadIdx.x;
   uint32_t run = 0;
   if (s < S) {
-    for (int g = 0; g < kL1Segs; ++g) {
-      const uint32_t v = segsum[(size_t)g * S + s];
-      segsum[(size_t)g * S + s] = run;
-      run += v;
+    for (int g0 = 0; g0 < kL1Segs; g0 += kScanBatch) {
+      uint32_t v[kScanBatch];
+#pragma unroll
+      for (int i = 0; i < kScanBatch; ++i) v[i] = segsum[(size_t)(g0 + i) * S + s];
+#pragma unroll
+      for (int i = 0; i < kScanBatch; ++i) {
+        segsum[(size_t)(g0 + i) * S + s] = run;
+        run += v[i];
+      }
     }
   }
   uint32_t total;
@@ -1079,10 +1118,15 @@ l2_st_scan_kernel(StGrid sg, const uint32_t* __restrict__ chunk_first,
   uint32_t run = 0;
   const uint32_t c1 = (int64_t)chunk_first[s + 1] < max_chunks ? chunk_first[s + 1]
                                                                  : (uint32_t)max_chunks;
-  for (uint32_t c = chunk_first[s]; c < c1; ++c) {
-    const uint32_t v = cnt2[(size_t)c * kWave + l];
-    base2[(size_t)c * kWave + l] = run;
-    run += v;
+  for (uint32_t c = chunk_first[s]; c < c1; c += kScanBatch) {
+    uint32_t v[kScanBatch];
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) v[i] = c + i < c1 ? cnt2[(size_t)(c + i) * kWave + l] : 0u;
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) {
+      if (c + i < c1) base2[(size_t)(c + i) * kWave + l] = run;
+      run += v[i];
+    }
   }
   const int x = (s % sg.sgx) * kSt + (l % kSt), y = (s / sg.sgx) * kSt + (l / kSt);
   if (x < sg.gx && y < sg.gy) tile_total[y * sg.gx + x] = run;
@@ -1090,30 +1134,67 @@ l2_st_scan_kernel(StGrid sg, const uint32_t* __restrict__ chunk_first,
 
 // Level 2d (one workgroup): tile starts, ranges (empty tiles [0,0], as the
 // reference's zero-filled ranges), bucket counts and their inclusive scan.
+// Thread t owns tiles [t*kTilesPer, (t+1)*kTilesPer) (the two-level path has
+// at most kMaxSt * 64 = 16384 tiles, 16 per thread); global loads and stores
+// go through LDS so they stay coalesced.
+constexpr int kTilesPer = kMaxSt * kWave / 1024;
+constexpr int kTileLds = 1024 * kTilesPer + 1024 * kTilesPer / 32;
+__device__ __forceinline__ int tpad(int i) { return i + (i >> 5); }
 __global__ void __launch_bounds__(1024)
 l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
                     uint32_t* __restrict__ tile_start, uint32_t* __restrict__ ranges,
                     uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets) {
   __shared__ uint32_t s_tmp[1024 / kWave + 1];
-  uint32_t carry = 0, bcarry = 0;
-  for (int base = 0; base < T; base += 1024) {
-    const int t = base + (int)threadIdx.x;
-    const uint32_t n = t < T ? tile_total[t] : 0u;
-    uint32_t total;
-    const uint32_t ex = block_excl_scan(n, s_tmp, &total);
-    const uint32_t bc = (n + 31u) / 32u;
-    uint32_t btotal;
-    const uint32_t bex = block_excl_scan(bc, s_tmp, &btotal);
-    if (t < T) {
-      const uint32_t st = carry + ex;
-      tile_start[t] = st;
-      ranges[2 * (size_t)t] = n ? st : 0u;
-      ranges[2 * (size_t)t + 1] = n ? st + n : 0u;
-      bucket_count[t] = bc;
-      bucket_offsets[t] = bcarry + bex + bc;
+  __shared__ uint32_t s_v[kTileLds];
+  const int t = (int)threadIdx.x;
+  const int t0 = t * kTilesPer;
+#pragma unroll
+  for (int i = 0; i < kTilesPer; ++i) {
+    const int idx = i * 1024 + t;
+    s_v[tpad(idx)] = idx < T ? tile_total[idx] : 0u;
+  }
+  __syncthreads();
+  uint32_t n[kTilesPer];
+  uint32_t sum = 0, bsum = 0;
+#pragma unroll
+  for (int i = 0; i < kTilesPer; ++i) {
+    n[i] = s_v[tpad(t0 + i)];
+    sum += n[i];
+    bsum += (n[i] + 31u) / 32u;
+  }
+  uint32_t st = block_excl_scan(sum, s_tmp, nullptr);  // has barriers
+  uint32_t bo = block_excl_scan(bsum, s_tmp, nullptr);
+  // tile starts into LDS, then tile_start and ranges
+#pragma unroll
+  for (int i = 0; i < kTilesPer; ++i) {
+    s_v[tpad(t0 + i)] = st;
+    st += n[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kTilesPer; ++i) {
+    const int idx = i * 1024 + t;
+    if (idx < T) {
+      const uint32_t a = s_v[tpad(idx)];
+      const uint32_t m = tile_total[idx];
+      tile_start[idx] = a;
+      *reinterpret_cast<uint2*>(ranges + 2 * (size_t)idx) = m ? make_uint2(a, a + m)
+                                                               : make_uint2(0u, 0u);
+      bucket_count[idx] = (m + 31u) / 32u;
     }
-    carry += total;
-    bcarry += btotal;
+  }
+  __syncthreads();
+  // inclusive bucket offsets
+#pragma unroll
+  for (int i = 0; i < kTilesPer; ++i) {
+    bo += (n[i] + 31u) / 32u;
+    s_v[tpad(t0 + i)] = bo;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kTilesPer; ++i) {
+    const int idx = i * 1024 + t;
+    if (idx < T) bucket_offsets[idx] = s_v[tpad(idx)];
   }
 }
 
