@@ -5,6 +5,12 @@ python_package/fastgs_core/__init__.py re-exports ``_fastgs_core``): the
 same functions, signatures, dict keys and autograd routes, computed by the
 hand-written HIP kernels in ``libfastgs_hip.so``.
 """
+from .densify import (  # noqa: F401
+    DensifyConfig,
+    GaussianTrainState,
+    OptimConfig,
+    compute_scene_extent,
+)
 from .loss import l1_ssim_loss  # noqa: F401
 from .train import (  # noqa: F401
     FastGSOptimizerPolicy,

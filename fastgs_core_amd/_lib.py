@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class PreprocessParams(Structure):
@@ -80,6 +80,30 @@ class RasterBwdIO(Structure):
         "dL_dconic_opacity", "dL_dviewspace")]
 
 
+class DensifyParams(Structure):
+    _fields_ = [
+        ("grad_thresh", c_float), ("grad_abs_thresh", c_float), ("clone_max_scale", c_float),
+        ("importance_threshold", c_float), ("min_opacity", c_float), ("max_screen_size", c_float),
+        ("world_max_scale", c_float), ("split_factor", c_int32),
+    ]
+
+
+class DensifyBuildIO(Structure):
+    _fields_ = ([("P_new", c_int32), ("sh_row", c_int32), ("split_factor", c_int32),
+                 ("reset_stats", c_int32), ("opacity_cap", c_float)]
+                + [(n, c_void_p) for n in ("rows", "l2_src", "l2_kind", "l2_child", "normals",
+                                           "means3d", "features_dc", "features_rest",
+                                           "opacity_logits", "log_scales", "rotations")]
+                + [("exp_avg", c_void_p * 6), ("exp_avg_sq", c_void_p * 6)]
+                + [(n, c_void_p) for n in ("max_radii2d", "grad_accum", "grad_accum_abs", "denom",
+                                           "tmp_radii", "d_means3d", "d_features_dc",
+                                           "d_features_rest", "d_opacity_logits", "d_log_scales",
+                                           "d_rotations")]
+                + [("d_exp_avg", c_void_p * 6), ("d_exp_avg_sq", c_void_p * 6)]
+                + [(n, c_void_p) for n in ("d_max_radii2d", "d_grad_accum", "d_grad_accum_abs",
+                                           "d_denom", "d_tmp_radii")])
+
+
 # Exported symbol -> (restype, argtypes).  The not-gpu test checks that the
 # library exports every one of these and that include/fastgs_hip.h declares
 # exactly this set.
@@ -115,6 +139,25 @@ SIGNATURES = {
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fgs_adam_step": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_float, c_float,
                                 c_float, c_float, c_int32, c_int32, c_void_p]),
+    "fgs_densify_stats": (c_int32, [c_int32] + [c_void_p] * 7 + [c_void_p]),
+    "fgs_densify_classify": (c_int32, [c_int32, POINTER(DensifyParams)] + [c_void_p] * 7
+                             + [c_void_p]),
+    "fgs_densify_layout": (c_int32, [c_int32, c_int32] + [c_void_p] * 5 + [c_void_p]),
+    "fgs_densify_prune_keys": (c_int32, [c_int32, POINTER(DensifyParams), c_int32]
+                               + [c_void_p] * 9 + [c_void_p]),
+    "fgs_densify_select": (c_int32, [c_int32, c_int64, c_void_p, c_void_p, c_void_p]),
+    "fgs_densify_keep_first": (c_int32, [c_int32, c_int64, c_void_p, c_void_p, c_void_p]),
+    "fgs_invert_flags": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p]),
+    "fgs_densify_compact": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "fgs_densify_build": (c_int32, [POINTER(DensifyBuildIO), c_void_p]),
+    "fgs_opacity_cap": (c_int32, [c_int32, c_float, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "fgs_metric_map_workspace_bytes": (c_size_t, [c_int64]),
+    "fgs_metric_map": (c_int32, [c_int32, c_int64, c_void_p, c_void_p, c_float, c_void_p,
+                                 c_void_p, c_void_p, c_void_p]),
+    "fgs_score_accumulate": (c_int32, [c_int32] + [c_void_p] * 4 + [c_void_p]),
+    "fgs_score_finalize": (c_int32, [c_int32, c_int32] + [c_void_p] * 5 + [c_void_p]),
+    "fgs_final_prune_mask": (c_int32, [c_int32, c_float, c_float] + [c_void_p] * 4
+                             + [c_void_p]),
 }
 
 _lib = None

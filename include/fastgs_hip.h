@@ -351,6 +351,169 @@ int32_t fgs_adam_step(float* param, const float* grad, float* exp_avg, float* ex
 /* Fill a u32 buffer with a value on the stream (a kernel, graph-safe). */
 int32_t fgs_fill_u32(uint32_t* dst, uint32_t value, int64_t n, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Densification and pruning.  No counterpart in the reference library: the  */
+/* reference's FastGS training script does these on the host with numpy      */
+/* (scripts/train_scanner_fastgs.py: scores :279-340, statistics :391-405,    */
+/* clone/split/prune :470-616 and :661-742, final prune :745-793, opacity     */
+/* cap/reset :619-658).  Rows are the reference's parameter rows; exp/log are */
+/* the library's deterministic ones.  Random numbers are inputs.              */
+/* ------------------------------------------------------------------------ */
+
+/* Gradient statistics of one step (:391-405): for rows with radii > 0,
+ * max_radii2d = max(max_radii2d, radii), grad_accum += |d_viewspace[:2]|,
+ * grad_accum_abs += |d_viewspace[2:]|, denom += 1; tmp_radii = radii on
+ * every row.  d_viewspace: the [P,4] viewspace gradient. */
+int32_t fgs_densify_stats(int32_t P, const int32_t* radii, const float* d_viewspace,
+                          float* max_radii2d, float* grad_accum, float* grad_accum_abs,
+                          float* denom, int32_t* tmp_radii, void* stream);
+
+/* Thresholds of densify_and_prune_fastgs (:661-742), as float32. */
+typedef struct {
+  float grad_thresh;          /* args.grad_thresh */
+  float grad_abs_thresh;      /* args.grad_abs_thresh */
+  float clone_max_scale;      /* args.dense * scene_extent */
+  float importance_threshold; /* args.importance_score_threshold */
+  float min_opacity;          /* args.min_opacity */
+  float max_screen_size;      /* args.max_screen_size (<= 0: off) */
+  float world_max_scale;      /* args.max_world_scale_factor * scene_extent (<= 0: off) */
+  int32_t split_factor;       /* args.split_factor */
+} fgs_densify_params;
+
+/* Clone and split flags (u32 0/1) of the P current rows: clone = importance >
+ * threshold && max scale <= clone_max_scale && |grad_accum/max(denom,1)| >=
+ * grad_thresh; split = importance > threshold && max scale > clone_max_scale
+ * && |grad_accum_abs/max(denom,1)| >= grad_abs_thresh. */
+int32_t fgs_densify_classify(int32_t P, const fgs_densify_params* prm, const float* grad_accum,
+                             const float* grad_accum_abs, const float* denom,
+                             const float* log_scales, const float* importance,
+                             uint32_t* clone_flag, uint32_t* split_flag, void* stream);
+
+/* The P2 = P - ns + nc + ns * split_factor pre-prune rows, from the
+ * inclusive scans of the flags (nc, ns: their totals): the rows that are not
+ * split sources in order, then the clones, then split_factor children per
+ * source, consecutive.  l2_src: source row; l2_kind: 0 kept, 1 clone, 2 split
+ * child; l2_child: the child's row in the normals array, else -1. */
+int32_t fgs_densify_layout(int32_t P, int32_t split_factor, const uint32_t* clone_incl,
+                           const uint32_t* split_incl, int32_t* l2_src, int32_t* l2_kind,
+                           int32_t* l2_child, void* stream);
+
+/* Prune candidates of the P2 pre-prune rows (opacity < min_opacity, screen
+ * size when nothing was appended, world scale) and their removal keys: for a
+ * candidate, the float bits of (-log(1 - u)) * (1e-6 + (1 - pruning_score))
+ * (u: uniforms[r] in [0,1)), whose k smallest are a weighted sample without
+ * replacement with weights 1 / (1e-6 + (1 - score)); otherwise 0xFFFFFFFF.
+ * pruning_score NULL: all keys 0xFFFFFFFF.  l2_src / l2_kind NULL: identity.
+ * Appended rows take their source's score. */
+int32_t fgs_densify_prune_keys(int32_t P2, const fgs_densify_params* prm, int32_t any_appended,
+                               const int32_t* l2_src, const int32_t* l2_kind,
+                               const float* opacity_logits, const float* log_scales,
+                               const float* max_radii2d, const float* pruning_score,
+                               const float* uniforms, uint64_t* keys, uint32_t* candidate,
+                               void* stream);
+
+/* keep[sorted_rows[j]] = (j >= k): the first k rows of a sorted order are
+ * removed. */
+int32_t fgs_densify_select(int32_t P2, int64_t k, const uint32_t* sorted_rows, uint32_t* keep,
+                           void* stream);
+
+/* keep[sorted_rows[j]] = (j < k): the first k rows of a sorted order kept. */
+int32_t fgs_densify_keep_first(int32_t P, int64_t k, const uint32_t* sorted_rows, uint32_t* keep,
+                               void* stream);
+
+/* out[i] = !in[i] (u32 flags). */
+int32_t fgs_invert_flags(int32_t n, const uint32_t* in, uint32_t* out, void* stream);
+
+/* rows[keep_incl[r] - 1] = r for the kept rows (keep_incl: inclusive scan of
+ * keep). */
+int32_t fgs_densify_compact(int32_t P2, const uint32_t* keep, const uint32_t* keep_incl,
+                            int32_t* rows, void* stream);
+
+/* The new row set: new row f comes from pre-prune row rows[f] (NULL:
+ * identity), which comes from source row l2_src (NULL with l2_kind: identity,
+ * all kept).  Parameters and their Adam moments (exp_avg / exp_avg_sq in the
+ * order means3d, features_dc, features_rest, opacity_logits, log_scales,
+ * rotations; NULL entries skipped) are copied from the source, moments of
+ * appended rows are zero; statistics are copied, or zero when reset_stats.
+ * Split children: mean + R(q)(exp(log_scale) * z) with z = normals[l2_child]
+ * and log scales log(exp(ls) / (0.8 split_factor)) (:560-583).  opacity_cap
+ * > 0: every opacity logit becomes logit(min(sigmoid(x), cap)) and the
+ * opacity moments restart at zero (:619-637).  Sources and destinations must
+ * not overlap. */
+typedef struct {
+  int32_t P_new;
+  int32_t sh_row;        /* floats per features_rest row */
+  int32_t split_factor;
+  int32_t reset_stats;
+  float opacity_cap;
+  const int32_t* rows;
+  const int32_t* l2_src;
+  const int32_t* l2_kind;
+  const int32_t* l2_child;
+  const float* normals;  /* [children, 3] */
+  const float* means3d;
+  const float* features_dc;
+  const float* features_rest;
+  const float* opacity_logits;
+  const float* log_scales;
+  const float* rotations;
+  const float* exp_avg[6];
+  const float* exp_avg_sq[6];
+  const float* max_radii2d;
+  const float* grad_accum;
+  const float* grad_accum_abs;
+  const float* denom;
+  const int32_t* tmp_radii;
+  float* d_means3d;
+  float* d_features_dc;
+  float* d_features_rest;
+  float* d_opacity_logits;
+  float* d_log_scales;
+  float* d_rotations;
+  float* d_exp_avg[6];
+  float* d_exp_avg_sq[6];
+  float* d_max_radii2d;
+  float* d_grad_accum;
+  float* d_grad_accum_abs;
+  float* d_denom;
+  int32_t* d_tmp_radii;
+} fgs_densify_build_io;
+int32_t fgs_densify_build(const fgs_densify_build_io* io, void* stream);
+
+/* logit(min(sigmoid(x), cap)) on every opacity logit, and the opacity Adam
+ * moments (NULL: skipped) set to zero (cap_opacity_logits /
+ * reset_opacity_logits, :619-658). */
+int32_t fgs_opacity_cap(int32_t P, float cap, float* opacity_logits, float* exp_avg,
+                        float* exp_avg_sq, void* stream);
+
+/* The scoring render's metric map (:300-304): l = mean over channels of
+ * |pred - target| per pixel ([C, HW] arrays), metric_map = (l - min) /
+ * max(max - min, 1e-6) > loss_thresh; photometric_loss (device float) = mean
+ * |pred - target|, summed in double. */
+size_t fgs_metric_map_workspace_bytes(int64_t HW);
+int32_t fgs_metric_map(int32_t C, int64_t HW, const float* pred, const float* target,
+                       float loss_thresh, void* workspace, int32_t* metric_map,
+                       float* photometric_loss, void* stream);
+
+/* counts += metric_count; score += photometric_loss * metric_count
+ * (:306-320). */
+int32_t fgs_score_accumulate(int32_t P, const int32_t* metric_count,
+                             const float* photometric_loss, float* counts, float* score,
+                             void* stream);
+
+/* pruning = (score - min) / max(max - min, 1e-6); importance (NULL: not
+ * written) = floor(counts / max(n_cams, 1)) (:334-339).  minmax_ws: 2
+ * words. */
+int32_t fgs_score_finalize(int32_t P, int32_t n_cams, const float* counts, const float* score,
+                           float* importance, float* pruning, uint32_t* minmax_ws, void* stream);
+
+/* Final prune mask (:754-757): opacity < min_opacity || score > score_thresh,
+ * and keys that sort ascending in order of descending opacity - score (the
+ * keep priority of :771-776; ties keep row order). */
+int32_t fgs_final_prune_mask(int32_t P, float min_opacity, float score_thresh,
+                             const float* opacity_logits, const float* pruning_score,
+                             uint32_t* prune, uint64_t* priority_keys, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
