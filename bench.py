@@ -108,6 +108,174 @@ def ssim(torch, F, img, tgt, win):
     return (num / den).mean()
 
 
+DENSIFY_LOOP = dict(P_hidden=300_000, P_start=100_000, W=1280, H=720, degree=3, cameras=50,
+                    iterations=500, interval=100, hidden_seed=101, start_seed=0, camera_seed=11,
+                    mse_until=600, grad_thresh=2.0e-4,
+                    desc="cfg5: densification loop, 500 iterations at 1280x720, 50 sphere "
+                         "cameras, targets from a hidden 300k scene, start 100k Gaussians "
+                         "(reference init), clone/split/prune every 100 iterations, "
+                         "grad threshold 2e-4")
+# The same loop with the clone threshold lowered so that the set grows by about
+# 1.6x per densification and the buffers are reallocated on the way to ~1M
+# (at 2e-4 the averaged viewspace gradients of this workload rarely qualify).
+DENSIFY_GROW = dict(DENSIFY_LOOP, grad_thresh=1.0e-6,
+                    desc="cfg5-grow: the cfg5 loop with the clone threshold at 1e-6, growing "
+                         "100k -> ~1M with buffer reallocation")
+
+
+def reference_init(torch, dev, seed, P, degree):
+    """The reference's starting model (init_model, train_scanner_fixed.py:601-631)
+    on seeded points and colours: points N(0,1)^3 clipped to [-2,2] (the scene
+    distribution of the other configs), colours U(0,1); isotropic scale 0.02,
+    identity rotations, opacity 0.82, DC = (colour - 0.5) / C0, higher SH 0."""
+    rng = np.random.default_rng(seed)
+    pts = np.clip(rng.standard_normal((P, 3)), -2.0, 2.0).astype(np.float32)
+    colors = rng.uniform(0.0, 1.0, (P, 3)).astype(np.float32)
+    M = (degree + 1) ** 2 - 1
+    rot = np.zeros((P, 4), np.float32)
+    rot[:, 0] = 1.0
+    lg = np.float32(math.log(0.82 / (1.0 - 0.82)))
+    return {"means3d": torch.from_numpy(pts).to(dev),
+            "features_dc": torch.from_numpy(((colors - 0.5) / 0.28209479177387814)
+                                            .astype(np.float32)).to(dev),
+            "features_rest": torch.zeros((P, M, 3), device=dev),
+            "opacity_logits": torch.full((P, 1), float(lg), device=dev),
+            "log_scales": torch.full((P, 3), math.log(0.02), device=dev),
+            "rotations": torch.from_numpy(rot).to(dev)}
+
+
+def run_densify_loop(args):
+    """the training loop of train_scanner_fastgs.py:968-1060
+    on the GPU state.  Per iteration: a camera popped from a seeded viewpoint
+    stack, render at the active SH degree (0 below iteration 1000, +1 per
+    1000), MSE loss (the reference's loss up to --mse-until 600), backward,
+    the densification statistics from this render's radii and viewspace
+    gradient, the learning-rate schedule and the FastGS Adam cadence.  Every
+    ``interval`` iterations: the metric-map scores over 10 sampled cameras
+    (two renders each) and densify_and_prune_fastgs.  The timed region is the
+    whole loop, densification included; targets are rendered beforehand."""
+    import torch
+
+    import fastgs_core
+    from fastgs_core_amd import synthetic as syn
+    from fastgs_core_amd.densify import DensifyConfig, GaussianTrainState, compute_scene_extent
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda", 0)
+    c = DENSIFY_GROW if args.config == "cfg5-grow" else DENSIFY_LOOP
+    W, H, deg = c["W"], c["H"], c["degree"]
+    HW = W * H
+    iterations = args.steps if args.steps is not None else c["iterations"]
+    cams = syn.sphere_cameras(c["cameras"], c["camera_seed"], W, H)
+    cam_in = [{"viewmatrix": torch.from_numpy(cm.viewmatrix.reshape(-1).copy()).to(dev),
+               "projmatrix": torch.from_numpy(cm.projmatrix.reshape(-1).copy()).to(dev),
+               "campos": torch.from_numpy(cm.campos.copy()).to(dev),
+               "background": torch.zeros(3, device=dev)} for cm in cams]
+
+    def to_params(sc):
+        opac = np.clip(sc["opacities"].astype(np.float64), 1e-6, 1 - 1e-6)
+        return {"means3d": torch.from_numpy(sc["means3d"]).to(dev),
+                "features_dc": torch.from_numpy(sc["dc"]).to(dev),
+                "features_rest": torch.from_numpy(sc["sh"]).to(dev),
+                "opacity_logits": torch.from_numpy(np.log(opac / (1 - opac)).astype(np.float32)
+                                                   .reshape(-1, 1)).to(dev),
+                "log_scales": torch.from_numpy(np.log(sc["scales"]).astype(np.float32)).to(dev),
+                "rotations": torch.from_numpy(sc["rotations"]).to(dev)}
+
+    zeros_mm = torch.zeros(HW, dtype=torch.int32, device=dev)
+
+    def render(ts, idx, degree, metric_map=None, vsp=None):
+        d = ts.render_inputs(cam_in[idx])
+        d["metric_map"] = metric_map if metric_map is not None else zeros_mm
+        if vsp is not None:
+            d["viewspace_points"] = vsp
+        cm = cams[idx]
+        return fastgs_core.rasterize_gaussians(d, W, H, 16, 16, cm.tan_fovx, cm.tan_fovy, degree,
+                                               get_flag=metric_map is not None)
+
+    # targets: the hidden scene rendered at full SH degree (untimed)
+    hidden = GaussianTrainState(to_params(syn.scene_config2(c["hidden_seed"], c["P_hidden"], deg)))
+    with torch.no_grad():
+        targets = [render(hidden, i, deg)["out_color"].detach().reshape(3, HW).clone()
+                   for i in range(len(cams))]
+    del hidden
+    start = reference_init(torch, dev, c["start_seed"], c["P_start"], deg)
+    dcfg = DensifyConfig(grad_thresh=c["grad_thresh"])
+    mse_until, sh_interval = c["mse_until"], 1000
+
+    def loop(n_iter, record, interval):
+        ts = GaussianTrainState(start)
+        extent = compute_scene_extent(ts.param("means3d").detach())
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(5)
+        rng = np.random.default_rng(42)
+        stack = []
+        losses = torch.zeros(max(n_iter, 1), device=dev)
+        events = []
+        for it in range(1, n_iter + 1):
+            ts.update_learning_rate(it)
+            active = min(it // sh_interval, deg)
+            if not stack:
+                stack = list(range(len(cams)))
+            idx = stack.pop(int(rng.integers(0, len(stack))))
+            vsp = torch.zeros((ts.P, 4), device=dev, requires_grad=True)
+            out = render(ts, idx, active, vsp=vsp)
+            diff = out["out_color"].reshape(3, HW) - targets[idx]
+            loss = (diff * diff).mean() if it <= mse_until else diff.abs().mean()
+            ts.zero_grad()
+            loss.backward()
+            losses[it - 1] = loss.detach()
+            ts.update_densification_stats(out["radii"], vsp.grad)
+            ts.step(it)
+            if it % interval == 0:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                ids = rng.choice(len(cams), size=min(dcfg.densify_camera_sample, len(cams)),
+                                 replace=False)
+                with torch.no_grad():
+                    imp, prn = ts.compute_gaussian_scores_fastgs(
+                        lambda i, mm: render(ts, i, active, metric_map=mm), targets,
+                        [int(i) for i in ids], dcfg.loss_thresh, True)
+                before = ts.P
+                info = ts.densify_and_prune_fastgs(dcfg, extent, imp, prn, generator=gen)
+                e1.record()
+                if record:
+                    events.append(dict(iteration=it, before=before, after=ts.P, start=e0,
+                                       end=e1, **{k: info[k] for k in (
+                                           "metric_hits", "cloned", "split_sources",
+                                           "total_prune_candidates", "actual_removed")}))
+        return ts, losses, events
+
+    # warm-up on a throwaway state, its last iteration a densification
+    loop(max(args.warmup, 1), False, max(args.warmup, 1))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ts, losses, events = loop(iterations, True, c["interval"])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    dens_ms = [e.pop("start").elapsed_time(e.pop("end")) for e in events]
+    for e, ms in zip(events, dens_ms):
+        e["ms"] = ms
+    lh = losses.cpu().numpy()
+    k = max(1, min(20, iterations // 5))
+    result = {
+        "metric": f"densification-loop iters/s ({args.config})", "value": iterations / dt,
+        "unit": "iters/s", "n_gpus": 1, "steps": iterations, "warmup": args.warmup,
+        "ms_per_step": dt * 1e3 / max(iterations, 1), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": c["desc"], "gaussians_start": c["P_start"],
+                   "gaussians_hidden": c["P_hidden"], "width": W, "height": H,
+                   "sh_degree": deg, "cameras": c["cameras"], "interval": c["interval"],
+                   "grad_thresh": c["grad_thresh"], "mse_until": c["mse_until"]},
+        "final_gaussians": ts.P, "capacity": ts.capacity, "reallocations": ts.reallocations,
+        "densify_events": events, "densify_ms_total": float(sum(dens_ms)),
+        "train_ms_per_iter": (dt * 1e3 - float(sum(dens_ms))) / max(iterations, 1),
+        "loss_first": float(lh[:k].mean()), "loss_last": float(lh[iterations - k:iterations].mean()),
+    }
+    print(json.dumps(result), flush=True)
+
+
 class StageTimer:
     """Event pairs recorded on the launch stream around each C-ABI stage.
     A stage entered more than once in one step (binning: the depth order, then
@@ -228,9 +396,10 @@ def cpu_baseline(cfg, sc, cams, seed=0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 20; the cfg5 loop runs its 500 iterations)")
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg5", "cfg5-grow"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-profile", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -241,6 +410,11 @@ def main():
                                    "for this build (see DESIGN.md: how the path would shard)",
                           "n_gpus": args.gpus}), flush=True)
         sys.exit(2)
+    if args.config in ("cfg5", "cfg5-grow"):
+        run_densify_loop(args)
+        return
+    if args.steps is None:
+        args.steps = 20
 
     import torch
     import torch.nn.functional as F
