@@ -299,64 +299,136 @@ __device__ __forceinline__ float unord_f(uint32_t u) {
   return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
 }
 
-// Workspace of the metric map: HW floats (L1 map), then reduction words.
+// Wave-wide float min / max / double sum (butterfly; every lane ends with the
+// result).  fminf / fmaxf drop NaN operands, as the restatement's scan does.
+__device__ __forceinline__ void wave_min_max(float& mn, float& mx) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, o, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  }
+}
+__device__ __forceinline__ double wave_sum_f64(double x) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+// Metric-map workspace: the per-pixel L1 map, then one (sum, min, max)
+// partial per block, then the reduced (min, max).
+constexpr int kMetricT = 256;
+constexpr int kMetricPix = 4;  // pixels per thread, kMetricT apart
+constexpr int64_t kMetricBlockPix = (int64_t)kMetricT * kMetricPix;
 struct MetricWs {
   float* map;
-  uint32_t* minmax;  // [0] ord(min), [1] ord(max)
-  double* sums;      // per-block partial sums of |pred - target|
+  double* bsum;
+  float* bmin;
+  float* bmax;
+  float* stat;  // [0] min, [1] max
 };
 
-// l = (|p0 - t0| + |p1 - t1| + |p2 - t2|) / C per pixel (l1_map_chw), its
-// min and max, and per-block sums of every |pred - target|.
-__global__ void __launch_bounds__(256)
-metric_l1_kernel(int32_t C, int64_t HW, const float* __restrict__ pred,
+__host__ __device__ inline int64_t metric_blocks(int64_t HW) {
+  return (HW + kMetricBlockPix - 1) / kMetricBlockPix;
+}
+
+// l = (|p0 - t0| + |p1 - t1| + ...) / C per pixel (l1_map_chw, :262-270),
+// and per block: the sum of every |pred - target| (double), min l, max l.
+template <int kC>
+__global__ void __launch_bounds__(kMetricT)
+metric_l1_kernel(int32_t C_rt, int64_t HW, const float* __restrict__ pred,
                  const float* __restrict__ target, MetricWs ws) {
-  __shared__ double s_sum[256 / kWave];
-  __shared__ uint32_t s_mm[2];
-  if (threadIdx.x == 0) {
-    s_mm[0] = 0xFFFFFFFFu;
-    s_mm[1] = 0u;
-  }
-  __syncthreads();
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  __shared__ double s_sum[kMetricT / kWave];
+  __shared__ float s_mn[kMetricT / kWave], s_mx[kMetricT / kWave];
+  const int C = kC > 0 ? kC : C_rt;
+  const int64_t base = (int64_t)blockIdx.x * kMetricBlockPix + threadIdx.x;
   double part = 0.0;
-  if (p < HW) {
-    float acc = 0.0f;
-    for (int c = 0; c < C; ++c) {
-      const float d = fabsf(pred[(size_t)c * HW + p] - target[(size_t)c * HW + p]);
-      acc = acc + d;
-      part += (double)d;
+  float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kMetricPix; ++k) {
+    const int64_t p = base + (int64_t)k * kMetricT;
+    if (p < HW) {
+      float acc = 0.0f;
+      for (int c = 0; c < C; ++c) {
+        const float d = fabsf(pred[(size_t)c * HW + p] - target[(size_t)c * HW + p]);
+        acc = acc + d;
+        part += (double)d;
+      }
+      const float l = acc / (float)C;
+      ws.map[p] = l;
+      mn = fminf(mn, l);
+      mx = fmaxf(mx, l);
     }
-    const float l = acc / (float)C;
-    ws.map[p] = l;
-    atomicMin(&s_mm[0], ord_f(l));
-    atomicMax(&s_mm[1], ord_f(l));
   }
-  for (int o = kWave / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, kWave);
-  if (lane_id() == 0) s_sum[threadIdx.x / kWave] = part;
+  part = wave_sum_f64(part);
+  wave_min_max(mn, mx);
+  const int w = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    s_sum[w] = part;
+    s_mn[w] = mn;
+    s_mx[w] = mx;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double b = 0.0;
-    for (int w = 0; w < 256 / kWave; ++w) b += s_sum[w];
-    ws.sums[blockIdx.x] = b;
-    atomicMin(&ws.minmax[0], s_mm[0]);
-    atomicMax(&ws.minmax[1], s_mm[1]);
+    double b = s_sum[0];
+    float bmn = s_mn[0], bmx = s_mx[0];
+    for (int i = 1; i < kMetricT / kWave; ++i) {
+      b += s_sum[i];
+      bmn = fminf(bmn, s_mn[i]);
+      bmx = fmaxf(bmx, s_mx[i]);
+    }
+    ws.bsum[blockIdx.x] = b;
+    ws.bmin[blockIdx.x] = bmn;
+    ws.bmax[blockIdx.x] = bmx;
   }
 }
 
-// metric_map = (l - min) / max(max - min, 1e-6) > loss_thresh, and the mean
-// photometric loss (block 0 sums the partial sums in a fixed order).
-__global__ void __launch_bounds__(256)
-metric_map_kernel(int32_t C, int64_t HW, int64_t nblocks, float loss_thresh, MetricWs ws,
-                  int32_t* __restrict__ metric_map, float* __restrict__ loss) {
-  const float mn = unord_f(ws.minmax[0]), mx = unord_f(ws.minmax[1]);
+// One block: the block partials reduced in a fixed order (so the loss is the
+// same on every run), min / max to ws.stat, loss = sum / (C * HW).
+__global__ void __launch_bounds__(kMetricT)
+metric_reduce_kernel(int64_t nb, int64_t count, MetricWs ws, float* __restrict__ loss) {
+  __shared__ double s_sum[kMetricT / kWave];
+  __shared__ float s_mn[kMetricT / kWave], s_mx[kMetricT / kWave];
+  double part = 0.0;
+  float mn = INFINITY, mx = -INFINITY;
+  for (int64_t b = threadIdx.x; b < nb; b += kMetricT) {
+    part += ws.bsum[b];
+    mn = fminf(mn, ws.bmin[b]);
+    mx = fmaxf(mx, ws.bmax[b]);
+  }
+  part = wave_sum_f64(part);
+  wave_min_max(mn, mx);
+  const int w = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    s_sum[w] = part;
+    s_mn[w] = mn;
+    s_mx[w] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = s_sum[0];
+    float bmn = s_mn[0], bmx = s_mx[0];
+    for (int i = 1; i < kMetricT / kWave; ++i) {
+      s += s_sum[i];
+      bmn = fminf(bmn, s_mn[i]);
+      bmx = fmaxf(bmx, s_mx[i]);
+    }
+    ws.stat[0] = bmn;
+    ws.stat[1] = bmx;
+    *loss = (float)(s / (double)count);
+  }
+}
+
+// metric_map = (l - min) / max(max - min, 1e-6) > loss_thresh
+// (normalized_positive_map, :262-270).
+__global__ void __launch_bounds__(kMetricT)
+metric_map_kernel(int64_t HW, float loss_thresh, MetricWs ws, int32_t* __restrict__ metric_map) {
+  const float mn = ws.stat[0], mx = ws.stat[1];
   const float dn = fmaxf(mx - mn, 1.0e-6f);
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p < HW) metric_map[p] = ((ws.map[p] - mn) / dn > loss_thresh) ? 1 : 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    double s = 0.0;
-    for (int64_t b = 0; b < nblocks; ++b) s += ws.sums[b];
-    *loss = (float)(s / (double)((int64_t)C * HW));
+  const int64_t base = (int64_t)blockIdx.x * kMetricBlockPix + threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < kMetricPix; ++k) {
+    const int64_t p = base + (int64_t)k * kMetricT;
+    if (p < HW) metric_map[p] = ((ws.map[p] - mn) / dn > loss_thresh) ? 1 : 0;
   }
 }
 
@@ -372,23 +444,36 @@ score_accumulate_kernel(int32_t P, const int32_t* __restrict__ metric_count,
   score[i] = score[i] + (*loss) * mc;
 }
 
-__global__ void __launch_bounds__(256)
+// min / max of x[0..P) into mm (ordered-int atomics, one pair per block; the
+// result does not depend on the order).
+__global__ void __launch_bounds__(kMetricT)
 minmax_kernel(int32_t P, const float* __restrict__ x, uint32_t* __restrict__ mm) {
-  __shared__ uint32_t s_mm[2];
-  if (threadIdx.x == 0) {
-    s_mm[0] = 0xFFFFFFFFu;
-    s_mm[1] = 0u;
+  __shared__ float s_mn[kMetricT / kWave], s_mx[kMetricT / kWave];
+  const int64_t base = (int64_t)blockIdx.x * kMetricBlockPix + threadIdx.x;
+  float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kMetricPix; ++k) {
+    const int64_t i = base + (int64_t)k * kMetricT;
+    if (i < P) {
+      mn = fminf(mn, x[i]);
+      mx = fmaxf(mx, x[i]);
+    }
+  }
+  wave_min_max(mn, mx);
+  const int w = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    s_mn[w] = mn;
+    s_mx[w] = mx;
   }
   __syncthreads();
-  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (i < P) {
-    atomicMin(&s_mm[0], ord_f(x[i]));
-    atomicMax(&s_mm[1], ord_f(x[i]));
-  }
-  __syncthreads();
   if (threadIdx.x == 0) {
-    atomicMin(&mm[0], s_mm[0]);
-    atomicMax(&mm[1], s_mm[1]);
+    float bmn = s_mn[0], bmx = s_mx[0];
+    for (int i = 1; i < kMetricT / kWave; ++i) {
+      bmn = fminf(bmn, s_mn[i]);
+      bmx = fmaxf(bmx, s_mx[i]);
+    }
+    atomicMin(&mm[0], ord_f(bmn));
+    atomicMax(&mm[1], ord_f(bmx));
   }
 }
 
@@ -603,9 +688,29 @@ extern "C" int32_t fgs_opacity_cap(int32_t P, float cap, float* opacity_logits, 
   return check_launch("opacity_cap_kernel");
 }
 
+static size_t metric_ws_layout(int64_t HW, MetricWs* ws, char* w) {
+  const int64_t nb = metric_blocks(HW);
+  size_t off = (size_t)((HW * 4 + 255) & ~255);
+  const size_t o_sum = off;
+  off += (size_t)((nb * 8 + 255) & ~255);
+  const size_t o_min = off;
+  off += (size_t)((nb * 4 + 255) & ~255);
+  const size_t o_max = off;
+  off += (size_t)((nb * 4 + 255) & ~255);
+  const size_t o_stat = off;
+  off += 256;
+  if (ws) {
+    ws->map = (float*)w;
+    ws->bsum = (double*)(w + o_sum);
+    ws->bmin = (float*)(w + o_min);
+    ws->bmax = (float*)(w + o_max);
+    ws->stat = (float*)(w + o_stat);
+  }
+  return off;
+}
+
 extern "C" size_t fgs_metric_map_workspace_bytes(int64_t HW) {
-  const int64_t nb = (HW + 255) / 256;
-  return (size_t)(((HW * 4 + 255) & ~255) + 256 + nb * 8);
+  return HW > 0 ? metric_ws_layout(HW, nullptr, nullptr) : 0;
 }
 
 extern "C" int32_t fgs_metric_map(int32_t C, int64_t HW, const float* pred, const float* target,
@@ -615,18 +720,20 @@ extern "C" int32_t fgs_metric_map(int32_t C, int64_t HW, const float* pred, cons
   if (!pred || !target || !workspace || !metric_map || !photometric_loss)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_metric_map: null pointer");
   hipStream_t st = (hipStream_t)stream;
-  char* w = (char*)workspace;
   MetricWs ws;
-  ws.map = (float*)w;
-  ws.minmax = (uint32_t*)(w + ((HW * 4 + 255) & ~255));
-  ws.sums = (double*)(w + ((HW * 4 + 255) & ~255) + 256);
-  const int64_t nb = (HW + 255) / 256;
-  fgs_fill_u32(ws.minmax, 0xFFFFFFFFu, 1, stream);
-  fgs_fill_u32(ws.minmax + 1, 0u, 1, stream);
-  hipLaunchKernelGGL(metric_l1_kernel, dim3((unsigned)nb), dim3(256), 0, st, C, HW, pred, target,
-                     ws);
-  hipLaunchKernelGGL(metric_map_kernel, dim3((unsigned)nb), dim3(256), 0, st, C, HW, nb,
-                     loss_thresh, ws, metric_map, photometric_loss);
+  metric_ws_layout(HW, &ws, (char*)workspace);
+  const int64_t nb = metric_blocks(HW);
+  if (nb > 0x7FFFFFFF) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_metric_map: HW too large");
+  if (C == 3)
+    hipLaunchKernelGGL(metric_l1_kernel<3>, dim3((unsigned)nb), dim3(kMetricT), 0, st, C, HW,
+                       pred, target, ws);
+  else
+    hipLaunchKernelGGL(metric_l1_kernel<0>, dim3((unsigned)nb), dim3(kMetricT), 0, st, C, HW,
+                       pred, target, ws);
+  hipLaunchKernelGGL(metric_reduce_kernel, dim3(1), dim3(kMetricT), 0, st, nb, (int64_t)C * HW,
+                     ws, photometric_loss);
+  hipLaunchKernelGGL(metric_map_kernel, dim3((unsigned)nb), dim3(kMetricT), 0, st, HW,
+                     loss_thresh, ws, metric_map);
   return check_launch("metric_map");
 }
 
@@ -652,7 +759,8 @@ extern "C" int32_t fgs_score_finalize(int32_t P, int32_t n_cams, const float* co
   hipStream_t st = (hipStream_t)stream;
   fgs_fill_u32(minmax_ws, 0xFFFFFFFFu, 1, stream);
   fgs_fill_u32(minmax_ws + 1, 0u, 1, stream);
-  hipLaunchKernelGGL(minmax_kernel, dim3(blocks_for(P)), dim3(256), 0, st, P, score, minmax_ws);
+  hipLaunchKernelGGL(minmax_kernel, dim3((unsigned)metric_blocks(P)), dim3(kMetricT), 0, st, P,
+                     score, minmax_ws);
   hipLaunchKernelGGL(score_finalize_kernel, dim3(blocks_for(P)), dim3(256), 0, st, P, n_cams,
                      minmax_ws, counts, score, importance, pruning);
   return check_launch("score_finalize");
