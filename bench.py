@@ -134,24 +134,16 @@ DENSIFY_GROW = dict(DENSIFY_LOOP, grad_thresh=1.0e-6,
 
 
 def reference_init(torch, dev, seed, P, degree):
-    """The reference's starting model (init_model, train_scanner_fixed.py:601-631)
-    on seeded points and colours: points N(0,1)^3 clipped to [-2,2] (the scene
-    distribution of the other configs), colours U(0,1); isotropic scale 0.02,
-    identity rotations, opacity 0.82, DC = (colour - 0.5) / C0, higher SH 0."""
+    """The reference's starting model (``scanner.init_model``,
+    train_scanner_fixed.py:601-631) on seeded points N(0,1)^3 clipped to
+    [-2,2] (the scene distribution of the other configs) and colours U(0,1)."""
+    from fastgs_core_amd import scanner
+
     rng = np.random.default_rng(seed)
     pts = np.clip(rng.standard_normal((P, 3)), -2.0, 2.0).astype(np.float32)
     colors = rng.uniform(0.0, 1.0, (P, 3)).astype(np.float32)
-    M = (degree + 1) ** 2 - 1
-    rot = np.zeros((P, 4), np.float32)
-    rot[:, 0] = 1.0
-    lg = np.float32(math.log(0.82 / (1.0 - 0.82)))
-    return {"means3d": torch.from_numpy(pts).to(dev),
-            "features_dc": torch.from_numpy(((colors - 0.5) / 0.28209479177387814)
-                                            .astype(np.float32)).to(dev),
-            "features_rest": torch.zeros((P, M, 3), device=dev),
-            "opacity_logits": torch.full((P, 1), float(lg), device=dev),
-            "log_scales": torch.full((P, 3), math.log(0.02), device=dev),
-            "rotations": torch.from_numpy(rot).to(dev)}
+    return {k: torch.from_numpy(v).to(dev)
+            for k, v in scanner.init_model(pts, colors, degree).items()}
 
 
 def run_densify_loop(args):
