@@ -293,21 +293,38 @@ radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* 
   __shared__ uint32_t s_h[8][256];
   for (int p = 0; p < pl.passes; ++p) s_h[p][threadIdx.x] = 0;
   __syncthreads();
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kThreads) {
-    K k;
-    if (kDepthKeys) {
-      const uint32_t dk = tiles_touched[i] ? __float_as_uint(depths[i]) : 0xFFFFFFFFu;
-      dkeys_out[i] = dk;
-      k = (K)dk;
-    } else {
-      k = keys[i];
+  // Grid-stride in batches of kHistBatch keys per thread, all loaded before
+  // the first is counted (clamped indices, so the loads carry no branch).
+  constexpr int kHistBatch = 16;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 < n;
+       i0 += stride * kHistBatch) {
+    K kk[kHistBatch];
+#pragma unroll
+    for (int b = 0; b < kHistBatch; ++b) {
+      const int64_t i = i0 + b * stride;
+      const int64_t ci = i < n ? i : n - 1;
+      if (kDepthKeys) {
+        const uint32_t tt = tiles_touched[ci];
+        const uint32_t db = __float_as_uint(depths[ci]);
+        kk[b] = (K)(tt ? db : 0xFFFFFFFFu);
+      } else {
+        kk[b] = keys[ci];
+      }
     }
-    int shift = pl.begin;
-    for (int p = 0; p < pl.passes; ++p) {
-      const uint32_t d = (uint32_t)(k >> shift) & ((1u << pl.bits[p]) - 1u);
-      atomicAdd(&s_h[p][d], 1u);
-      shift += pl.bits[p];
+#pragma unroll
+    for (int b = 0; b < kHistBatch; ++b) {
+      const int64_t i = i0 + b * stride;
+      if (i < n) {
+        const K k = kk[b];
+        if (kDepthKeys) dkeys_out[i] = (uint32_t)k;
+        int shift = pl.begin;
+        for (int p = 0; p < pl.passes; ++p) {
+          const uint32_t d = (uint32_t)(k >> shift) & ((1u << pl.bits[p]) - 1u);
+          atomicAdd(&s_h[p][d], 1u);
+          shift += pl.bits[p];
+        }
+      }
     }
   }
   __syncthreads();
@@ -345,12 +362,30 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   K key[kItems];
   uint32_t val[kItems];
   uint32_t rank[kItems];
+  // Every load is issued before the first ranking step (indices past the end
+  // are clamped to the last element, so the loads carry no branch); ranking
+  // item by item through LDS would otherwise wait out one memory latency per
+  // item.
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int64_t idx = base + it * kWave + lane;
+    key[it] = keys_in[idx < n ? idx : n - 1];
+  }
+  if (vals_in) {  // uniform
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int64_t idx = base + it * kWave + lane;
+      val[it] = vals_in[idx < n ? idx : n - 1];
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) val[it] = (uint32_t)(base + it * kWave + lane);
+  }
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
     const int64_t idx = base + it * kWave + lane;
     const bool valid = idx < n;
-    key[it] = valid ? keys_in[idx] : (K)0;
-    val[it] = valid ? (vals_in ? vals_in[idx] : (uint32_t)idx) : 0u;
+    if (!valid) key[it] = (K)0;
     const uint32_t d = (uint32_t)(key[it] >> shift) & mask;
     uint64_t peers = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
