@@ -23,6 +23,7 @@ There is no CPU fallback: without a ROCm GPU every entry point raises.
 from __future__ import annotations
 
 import ctypes
+import threading
 from typing import Any, Dict, Optional
 
 import numpy as np
@@ -104,7 +105,15 @@ def _p(t: Optional[torch.Tensor]):
     return t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev: torch.device):
+    """The current stream of ``dev`` as the C ABI's void* (the raw handle
+    lookup skips building a torch Stream object on every call)."""
+    if _raw_stream is not None:
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        return ctypes.c_void_p(_raw_stream(idx))
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
@@ -336,9 +345,10 @@ def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: f
     T = gx * gy
     keys = torch.empty(K, dtype=torch.int64, device=dev)
     plist = torch.empty(K, dtype=torch.int32, device=dev)
-    ranges = torch.empty((T, 2), dtype=torch.int32, device=dev)
-    bucket_count = torch.empty(T, dtype=torch.int32, device=dev)
-    bucket_offsets = torch.empty(T, dtype=torch.int32, device=dev)
+    tbuf = torch.empty(4 * T, dtype=torch.int32, device=dev)  # ranges, counts, offsets
+    ranges = tbuf[: 2 * T].view(T, 2)
+    bucket_count = tbuf[2 * T: 3 * T]
+    bucket_offsets = tbuf[3 * T:]
     ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
     io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
                         _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws),
@@ -355,21 +365,37 @@ def _last_u32(t: torch.Tensor) -> int:
     return int(t[-1].item()) & 0xFFFFFFFF
 
 
+class _ReadSlots(threading.local):
+    """Per-thread pinned 4-byte slots and events for the asynchronous reads,
+    reused from call to call (two can be in flight: K and B)."""
+
+    def __init__(self):
+        self.free = []
+
+
+_READ_SLOTS = _ReadSlots()
+
+
 def _last_u32_async(t: torch.Tensor):
     """read_last_u32 split in two: the 4-byte copy to pinned host memory and an
     event are queued now, the value is read by _wait_u32. Work queued in
     between runs on the GPU while the host waits."""
-    host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    if _READ_SLOTS.free:
+        host, view, ev = _READ_SLOTS.free.pop()
+    else:
+        host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        view, ev = host.numpy(), torch.cuda.Event()
     host.copy_(t[-1:], non_blocking=True)
-    ev = torch.cuda.Event()
     ev.record(torch.cuda.current_stream(t.device))
-    return host, ev
+    return host, view, ev
 
 
 def _wait_u32(pending) -> int:
-    host, ev = pending
+    _, view, ev = pending
     ev.synchronize()
-    return int(host[0]) & 0xFFFFFFFF
+    v = int(view[0]) & 0xFFFFFFFF
+    _READ_SLOTS.free.append(pending)
+    return v
 
 
 def _count_and_depth_order(point_offsets, depths, tiles):
@@ -501,23 +527,15 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     gx, gy = cfg["gx"], cfg["gy"]
     T = gx * gy
     point_offsets = _inclusive_scan_i32(tiles)
+    # the zero-count metric array is made before the wait for K: the host work
+    # between K's arrival and the binning launch is on the GPU's critical path
+    metric_count = torch.zeros(P if get_flag else 0, dtype=torch.int32, device=dev)
+    background = _to(inputs["background"], dev, torch.float32)
+    metric_map = _to(inputs["metric_map"], dev, torch.int32)
     K, depth_ws = _count_and_depth_order(point_offsets, depths.detach(), tiles)
-    i32 = dict(dtype=torch.int32, device=dev)
-    f32 = dict(dtype=torch.float32, device=dev)
-    point_list_keys = torch.zeros(0, dtype=torch.int64, device=dev)
-    point_list = torch.zeros(0, **i32)
-    ranges = torch.zeros((0, 2), **i32)
-    bucket_count = torch.zeros(0, **i32)
-    bucket_offsets = torch.zeros(0, **i32)
-    bucket_to_tile = torch.zeros(0, **i32)
-    sampled_t = torch.zeros(0, **f32)
-    sampled_ar = torch.zeros(0, **f32)
-    final_t = torch.zeros(0, **f32)
-    n_contrib = torch.zeros(0, **i32)
-    max_contrib = torch.zeros(0, **i32)
-    pixel_colors = torch.zeros(0, **f32)
-    out_color = torch.zeros(0, **f32)
-    metric_count = torch.zeros(P if get_flag else 0, **i32)
+    point_list_keys = point_list = ranges = bucket_count = bucket_offsets = None
+    bucket_to_tile = sampled_t = sampled_ar = final_t = n_contrib = max_contrib = None
+    pixel_colors = out_color = None
     B = 0
     if K > 0:
         with torch.no_grad():
@@ -536,8 +554,6 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
             pending_b = _last_u32_async(bucket_offsets)
             B = (K + 31 * T) // 32
         if B > 0:
-            background = _to(inputs["background"], dev, torch.float32)
-            metric_map = _to(inputs["metric_map"], dev, torch.int32)
             rcfg = dict(W=cfg["W"], H=cfg["H"], C=3, T=T, B=B, get_flag=bool(get_flag),
                         write_sampled=ws)
             (bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib, max_contrib,
@@ -546,7 +562,25 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
                 metric_map, metric_count, vsp_out)
         if pending_b is not None:
             B = _wait_u32(pending_b)
-            bucket_to_tile = bucket_to_tile[:B]
+            if bucket_to_tile is not None:
+                bucket_to_tile = bucket_to_tile[:B]
+    if point_list is None or final_t is None:  # nothing rendered: the reference's empty outputs
+        i32 = dict(dtype=torch.int32, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        if point_list is None:
+            point_list_keys = torch.zeros(0, dtype=torch.int64, device=dev)
+            point_list = torch.zeros(0, **i32)
+            ranges = torch.zeros((0, 2), **i32)
+            bucket_count = torch.zeros(0, **i32)
+            bucket_offsets = torch.zeros(0, **i32)
+        bucket_to_tile = torch.zeros(0, **i32)
+        sampled_t = torch.zeros(0, **f32)
+        sampled_ar = torch.zeros(0, **f32)
+        final_t = torch.zeros(0, **f32)
+        n_contrib = torch.zeros(0, **i32)
+        max_contrib = torch.zeros(0, **i32)
+        pixel_colors = torch.zeros(0, **f32)
+        out_color = torch.zeros(0, **f32)
     return {
         "rendered": K, "num_buckets": B, "out_color": out_color, "radii": radii,
         "point_offsets": point_offsets, "ranges": ranges, "bucket_count": bucket_count,
