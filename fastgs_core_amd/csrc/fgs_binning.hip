@@ -217,17 +217,44 @@ static size_t scan_ws_bytes(int64_t n) { return scan_state_bytes(n); }
 // Fill / copy helpers (kernels rather than hipMemsetAsync so that callers may
 // capture these calls in HIP graphs).
 // ---------------------------------------------------------------------------
-__global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    dst[i] = value;
+// Up to kFillSpans arrays filled with one value in one launch: 16-byte stores
+// from each array's first 16-byte boundary, single words for the ends.
+__global__ void __launch_bounds__(256) fill_spans_kernel(FillSpans f) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+  const uint4 v4 = make_uint4(f.value, f.value, f.value, f.value);
+  for (int s = 0; s < f.count; ++s) {
+    uint32_t* p = f.p[s];
+    const int64_t n = f.n[s];
+    int64_t head = (int64_t)(((16u - (uint32_t)(reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) >> 2);
+    if (head > n) head = n;
+    if (tid < head) p[tid] = f.value;
+    const int64_t nv = (n - head) >> 2;
+    uint4* q = reinterpret_cast<uint4*>(p + head);
+    for (int64_t i = tid; i < nv; i += nthreads) q[i] = v4;
+    const int64_t done = head + nv * 4;
+    if (tid < n - done) p[done + tid] = f.value;
+  }
+}
+
+void launch_fill_spans(const FillSpans& f, hipStream_t st) {
+  int64_t words = 0;
+  for (int s = 0; s < f.count; ++s) words += f.n[s] > 0 ? f.n[s] : 0;
+  if (words <= 0) return;
+  int64_t blocks = (words / 4 + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(fill_spans_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
 }
 
 static void launch_fill(uint32_t* dst, uint32_t v, int64_t n, hipStream_t st) {
   if (n <= 0) return;
-  int64_t blocks = (n + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, dst, v, n);
+  FillSpans f{};
+  f.p[0] = dst;
+  f.n[0] = n;
+  f.count = 1;
+  f.value = v;
+  launch_fill_spans(f, st);
 }
 
 // Scan with its state at `state` (scan_state_bytes(n), zeroed here unless

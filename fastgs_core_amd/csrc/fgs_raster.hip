@@ -528,28 +528,38 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
   hipStream_t st = (hipStream_t)stream;
   const int C = p->num_channels;
   const int NCH = C < 3 ? C : 3;
-  // Elements the kernel may leave unwritten are cleared first.
-  if (p->get_flag && p->num_points > 0)
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->metric_count), 0u, p->num_points, stream);
+  // Elements the kernel may leave unwritten are cleared first, in as few
+  // fill launches as possible.
+  FillSpans f{};
+  auto span = [&](void* ptr, int64_t n) {
+    if (n <= 0) return;
+    if (f.count == kFillSpans) {
+      launch_fill_spans(f, st);
+      f.count = 0;
+    }
+    f.p[f.count] = reinterpret_cast<uint32_t*>(ptr);
+    f.n[f.count] = n;
+    ++f.count;
+  };
+  if (p->get_flag && p->num_points > 0) span(io->metric_count, p->num_points);
   if (p->write_sampled && p->bucket_sum > 0) {
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->sampled_t), 0u, p->bucket_sum * 256, stream);
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->sampled_ar), 0u, p->bucket_sum * 256 * C, stream);
+    span(io->sampled_t, p->bucket_sum * 256);
+    span(io->sampled_ar, p->bucket_sum * 256 * C);
   }
   if (C > 3) {
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->pixel_colors) + 3 * HW, 0u, (C - 3) * HW, stream);
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->out_color) + 3 * HW, 0u, (C - 3) * HW, stream);
+    span(io->pixel_colors + 3 * HW, (C - 3) * HW);
+    span(io->out_color + 3 * HW, (C - 3) * HW);
   }
-  if (p->bucket_sum > 0)
-    fgs_fill_u32(io->bucket_to_tile, 0u, p->bucket_sum, stream);
+  if (p->bucket_sum > 0) span(io->bucket_to_tile, p->bucket_sum);
   if (tiles < gx * gy) {
     // Pixels of tiles beyond num_tiles are never rendered: clear them.
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->final_t), 0u, HW, stream);
-    fgs_fill_u32(io->n_contrib, 0u, HW, stream);
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->pixel_colors), 0u, C * HW, stream);
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->out_color), 0u, C * HW, stream);
+    span(io->final_t, HW);
+    span(io->n_contrib, HW);
+    span(io->pixel_colors, C * HW);
+    span(io->out_color, C * HW);
   }
-  if (p->num_tiles > tiles)
-    fgs_fill_u32(io->max_contrib + tiles, 0u, p->num_tiles - tiles, stream);
+  if (p->num_tiles > tiles) span(io->max_contrib + tiles, p->num_tiles - tiles);
+  if (f.count) launch_fill_spans(f, st);
   if (tiles == 0) return check_launch("rasterize_fwd");
   RasterShape sh{W, H, gx, gy};
   const int mode = (p->write_sampled && p->bucket_sum > 0 ? 1 : 0) | (p->get_flag ? 2 : 0);
@@ -573,10 +583,17 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   if (P > 0 && (!io->dL_dmeans2d || !io->dL_dcolors || !io->dL_dconic_opacity || !io->dL_dviewspace))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_rasterize_bwd: missing gradient tensor");
   hipStream_t st = (hipStream_t)stream;
-  if (P > 0) {
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->dL_dcolors), 0u, (int64_t)C * P, stream);
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->dL_dconic_opacity), 0u, 4 * (int64_t)P, stream);
-    fgs_fill_u32(reinterpret_cast<uint32_t*>(io->dL_dviewspace), 0u, 4 * (int64_t)P, stream);
+  if (P > 0) {  // the atomically accumulated gradients start at zero: one launch
+    FillSpans f{};
+    f.p[0] = reinterpret_cast<uint32_t*>(io->dL_dcolors);
+    f.n[0] = (int64_t)C * P;
+    f.p[1] = reinterpret_cast<uint32_t*>(io->dL_dconic_opacity);
+    f.n[1] = 4 * (int64_t)P;
+    f.p[2] = reinterpret_cast<uint32_t*>(io->dL_dviewspace);
+    f.n[2] = 4 * (int64_t)P;
+    f.count = 3;
+    f.value = 0u;
+    launch_fill_spans(f, st);
   }
   if (P == 0) return check_launch("rasterize_bwd");
   if (tiles == 0) {
