@@ -257,7 +257,9 @@ __device__ __forceinline__ void wave_reduce_terms(float (&v)[kGradTerms], float*
 // Gradient terms of one splat for the lane's four pixels (one per 16x4
 // strip), accumulated into v.  The blend decisions repeat the forward's
 // operations exactly (same power, exp and thresholds), so T recovery and the
-// set of contributing splats match it.
+// set of contributing splats match it.  (The hardware exp2 with an exact
+// fallback next to the thresholds measured slower: v_exp_f32 issues at a
+// quarter of the rate and the threshold test costs what it saves.)
 //
 // Per pixel the colour behind the splat enters only through
 // SdL = T_final * (bg . dL) + sum_c S_c dL_c (S_c: colour accumulated behind
@@ -276,19 +278,19 @@ __device__ __forceinline__ void wave_reduce_terms(float (&v)[kGradTerms], float*
 // whether any pixel of the wave blends the splat (wave-uniform); v is left
 // untouched otherwise.
 template <int NCH, bool kSafe>
-__device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, const float cz,
-                                                const float4 h, const float2 rows, const int jj,
-                                                const float pxf, const float pyf0,
-                                                const float ty0, const int (&nc)[4],
-                                                float (&T)[4], float (&SdL)[4],
-                                                const float (&dL)[4][3],
+__device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, const float4 cu,
+                                                const float4 h, const int jj, const float pxf,
+                                                const float pyf0, const float ty0,
+                                                const int (&nc)[4], float (&T)[4],
+                                                float (&SdL)[4], const float (&dL)[4][3],
                                                 float (&v)[kGradTerms]) {
   bool any = false;
+  const float dx = a.x - pxf;
+  const float dxdx = dx * dx;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const float strip_lo = ty0 + (float)(4 * k);
-    if (!(rows.y >= strip_lo && rows.x <= strip_lo + 3.0f)) continue;  // wave-uniform
-    const float dx = a.x - pxf;
+    if (!(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;  // wave-uniform
     const float dy = a.y - (pyf0 + (float)(4 * k));
     const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
     const float G = det_expf(power);
@@ -305,7 +307,7 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
     {
 #pragma clang fp contract(fast)
       const float aT = act ? alpha * Tj : 0.0f;
-      const float col[3] = {b.z, b.w, cz};
+      const float col[3] = {b.z, b.w, cu.w};
       float cdl = col[0] * dL[k][0];
 #pragma unroll
       for (int c = 1; c < NCH; ++c) cdl += col[c] * dL[k][c];
@@ -321,12 +323,14 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
       }
       const bool geo = act && !(oG > 0.99f);
       const float gm = geo ? G : 0.0f;
-      const float w = gm * (b.y * dL_dalpha);
-      const float tmp_x = -w * (h.x * dx + h.y * dy);
-      const float tmp_y = -w * (h.z * dy + h.w * dx);
-      const float hw = -0.5f * w;
-      const float t[8] = {tmp_x,       tmp_y,       fabsf(tmp_x), fabsf(tmp_y),
-                          hw * dx * dx, hw * dx * dy, hw * dy * dy, gm * dL_dalpha};
+      // w2 = -w/2 (cu.z = -o/2): the conic terms are w2 (dx^2, dx dy, dy^2)
+      // and the means2d terms -w (..) = 2 w2 (..), doubled when flushed.
+      const float w2 = gm * (cu.z * dL_dalpha);
+      const float tx = w2 * (h.x * dx + h.y * dy);
+      const float ty = w2 * (h.z * dy + h.w * dx);
+      const float w2dy = w2 * dy;
+      const float t[8] = {tx,          ty,          fabsf(tx), fabsf(ty),
+                          w2 * dxdx,   w2dy * dx,   w2dy * dy, gm * dL_dalpha};
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] += kSafe ? (geo ? t[i] : 0.0f) : t[i];
     }
@@ -354,8 +358,7 @@ __device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, 
     float v[kGradTerms];
 #pragma unroll
     for (int k = 0; k < kGradTerms; ++k) v[k] = -0.0f;
-    if (bwd_splat_terms<NCH, kSafe>(a, b, cu.w, hh, make_float2(cu.x, cu.y), lo + j, pxf, pyf0,
-                                    ty0, nc, T, SdL, dL, v))
+    if (bwd_splat_terms<NCH, kSafe>(a, b, cu, hh, lo + j, pxf, pyf0, ty0, nc, T, SdL, dL, v))
       wave_reduce_terms(v, s_rec + j * kRec, l);
   }
 }
@@ -368,7 +371,7 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
   __shared__ float4 s_a[kBwdBatch];
   __shared__ float4 s_b[kBwdBatch];
   __shared__ float4 s_h[kBwdBatch];     // conic scaled by (W/2, H/2)
-  __shared__ float4 s_cull[kBwdBatch];  // (row_lo, row_hi, -, colour 3)
+  __shared__ float4 s_cull[kBwdBatch];  // (row_lo, row_hi, -opacity/2, colour 3)
   __shared__ uint32_t s_g[kBwdBatch];
   __shared__ float s_rec[kBwdBatch * kRec];
   const int tile = (int)blockIdx.x;
@@ -436,7 +439,7 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
                        __builtin_isfinite(a.z) && __builtin_isfinite(a.w) &&
                        __builtin_isfinite(b.x) && __builtin_isfinite(b.y) &&
                        __builtin_isfinite(b.z) && __builtin_isfinite(b.w) && __builtin_isfinite(c);
-      s_cull[l] = make_float4(cu.x, cu.y, 0.0f, c);
+      s_cull[l] = make_float4(cu.x, cu.y, -0.5f * b.y, c);
     }
 #pragma unroll
     for (int i = 0; i < kRec; ++i) s_rec[i * kBwdBatch + l] = 0.0f;
@@ -463,7 +466,7 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
       const int q = i * kBwdBatch + l;
       const int s = q / kRec, t = q - (q / kRec) * kRec;
       if (s < cnt && t < 8 + NCH) {
-        const float w = s_rec[q];
+        const float w = t < 4 ? 2.0f * s_rec[q] : s_rec[q];  // means2d terms were halved
         const uint32_t g = s_g[s];
         if (w != 0.0f && g < (uint32_t)P) {
           float* dst = t < 4 ? io.dL_dviewspace + 4 * (size_t)g + t
