@@ -54,11 +54,15 @@ __device__ __forceinline__ void stage_splat(uint32_t g, uint32_t P, const float*
 
 // Rows [lo, hi] outside which no pixel of a splat can reach alpha >= 1/255.
 // alpha >= 1/255 needs o*exp(power) >= 1/255, i.e. q(d) = d^T Conic d <= tau =
-// 2 ln(255 o).  The row extent of {q <= tau} is sqrt(tau * a / det); it is
-// widened to tau' = 1.1 tau + 1 plus 2 pixels, which covers the rounding of
-// the hardware log and of the forward's exp.  Ill-conditioned or non-positive
-// conics, NaN opacities and non-finite centres are not culled; o < 0.999/255
-// never blends.
+// 2 ln(255 o).  The row extent of {q <= tau} is sqrt(tau * a / det).  Margins:
+// the float power of a pixel differs from -q/2 by at most ~7e-7 (a dx^2 +
+// c dy^2) <= 7e-7 q (1 + |rho|) / (1 - |rho|) < 3e-3 q for the conics culled
+// here (det > 1e-3 a c, rho = b / sqrt(a c)); the exp, the hardware log and
+// the product o*G move the threshold by ~1e-6; det loses at most ~6e-5 to
+// cancellation.  tau' = 1.01 tau + 0.05 and hy * 1.001 + 0.25 px cover all of
+// these several times over.  Ill-conditioned or non-positive conics, NaN
+// opacities and non-finite centres are not culled; o < 0.999/255 never
+// blends.
 __device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c, float o) {
   const float inf = __builtin_huge_valf();
   float2 r = make_float2(-inf, inf);
@@ -67,8 +71,8 @@ __device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c,
   const float tau = 2.0f * __logf(255.0f * o);
   const float det = a * c - b * b;
   if (!(a > 0.f) || !(c > 0.f) || !(det > 1e-3f * a * c)) return r;
-  const float tq = fmaxf(tau, 0.0f) * 1.1f + 1.0f;
-  const float hy = __builtin_sqrtf(tq * a / det) + 2.0f;
+  const float tq = fmaxf(tau, 0.0f) * 1.01f + 0.05f;
+  const float hy = __builtin_sqrtf(tq * a / det) * 1.001f + 0.25f;
   return make_float2(y - hy, y + hy);
 }
 
@@ -281,7 +285,8 @@ template <int NCH, bool kSafe>
 __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, const float4 cu,
                                                 const float4 h, const int jj, const float pxf,
                                                 const float pyf0, const float ty0,
-                                                const int (&nc)[4], float (&T)[4],
+                                                const int (&nc)[4], const int (&nc_max)[4],
+                                                float (&T)[4],
                                                 float (&SdL)[4], const float (&dL)[4][3],
                                                 float (&v)[kGradTerms]) {
   bool any = false;
@@ -289,6 +294,7 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
   const float dxdx = dx * dx;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
+    if (jj >= nc_max[k]) continue;  // every pixel of the strip ends before this splat
     const float strip_lo = ty0 + (float)(4 * k);
     if (!(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;  // wave-uniform
     const float dy = a.y - (pyf0 + (float)(4 * k));
@@ -348,7 +354,7 @@ __device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, 
                                           const float4* s_cull, float* s_rec, const int lo,
                                           const int cnt, const int l, const float pxf,
                                           const float pyf0, const float ty0, const int (&nc)[4],
-                                          float (&T)[4], float (&SdL)[4],
+                                          const int (&nc_max)[4], float (&T)[4], float (&SdL)[4],
                                           const float (&dL)[4][3]) {
   for (int j = cnt - 1; j >= 0; --j) {
     const float4 a = s_a[j];
@@ -358,7 +364,8 @@ __device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, 
     float v[kGradTerms];
 #pragma unroll
     for (int k = 0; k < kGradTerms; ++k) v[k] = -0.0f;
-    if (bwd_splat_terms<NCH, kSafe>(a, b, cu, hh, lo + j, pxf, pyf0, ty0, nc, T, SdL, dL, v))
+    if (bwd_splat_terms<NCH, kSafe>(a, b, cu, hh, lo + j, pxf, pyf0, ty0, nc, nc_max, T, SdL, dL,
+                                    v))
       wave_reduce_terms(v, s_rec + j * kRec, l);
   }
 }
@@ -410,6 +417,12 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
     lane_finite = lane_finite && __builtin_isfinite(SdL[k]) && __builtin_isfinite(T[k]);
   }
   const bool tile_finite = __ballot(!lane_finite) == 0ull;
+  // per strip, the largest contributor count of its pixels: splats at or
+  // beyond it reach no pixel of the strip (wave-uniform)
+  int nc_max[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    nc_max[k] = __builtin_amdgcn_readfirstlane((int)wave_max_u32((uint32_t)nc[k]));
   const float pxf = (float)px;
   const float pyf0 = (float)row0;
   const float ty0 = (float)(ty * kTile);
@@ -452,11 +465,11 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
     const bool fast = tile_finite && __ballot(!ok) == 0ull;
     __syncthreads();
     if (fast)
-      bwd_batch<NCH, false>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, T, SdL,
-                            dL);
+      bwd_batch<NCH, false>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, nc_max,
+                            T, SdL, dL);
     else
-      bwd_batch<NCH, true>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, T, SdL,
-                           dL);
+      bwd_batch<NCH, true>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, nc_max,
+                           T, SdL, dL);
     __syncthreads();
     // Flush: item q = (splat q/12, term q%12), so the lanes of one atomic
     // instruction cover the consecutive terms of about five splats.

@@ -713,6 +713,18 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
   const real ddelx_dx = (real)0.5 * (real)W;
   const real ddely_dy = (real)0.5 * (real)H;
   const int ntiles = gx * gy < rp->num_tiles ? gx * gy : rp->num_tiles;
+  /* The per-Gaussian sums are accumulated in double and added to the outputs
+   * once at the end: the parallel order of the additions (the reference's
+   * float atomics have none either) then moves the result by far less than a
+   * float ulp, so the oracle gives the same gradients on every run. */
+  size_t lmax = 0;
+  for (int tile = 0; tile < ntiles; ++tile)
+    if (ranges[2 * tile + 1] > lmax) lmax = ranges[2 * tile + 1];
+  uint32_t gn = 0;
+  for (size_t i = 0; i < lmax; ++i)
+    if (point_list[i] + 1 > gn) gn = point_list[i] + 1;
+  const int AW = 10 + NC; /* means2d 2, vsp 4, conic 4, colours NC */
+  double* acc = (double*)calloc((size_t)gn * AW + 1, sizeof(double));
 #pragma omp parallel
   {
     int cap = 0;
@@ -773,7 +785,7 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
               real col = colors[(size_t)g * NC + c];
               real dcol = alpha * Tj * dL[c];
 #pragma omp atomic
-              dcolors[(size_t)g * NC + c] += dcol;
+              acc[(size_t)g * AW + 10 + c] += (double)dcol;
               dL_dalpha += (col * Tj - rci * S[c]) * dL[c];
               S[c] += col * alpha * Tj;
             }
@@ -789,26 +801,27 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
             real v1 = (real)-0.5 * gdx * dy * dL_dG;
             real v2 = (real)-0.5 * gdy * dy * dL_dG;
             real v3 = G * dL_dalpha;
+            double* a = acc + (size_t)g * AW;
 #pragma omp atomic
-            dmeans2d[2 * (size_t)g + 0] += tmp_x;
+            a[0] += (double)tmp_x;
 #pragma omp atomic
-            dmeans2d[2 * (size_t)g + 1] += tmp_y;
+            a[1] += (double)tmp_y;
 #pragma omp atomic
-            dvsp[4 * (size_t)g + 0] += tmp_x;
+            a[2] += (double)tmp_x;
 #pragma omp atomic
-            dvsp[4 * (size_t)g + 1] += tmp_y;
+            a[3] += (double)tmp_y;
 #pragma omp atomic
-            dvsp[4 * (size_t)g + 2] += RABS(tmp_x);
+            a[4] += (double)RABS(tmp_x);
 #pragma omp atomic
-            dvsp[4 * (size_t)g + 3] += RABS(tmp_y);
+            a[5] += (double)RABS(tmp_y);
 #pragma omp atomic
-            dconic[4 * (size_t)g + 0] += v0;
+            a[6] += (double)v0;
 #pragma omp atomic
-            dconic[4 * (size_t)g + 1] += v1;
+            a[7] += (double)v1;
 #pragma omp atomic
-            dconic[4 * (size_t)g + 2] += v2;
+            a[8] += (double)v2;
 #pragma omp atomic
-            dconic[4 * (size_t)g + 3] += v3;
+            a[9] += (double)v3;
           }
         }
       }
@@ -816,6 +829,15 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
     free(rec_g);
     free(rec);
   }
+  for (uint32_t g = 0; g < gn; ++g) {
+    const double* a = acc + (size_t)g * AW;
+    dmeans2d[2 * (size_t)g + 0] += (real)a[0];
+    dmeans2d[2 * (size_t)g + 1] += (real)a[1];
+    for (int q = 0; q < 4; ++q) dvsp[4 * (size_t)g + q] += (real)a[2 + q];
+    for (int q = 0; q < 4; ++q) dconic[4 * (size_t)g + q] += (real)a[6 + q];
+    for (int c = 0; c < C; ++c) dcolors[(size_t)g * NC + c] += (real)a[10 + c];
+  }
+  free(acc);
 }
 
 /* ------------------------------------------------------------------------ */
