@@ -150,7 +150,7 @@ def run_densify_loop(args):
     """the training loop of train_scanner_fastgs.py:968-1060
     on the GPU state.  Per iteration: a camera popped from a seeded viewpoint
     stack, render at the active SH degree (0 below iteration 1000, +1 per
-    1000), MSE loss (the reference's loss up to --mse-until 600), backward,
+    1000), MSE loss (the reference's loss up to --mse-until 600; fused kernels), backward,
     the densification statistics from this render's radii and viewspace
     gradient, the learning-rate schedule and the FastGS Adam cadence.  Every
     ``interval`` iterations: the metric-map scores over 10 sampled cameras
@@ -159,6 +159,7 @@ def run_densify_loop(args):
     import torch
 
     import fastgs_core
+    import fastgs_core_amd
     from fastgs_core_amd import synthetic as syn
     from fastgs_core_amd.densify import DensifyConfig, GaussianTrainState, compute_scene_extent
 
@@ -222,8 +223,9 @@ def run_densify_loop(args):
             idx = stack.pop(int(rng.integers(0, len(stack))))
             vsp = torch.zeros((ts.P, 4), device=dev, requires_grad=True)
             out = render(ts, idx, active, vsp=vsp)
-            diff = out["out_color"].reshape(3, HW) - targets[idx]
-            loss = (diff * diff).mean() if it <= mse_until else diff.abs().mean()
+            img = out["out_color"].reshape(3, HW)
+            loss = (fastgs_core_amd.mse_loss(img, targets[idx]) if it <= mse_until
+                    else fastgs_core_amd.l1_loss(img, targets[idx]))
             ts.zero_grad()
             loss.backward()
             losses[it - 1] = loss.detach()

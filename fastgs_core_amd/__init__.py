@@ -11,7 +11,7 @@ from .densify import (  # noqa: F401
     OptimConfig,
     compute_scene_extent,
 )
-from .loss import l1_ssim_loss  # noqa: F401
+from .loss import l1_loss, l1_ssim_loss, mse_loss  # noqa: F401
 from .train import (  # noqa: F401
     FastGSOptimizerPolicy,
     FusedAdam,

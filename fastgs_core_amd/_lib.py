@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class PreprocessParams(Structure):
@@ -80,6 +80,11 @@ class RasterBwdIO(Structure):
         "dL_dconic_opacity", "dL_dviewspace")]
 
 
+class AdamGroup(Structure):  # fgs_adam_group
+    _fields_ = [("param", c_void_p), ("grad", c_void_p), ("exp_avg", c_void_p),
+                ("exp_avg_sq", c_void_p), ("n", c_int64), ("lr", c_float), ("step", c_int32)]
+
+
 class DensifyParams(Structure):
     _fields_ = [
         ("grad_thresh", c_float), ("grad_abs_thresh", c_float), ("clone_max_scale", c_float),
@@ -139,6 +144,13 @@ SIGNATURES = {
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fgs_adam_step": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_float, c_float,
                                 c_float, c_float, c_int32, c_int32, c_void_p]),
+    "fgs_adam_step_multi": (c_int32, [POINTER(AdamGroup), c_int32, c_float, c_float, c_float,
+                                      c_int32, c_void_p]),
+    "fgs_pointwise_loss_workspace_bytes": (c_size_t, [c_int64]),
+    "fgs_pointwise_loss_fwd": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p,
+                                         c_void_p, c_void_p]),
+    "fgs_pointwise_loss_bwd": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p,
+                                         c_void_p, c_void_p]),
     "fgs_densify_stats": (c_int32, [c_int32] + [c_void_p] * 7 + [c_void_p]),
     "fgs_densify_classify": (c_int32, [c_int32, POINTER(DensifyParams)] + [c_void_p] * 7
                              + [c_void_p]),

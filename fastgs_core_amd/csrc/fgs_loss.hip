@@ -261,6 +261,69 @@ static LossArgs make_args(int C, int H, int W, float w_l1, float w_ssim) {
   return a;
 }
 
+// Pointwise photometric losses of the training script's loss_fn
+// (scripts/train_scanner_fastgs.py:911-966): mean |x - y| (mode 0) or mean
+// (x - y)^2 (mode 1).  Each term is formed in float and summed in double:
+// per-block partials, then one block reduces them in a fixed order.
+constexpr int kPwItems = 8;  // elements per thread, 256 threads per block
+constexpr int64_t kPwBlock = 256 * kPwItems;
+
+__device__ __forceinline__ float pw_term(float x, float y, int mode) {
+  const float d = x - y;
+  return mode ? d * d : fabsf(d);
+}
+
+__global__ void __launch_bounds__(256)
+pointwise_loss_partials_kernel(const float* __restrict__ x, const float* __restrict__ y, int64_t n,
+                               int mode, double* __restrict__ partials) {
+  __shared__ double s_w[256 / kWave];
+  const int64_t base = (int64_t)blockIdx.x * kPwBlock + threadIdx.x;
+  double acc = 0.0;
+#pragma unroll
+  for (int k = 0; k < kPwItems; ++k) {
+    const int64_t i = base + (int64_t)k * 256;
+    if (i < n) acc += (double)pw_term(x[i], y[i], mode);
+  }
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, kWave);
+  if (lane_id() == 0) s_w[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double b = 0.0;
+    for (int w = 0; w < 256 / kWave; ++w) b += s_w[w];
+    partials[blockIdx.x] = b;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+pointwise_loss_reduce_kernel(const double* __restrict__ partials, int64_t nb, double inv_n,
+                             float* __restrict__ loss) {
+  __shared__ double s[256];
+  const int t = (int)threadIdx.x;
+  double acc = 0.0;
+  for (int64_t b = t; b < nb; b += 256) acc += partials[b];
+  s[t] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o) s[t] += s[t + o];
+    __syncthreads();
+  }
+  if (t == 0) loss[0] = (float)(s[0] * inv_n);
+}
+
+// dL/dx = g * sign(x - y) / n (mode 0; 0 where x == y) or g * 2 (x - y) / n.
+__global__ void __launch_bounds__(256)
+pointwise_loss_bwd_kernel(const float* __restrict__ x, const float* __restrict__ y, int64_t n,
+                          int mode, const float* __restrict__ grad_out, float inv_n,
+                          float* __restrict__ dx) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float g = (grad_out ? grad_out[0] : 1.0f) * inv_n;
+  const float d = x[i] - y[i];
+  const float s = mode ? 2.0f * d : (d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f));
+  dx[i] = g * s;
+}
+
 }  // namespace fgs
 
 using namespace fgs;
@@ -300,4 +363,36 @@ extern "C" int32_t fgs_l1_ssim_bwd(const float* img, const float* tgt, const flo
   hipLaunchKernelGGL(l1_ssim_bwd_kernel, dim3(nt, C), dim3(kSW), 0, (hipStream_t)stream, a, img,
                      tgt, dmaps, grad_out, dimg);
   return check_launch("l1_ssim_bwd");
+}
+
+extern "C" size_t fgs_pointwise_loss_workspace_bytes(int64_t n) {
+  const int64_t nb = (n + kPwBlock - 1) / kPwBlock;
+  return (size_t)((nb < 1 ? 1 : nb) * 8);
+}
+
+extern "C" int32_t fgs_pointwise_loss_fwd(const float* x, const float* y, int64_t n, int32_t mode,
+                                          void* workspace, float* loss, void* stream) {
+  if (n <= 0 || (mode != 0 && mode != 1))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_pointwise_loss_fwd: bad arguments");
+  if (!x || !y || !workspace || !loss)
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_pointwise_loss_fwd: null pointer");
+  const int64_t nb = (n + kPwBlock - 1) / kPwBlock;
+  if (nb > 0x7FFFFFFF) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_pointwise_loss_fwd: too large");
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(pointwise_loss_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, x, y, n,
+                     mode, (double*)workspace);
+  hipLaunchKernelGGL(pointwise_loss_reduce_kernel, dim3(1), dim3(256), 0, st,
+                     (const double*)workspace, nb, 1.0 / (double)n, loss);
+  return check_launch("pointwise_loss_fwd");
+}
+
+extern "C" int32_t fgs_pointwise_loss_bwd(const float* x, const float* y, int64_t n, int32_t mode,
+                                          const float* grad_out, float* dx, void* stream) {
+  if (n <= 0 || (mode != 0 && mode != 1))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_pointwise_loss_bwd: bad arguments");
+  if (!x || !y || !dx)
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_pointwise_loss_bwd: null pointer");
+  hipLaunchKernelGGL(pointwise_loss_bwd_kernel, dim3(ceil_div_u(n, 256)), dim3(256), 0,
+                     (hipStream_t)stream, x, y, n, mode, grad_out, (float)(1.0 / (double)n), dx);
+  return check_launch("pointwise_loss_bwd_kernel");
 }

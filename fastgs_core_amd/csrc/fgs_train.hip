@@ -100,6 +100,58 @@ adam_kernel(int64_t n, AdamArgs a, float* __restrict__ p, const float* __restric
     p[i] = p[i] - (a.step_size * mi) / (sqrtf(vi) + a.eps);
 }
 
+// Several tensors in one launch: the blocks of group k are [block_end[k-1],
+// block_end[k]); per-group step size and bias correction, the same update.
+constexpr int kAdamGroups = 8;
+struct AdamGroupDev {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  int64_t n;
+  float step_size, bc2_sqrt;
+};
+struct AdamMulti {
+  AdamGroupDev grp[kAdamGroups];
+  int64_t block_end[kAdamGroups];
+  int count;
+  float b1, b2, one_minus_b1, one_minus_b2, eps;
+  int bias_correction;
+};
+
+__global__ void __launch_bounds__(256) adam_multi_kernel(const AdamMulti a) {
+  int k = 0;
+  while (k < a.count - 1 && (int64_t)blockIdx.x >= a.block_end[k]) ++k;  // uniform
+  const int64_t b0 = k ? a.block_end[k - 1] : 0;
+  const AdamGroupDev& G = a.grp[k];
+  const int64_t i = ((int64_t)blockIdx.x - b0) * blockDim.x + threadIdx.x;
+  if (i >= G.n) return;
+  const float gi = G.g[i];
+  const float mi = a.b1 * G.m[i] + a.one_minus_b1 * gi;
+  const float vi = a.b2 * G.v[i] + a.one_minus_b2 * (gi * gi);
+  G.m[i] = mi;
+  G.v[i] = vi;
+  if (a.bias_correction)
+    G.p[i] = G.p[i] - (G.step_size * mi) / (sqrtf(vi) / G.bc2_sqrt + a.eps);
+  else
+    G.p[i] = G.p[i] - (G.step_size * mi) / (sqrtf(vi) + a.eps);
+}
+
+// Step size and sqrt of the second bias correction of one Adam step (bias
+// corrections in double, as a host optimizer computes them).
+static void adam_scales(float lr, float beta1, float beta2, int32_t step, int32_t bias_correction,
+                        float* step_size, float* bc2_sqrt) {
+  if (bias_correction) {
+    const double bc1 = 1.0 - __builtin_pow((double)beta1, (double)step);
+    const double bc2 = 1.0 - __builtin_pow((double)beta2, (double)step);
+    *step_size = (float)((double)lr / bc1);
+    *bc2_sqrt = (float)__builtin_sqrt(bc2);
+  } else {
+    *step_size = lr;
+    *bc2_sqrt = 1.0f;
+  }
+}
+
 }  // namespace fgs
 
 using namespace fgs;
@@ -147,17 +199,47 @@ extern "C" int32_t fgs_adam_step(float* param, const float* grad, float* exp_avg
   a.one_minus_b2 = 1.0f - beta2;
   a.eps = eps;
   a.bias_correction = bias_correction ? 1 : 0;
-  if (bias_correction) {
-    // bias corrections in double, as a host optimizer computes them
-    const double bc1 = 1.0 - __builtin_pow((double)beta1, (double)step);
-    const double bc2 = 1.0 - __builtin_pow((double)beta2, (double)step);
-    a.step_size = (float)((double)lr / bc1);
-    a.bc2_sqrt = (float)__builtin_sqrt(bc2);
-  } else {
-    a.step_size = lr;
-    a.bc2_sqrt = 1.0f;
-  }
+  adam_scales(lr, beta1, beta2, step, bias_correction, &a.step_size, &a.bc2_sqrt);
   hipLaunchKernelGGL(adam_kernel, dim3(ceil_div_u(n, 256)), dim3(256), 0, (hipStream_t)stream, n,
                      a, param, grad, exp_avg, exp_avg_sq);
   return check_launch("adam_kernel");
+}
+
+extern "C" int32_t fgs_adam_step_multi(const fgs_adam_group* groups, int32_t count, float beta1,
+                                       float beta2, float eps, int32_t bias_correction,
+                                       void* stream) {
+  if (count < 0 || count > kAdamGroups || (count > 0 && !groups) ||
+      !(beta1 >= 0.0f && beta1 < 1.0f) || !(beta2 >= 0.0f && beta2 < 1.0f))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_adam_step_multi: bad arguments");
+  AdamMulti a{};
+  a.b1 = beta1;
+  a.b2 = beta2;
+  a.one_minus_b1 = 1.0f - beta1;
+  a.one_minus_b2 = 1.0f - beta2;
+  a.eps = eps;
+  a.bias_correction = bias_correction ? 1 : 0;
+  int64_t blocks = 0;
+  for (int k = 0; k < count; ++k) {
+    const fgs_adam_group& g = groups[k];
+    if (g.n < 0 || g.step < 1)
+      return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_adam_step_multi: bad group");
+    if (g.n > 0 && (!g.param || !g.grad || !g.exp_avg || !g.exp_avg_sq))
+      return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_adam_step_multi: null pointer");
+    if (g.n == 0) continue;
+    AdamGroupDev& d = a.grp[a.count];
+    d.p = g.param;
+    d.g = g.grad;
+    d.m = g.exp_avg;
+    d.v = g.exp_avg_sq;
+    d.n = g.n;
+    adam_scales(g.lr, beta1, beta2, g.step, bias_correction, &d.step_size, &d.bc2_sqrt);
+    blocks += (g.n + 255) / 256;
+    a.block_end[a.count] = blocks;
+    ++a.count;
+  }
+  if (a.count == 0) return FGS_OK;
+  if (blocks > 0x7FFFFFFF) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_adam_step_multi: too large");
+  hipLaunchKernelGGL(adam_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     a);
+  return check_launch("adam_multi_kernel");
 }

@@ -10,7 +10,7 @@ stay on the device:
   and the densification statistics in capacity-sized buffers (two sets).  A
   densify or prune step computes the new row map on the GPU and writes the new
   set into the other buffers in one gather pass; capacity grows by 1.5x only
-  when the new count exceeds it, so the step count of reallocations is
+  when the new count exceeds it, so the number of reallocations is
   logarithmic in the growth.
 * ``GaussianTrainState.step`` is the FastGS optimizer policy (the cadence of
   :159-171, MLX Adam without bias correction) on the fused Adam kernel.
@@ -238,6 +238,7 @@ class GaussianTrainState:
         main = FastGSOptimizerPolicy.should_step_main(iteration)
         sh = FastGSOptimizerPolicy.should_step_sh(iteration)
         b1, b2 = self.optim.betas
+        groups, keep = [], []
         for n in PARAM_NAMES:
             if (n == "features_rest" and not sh) or (n != "features_rest" and not main):
                 continue
@@ -245,12 +246,15 @@ class GaussianTrainState:
             if leaf.grad is None or leaf.numel() == 0:
                 continue
             g = leaf.grad.to(torch.float32).contiguous()
+            keep.append(g)
             m, v = self.moments(n)
             self.step_count[n] += 1
-            _check(self.lib.fgs_adam_step(_p(leaf), _p(g), _p(m), _p(v), leaf.numel(),
-                                          float(self.lrs[n]), float(b1), float(b2),
-                                          float(self.optim.eps), self.step_count[n], 0,
-                                          _stream(self.dev)))
+            groups.append(_lib.AdamGroup(_p(leaf), _p(g), _p(m), _p(v), leaf.numel(),
+                                         float(self.lrs[n]), self.step_count[n]))
+        if groups:  # the six tensors in one launch
+            arr = (_lib.AdamGroup * len(groups))(*groups)
+            _check(self.lib.fgs_adam_step_multi(arr, len(groups), float(b1), float(b2),
+                                                float(self.optim.eps), 0, _stream(self.dev)))
 
     def zero_grad(self) -> None:
         for t in self._leaves.values():

@@ -60,3 +60,53 @@ def l1_ssim_loss(img: torch.Tensor, target: torch.Tensor, w_l1: float = 1.0,
     img = img.to(torch.float32).contiguous()
     target = target.detach().to(device=img.device, dtype=torch.float32).contiguous()
     return _L1SSIM.apply(img, target, w_l1, w_ssim)
+
+
+class _Pointwise(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, img, tgt, mode):
+        lib = _lib.load()
+        dev = img.device
+        n = img.numel()
+        loss = torch.empty((), dtype=torch.float32, device=dev)
+        ws = torch.empty(int(lib.fgs_pointwise_loss_workspace_bytes(n)), dtype=torch.uint8,
+                         device=dev)
+        with _stage("loss_fwd"):
+            _lib.check(lib.fgs_pointwise_loss_fwd(_p(img), _p(tgt), n, mode, _p(ws), _p(loss),
+                                                  _stream(dev)))
+        ctx.save_for_backward(img, tgt)
+        ctx.mode = mode
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        lib = _lib.load()
+        img, tgt = ctx.saved_tensors
+        g = g.to(torch.float32).contiguous()
+        dimg = torch.empty_like(img)
+        with _stage("loss_bwd"):
+            _lib.check(lib.fgs_pointwise_loss_bwd(_p(img), _p(tgt), img.numel(), ctx.mode, _p(g),
+                                                  _p(dimg), _stream(img.device)))
+        return dimg, None, None
+
+
+def _pointwise(img: torch.Tensor, target: torch.Tensor, mode: int, name: str) -> torch.Tensor:
+    if img.shape != target.shape or img.numel() == 0:
+        raise ValueError(f"{name} expects two non-empty tensors of one shape, got "
+                         f"{tuple(img.shape)} and {tuple(target.shape)}")
+    if not img.is_cuda:
+        raise RuntimeError("fastgs_core_amd requires a ROCm GPU; there is no CPU fallback")
+    img = img.to(torch.float32).contiguous()
+    target = target.detach().to(device=img.device, dtype=torch.float32).contiguous()
+    return _Pointwise.apply(img, target, mode)
+
+
+def l1_loss(img: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """mean |img - target| (the training script's L1, train_scanner_fastgs.py:962):
+    one HIP kernel pair each way, sums in double; differentiable in ``img``."""
+    return _pointwise(img, target, 0, "l1_loss")
+
+
+def mse_loss(img: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """mean (img - target)^2 (the training script's MSE, train_scanner_fastgs.py:963)."""
+    return _pointwise(img, target, 1, "mse_loss")

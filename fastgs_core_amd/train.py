@@ -92,15 +92,22 @@ class FusedAdam(torch.optim.Optimizer):
 
     @torch.no_grad()
     def step(self, closure=None):
+        """One update of every parameter with a gradient: the tensors of a
+        parameter group go to the GPU eight per launch (fgs_adam_step_multi)."""
         loss = closure() if closure is not None else None
         lib = _lib.load()
         for group in self.param_groups:
             b1, b2 = group["betas"]
+            batch, keep = [], []
+            dev = None
             for p in group["params"]:
                 if p.grad is None:
                     continue
                 if not p.is_cuda or p.dtype != torch.float32 or not p.is_contiguous():
                     raise RuntimeError("FusedAdam needs contiguous float32 GPU parameters")
+                if dev is not None and p.device != dev:
+                    raise RuntimeError("FusedAdam: the parameters of a group share one device")
+                dev = p.device
                 st = self.state[p]
                 if not st:
                     st["step"] = 0
@@ -108,11 +115,17 @@ class FusedAdam(torch.optim.Optimizer):
                     st["exp_avg_sq"] = torch.zeros_like(p)
                 st["step"] += 1
                 g = p.grad.to(torch.float32).contiguous()
-                _lib.check(lib.fgs_adam_step(_p(p), _p(g), _p(st["exp_avg"]), _p(st["exp_avg_sq"]),
-                                             p.numel(), float(group["lr"]), float(b1), float(b2),
-                                             float(group["eps"]), int(st["step"]),
-                                             int(bool(group["bias_correction"])),
-                                             _stream(p.device)))
+                keep.append(g)
+                batch.append(_lib.AdamGroup(_p(p), _p(g), _p(st["exp_avg"]),
+                                            _p(st["exp_avg_sq"]), p.numel(), float(group["lr"]),
+                                            int(st["step"])))
+            for i in range(0, len(batch), 8):
+                part = batch[i:i + 8]
+                arr = (_lib.AdamGroup * len(part))(*part)
+                _lib.check(lib.fgs_adam_step_multi(arr, len(part), float(b1), float(b2),
+                                                   float(group["eps"]),
+                                                   int(bool(group["bias_correction"])),
+                                                   _stream(dev)))
         return loss
 
 

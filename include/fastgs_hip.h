@@ -317,6 +317,18 @@ int32_t fgs_l1_ssim_bwd(const float* img, const float* tgt, const float* dmaps,
                         const float* grad_out, int32_t C, int32_t H, int32_t W, float w_l1,
                         float w_ssim, float* dimg, void* stream);
 
+/* The pointwise losses of the FastGS training script's loss_fn
+ * (scripts/train_scanner_fastgs.py:911-966): *loss = mean |x - y| (mode 0)
+ * or mean (x - y)^2 (mode 1) over n floats, terms summed in double in a fixed
+ * order; the backward writes dx = g * sign(x - y) / n or g * 2 (x - y) / n
+ * (g = *grad_out, 1 when NULL).  No counterpart in the reference library (its
+ * script computes them with MLX). */
+size_t fgs_pointwise_loss_workspace_bytes(int64_t n);
+int32_t fgs_pointwise_loss_fwd(const float* x, const float* y, int64_t n, int32_t mode,
+                               void* workspace, float* loss, void* stream);
+int32_t fgs_pointwise_loss_bwd(const float* x, const float* y, int64_t n, int32_t mode,
+                               const float* grad_out, float* dx, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Training-step glue.  No counterpart in the reference library: the         */
 /* reference's training scripts do these in MLX (activations                 */
@@ -347,6 +359,22 @@ int32_t fgs_activations_bwd(int32_t P, const float* quats, const float* scales,
 int32_t fgs_adam_step(float* param, const float* grad, float* exp_avg, float* exp_avg_sq,
                       int64_t n, float lr, float beta1, float beta2, float eps, int32_t step,
                       int32_t bias_correction, void* stream);
+
+/* Up to 8 tensors in one launch, each with its own learning rate and step
+ * count, the update of fgs_adam_step.  No counterpart in the reference: its
+ * MLX optimizer steps each array on its own (train_scanner_fastgs.py:77-182);
+ * one launch for the six Gaussian parameter tensors saves five. */
+typedef struct {
+  float* param;
+  const float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  int64_t n;
+  float lr;
+  int32_t step;
+} fgs_adam_group;
+int32_t fgs_adam_step_multi(const fgs_adam_group* groups, int32_t count, float beta1, float beta2,
+                            float eps, int32_t bias_correction, void* stream);
 
 /* Fill a u32 buffer with a value on the stream (a kernel, graph-safe). */
 int32_t fgs_fill_u32(uint32_t* dst, uint32_t value, int64_t n, void* stream);

@@ -152,3 +152,66 @@ def test_fastgs_policy_steps_on_cadence():
         if not torch.equal(params["features_rest"].detach(), before):
             sh_changes.append(it)
     assert sh_changes == [16, 32]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bias_correction", [0, 1])
+def test_adam_multi_matches_single_tensor_steps(bias_correction):
+    """fgs_adam_step_multi over tensors of different sizes, learning rates and
+    step counts gives the bits of one fgs_adam_step per tensor."""
+    import ctypes
+
+    import torch
+
+    from fastgs_core_amd import _lib
+    from fastgs_core_amd.rasterizer import _p, _stream
+
+    print(f"[gpu-test] adam multi vs single bc={bias_correction}", flush=True)
+    lib = _lib.load()
+    dev = torch.device("cuda")
+    torch.manual_seed(1)
+    sizes, lrs, steps = [1, 255, 256, 257, 10007, 3], [1e-3, 3e-3, 1e-4, 5e-2, 2e-3, 1.0], \
+        [1, 2, 7, 30, 3, 1000]
+    single = [[torch.randn(n, device=dev) for _ in range(4)] for n in sizes]
+    for t in single:
+        t[3] = t[3].abs()  # second moments are non-negative
+    multi = [[x.clone() for x in t] for t in single]
+    for (p, g, m, v), lr, st in zip(single, lrs, steps):
+        _lib.check(lib.fgs_adam_step(_p(p), _p(g), _p(m), _p(v), p.numel(), lr, 0.9, 0.99, 1e-8,
+                                     st, bias_correction, _stream(dev)))
+    groups = [_lib.AdamGroup(_p(p), _p(g), _p(m), _p(v), p.numel(), lr, st)
+              for (p, g, m, v), lr, st in zip(multi, lrs, steps)]
+    arr = (_lib.AdamGroup * len(groups))(*groups)
+    _lib.check(lib.fgs_adam_step_multi(arr, len(groups), 0.9, 0.99, 1e-8, bias_correction,
+                                       _stream(dev)))
+    for a, b in zip(single, multi):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+    with pytest.raises(ValueError):
+        over = (_lib.AdamGroup * 9)(*(groups + groups[:3]))
+        _lib.check(lib.fgs_adam_step_multi(over, 9, 0.9, 0.99, 1e-8, 0, _stream(dev)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["l1", "mse"])
+def test_pointwise_loss_matches_torch_float64(mode):
+    import torch
+
+    print(f"[gpu-test] pointwise loss {mode}", flush=True)
+    dev = torch.device("cuda")
+    torch.manual_seed(2)
+    x = torch.rand(3, 97, 131, device=dev)
+    y = torch.rand(3, 97, 131, device=dev)
+    y[0, 0, :7] = x[0, 0, :7]  # ties: the L1 gradient is 0 there
+    xa = x.clone().requires_grad_(True)
+    fn = fg.l1_loss if mode == "l1" else fg.mse_loss
+    loss = fn(xa, y)
+    loss.backward(torch.tensor(1.7, device=dev))
+    xd = x.double().cpu().requires_grad_(True)
+    d = xd - y.double().cpu()
+    ref = d.abs().mean() if mode == "l1" else (d * d).mean()
+    (ref * 1.7).backward()
+    assert abs(float(loss) - float(ref)) <= 1e-6 * abs(float(ref))
+    torch.testing.assert_close(xa.grad.double().cpu(), xd.grad, rtol=1e-6, atol=1e-12)
+    if mode == "l1":
+        assert (xa.grad[0, 0, :7] == 0).all()
