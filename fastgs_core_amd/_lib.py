@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class PreprocessParams(Structure):
@@ -77,7 +77,7 @@ class RasterBwdIO(Structure):
     _fields_ = [(n, c_void_p) for n in (
         "ranges", "point_list", "means2d", "colors", "conic_opacity", "background", "final_t",
         "n_contrib", "max_contrib", "dL_dout_color", "dL_dmeans2d", "dL_dcolors",
-        "dL_dconic_opacity", "dL_dviewspace")]
+        "dL_dconic_opacity", "dL_dviewspace", "tile_order")]
 
 
 class AdamGroup(Structure):  # fgs_adam_group

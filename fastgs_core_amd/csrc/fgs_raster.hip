@@ -381,7 +381,8 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
   __shared__ float4 s_cull[kBwdBatch];  // (row_lo, row_hi, -opacity/2, colour 3)
   __shared__ uint32_t s_g[kBwdBatch];
   __shared__ float s_rec[kBwdBatch * kRec];
-  const int tile = (int)blockIdx.x;
+  const int tile = io.tile_order ? (int)io.tile_order[blockIdx.x] : (int)blockIdx.x;
+  if (tile < 0 || tile >= sh.gx * sh.gy) return;  // uniform; a permutation never takes it
   const int tx = tile % sh.gx, ty = tile / sh.gx;
   const int l = (int)threadIdx.x;
   const int px = tx * kTile + (l & 15);
@@ -493,6 +494,45 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
   }
 }
 
+// Launch order of the backward's tiles, heaviest first: a counting sort of
+// the tiles by max_contrib (the length of each tile's walk) into 1024 buckets
+// between 0 and the largest value, largest bucket first.  Per-tile work varies
+// several-fold, and workgroups start in index order, so in index order the
+// last heavy tiles run alone at the end of the launch; heaviest first, light
+// tiles fill that tail.  Tiles of one bucket leave in no fixed order (LDS
+// atomics): only the schedule depends on it.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBuckets = 1024;
+
+__global__ void __launch_bounds__(kOrderThreads)
+tile_order_kernel(const uint32_t* __restrict__ max_contrib, int T, uint32_t* __restrict__ order) {
+  __shared__ uint32_t s_cnt[kOrderBuckets];
+  __shared__ uint32_t s_tmp[kOrderThreads / kWave + 1];
+  __shared__ uint32_t s_max;
+  const int t = (int)threadIdx.x;
+  uint32_t m = 0;
+  for (int i = t; i < T; i += kOrderThreads) m = max_contrib[i] > m ? max_contrib[i] : m;
+  m = wave_max_u32(m);
+  if (t == 0) s_max = 0u;
+  s_cnt[t] = 0u;
+  __syncthreads();
+  if (lane_id() == 0) atomicMax(&s_max, m);
+  __syncthreads();
+  const uint64_t mx = s_max;
+  auto bucket = [mx](uint32_t v) -> uint32_t {
+    return mx == 0 ? 0u
+                   : (uint32_t)(kOrderBuckets - 1) -
+                         (uint32_t)(((uint64_t)v * (uint64_t)(kOrderBuckets - 1)) / mx);
+  };
+  for (int i = t; i < T; i += kOrderThreads) atomicAdd(&s_cnt[bucket(max_contrib[i])], 1u);
+  __syncthreads();
+  const uint32_t first = block_excl_scan(s_cnt[t], s_tmp, nullptr);
+  s_cnt[t] = first;
+  __syncthreads();
+  for (int i = t; i < T; i += kOrderThreads)
+    order[atomicAdd(&s_cnt[bucket(max_contrib[i])], 1u)] = (uint32_t)i;
+}
+
 // dL/dmeans2d equals the first two viewspace terms: copied after the
 // accumulation instead of being accumulated twice.
 __global__ void __launch_bounds__(256)
@@ -586,6 +626,10 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
   return check_launch("raster_fwd_kernel");
 }
 
+// Grids above this many tiles run in index order (one workgroup sorts the
+// order; at 2^16 tiles, a 4096x4096 image, that is 64 tiles per thread).
+constexpr int kMaxOrderedTiles = 1 << 16;
+
 extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raster_bwd_io* io,
                                      void* stream) {
   if (raster_check(p, "fgs_rasterize_bwd: bad parameters") != FGS_OK) return FGS_ERR_INVALID_ARGUMENT;
@@ -622,12 +666,18 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_rasterize_bwd: missing tensor");
   const int NCH = C < 3 ? C : 3;
   RasterShape sh{W, H, gx, gy};
-  if (NCH == 3)
-    hipLaunchKernelGGL(raster_bwd_kernel<3>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
-  else if (NCH == 2)
-    hipLaunchKernelGGL(raster_bwd_kernel<2>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
+  fgs_raster_bwd_io kio = *io;
+  if (kio.tile_order && tiles <= kMaxOrderedTiles)
+    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, io->max_contrib,
+                       tiles, kio.tile_order);
   else
-    hipLaunchKernelGGL(raster_bwd_kernel<1>, dim3(tiles), dim3(64), 0, st, *p, *io, sh);
+    kio.tile_order = nullptr;  // index order
+  if (NCH == 3)
+    hipLaunchKernelGGL(raster_bwd_kernel<3>, dim3(tiles), dim3(64), 0, st, *p, kio, sh);
+  else if (NCH == 2)
+    hipLaunchKernelGGL(raster_bwd_kernel<2>, dim3(tiles), dim3(64), 0, st, *p, kio, sh);
+  else
+    hipLaunchKernelGGL(raster_bwd_kernel<1>, dim3(tiles), dim3(64), 0, st, *p, kio, sh);
   if (check_launch("raster_bwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
   hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
                      io->dL_dviewspace, io->dL_dmeans2d, P);

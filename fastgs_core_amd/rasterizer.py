@@ -307,11 +307,12 @@ class _Rasterize(torch.autograd.Function):
         d_colors = torch.empty((P, colors.shape[1] if colors.dim() == 2 else C), **f32)
         d_conic = torch.empty((P, 4), **f32)
         d_vsp = torch.empty((P, 4), **f32)
+        tile_order = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
         prm = _lib.RasterParams(W, H, C, T, B, 0, 0, P, point_list.numel())
         io = _lib.RasterBwdIO(
             _p(ranges), _p(point_list), _p(means2d), _p(colors), _p(conic_opacity),
             _p(background), _p(final_t), _p(n_contrib), _p(max_contrib), _p(g_out),
-            _p(d_means2d), _p(d_colors), _p(d_conic), _p(d_vsp))
+            _p(d_means2d), _p(d_colors), _p(d_conic), _p(d_vsp), _p(tile_order))
         with _stage("rasterize_bwd"):
             _lib.check(lib.fgs_rasterize_bwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
         need = ctx.needs_input_grad

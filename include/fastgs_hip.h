@@ -288,6 +288,10 @@ typedef struct {
   float* dL_dcolors;            /* [P,num_channels] */
   float* dL_dconic_opacity;     /* [P,4] */
   float* dL_dviewspace;         /* [P,4] */
+  uint32_t* tile_order;         /* [T] scratch, or NULL.  When set (and T <= 65536) the tiles
+                                   are walked heaviest first by max_contrib, which shortens the
+                                   launch's tail; NULL walks them in index order.  The result is
+                                   the same either way, up to the order of float atomic adds. */
 } fgs_raster_bwd_io;
 
 /* Gradients of the blend w.r.t. means2d (scaled by (W/2,H/2)), colours,
