@@ -335,6 +335,16 @@ struct EmitStRecord {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also makes every
+// earlier global access of the thread complete (s_waitcnt vmcnt(0)), which
+// drains loads issued ahead and fire-and-forget atomics; where the barrier
+// guards nothing but LDS, this form lets them stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int l = lane_id();
   return (l == 0) ? 0ull : ((~0ull) >> (64 - l));

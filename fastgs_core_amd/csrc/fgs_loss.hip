@@ -9,17 +9,21 @@
 // Both passes use one wavefront per strip of 64 columns x 32 output rows of
 // one plane, lane l owning column l.  The wavefront walks the strip's 42
 // input rows (5-row halo above and below) top to bottom: each row's 74
-// values (5-column halo each side) are staged in LDS, the lane blurs its
-// column horizontally and keeps the result for the last 11 rows in a register
-// ring (the row loop is unrolled by 11, so the ring is indexed statically);
-// once 11 rows are in, the vertical blur of the ring gives one output row.
-// The next row's values are loaded while the current one is processed.
+// values (5-column halo each side) are staged in LDS (two row buffers, so one
+// barrier per row), the lane blurs its column horizontally and keeps the
+// result for the last 11 rows in a register ring (the row loop is unrolled by
+// 11, so the ring is indexed statically); once 11 rows are in, the vertical
+// blur of the ring gives one output row.  Input rows are loaded 11 rows
+// before they are staged (a second register ring), so a row's global load
+// latency overlaps the work of the rows before it; the one barrier per row
+// orders LDS only, so those loads stay in flight across it.
 //
 // Forward: the five moments x, y, x^2, y^2, xy are blurred; the SSIM value
 // and its partial derivatives with respect to the three blurred moments of x
 // (E[x], E[x^2], E[xy]) are written per pixel, and per-strip partial sums of
-// SSIM and |x - y| go to a partials array that a second kernel reduces in a
-// fixed order (deterministic).
+// SSIM and |x - y| (the latter from the staged centre column) go to a
+// partials array that a second kernel reduces in a fixed order
+// (deterministic).
 //
 // Backward: the three partial-derivative maps are blurred the same way
 // (the zero-padded symmetric blur is self-adjoint) and combined with x, y:
@@ -52,45 +56,62 @@ __device__ __forceinline__ void load_row(const float* __restrict__ p, const Loss
   v1 = (rin && l < 2 * kLR && cb < a.W) ? p[(size_t)gr * a.W + cb] : 0.0f;
 }
 
+// Input rows of NM planes loaded 11 rows ahead: row i lives in slot i % 11,
+// the slot the unrolled row loop stages it from, and the load of row i + 11
+// refills that slot right after.  Static slots keep the in-flight registers
+// from being copied (a copy would wait for the load).
+template <int NM>
+struct RowRing {
+  float v0[NM][11], v1[NM][11];
+  __device__ __forceinline__ void fill(const float* const (&p)[NM], const LossArgs& a, int gr0,
+                                       int c0, int l) {
+#pragma unroll
+    for (int q = 0; q < 11; ++q)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) load_row(p[m], a, gr0 + q, c0, l, v0[m][q], v1[m][q]);
+  }
+};
+
 __global__ void __launch_bounds__(kSW)
 l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float* __restrict__ tgt,
                    float* __restrict__ dmaps, float* __restrict__ partials) {
-  __shared__ float s_x[kRowIn];
-  __shared__ float s_y[kRowIn];
+  __shared__ float s_x[2][kRowIn];
+  __shared__ float s_y[2][kRowIn];
   const int strip = (int)blockIdx.x % a.strips_x, chunk = (int)blockIdx.x / a.strips_x;
   const int plane = (int)blockIdx.y;
   const int l = (int)threadIdx.x;
   const int c0 = strip * kSW, r0 = chunk * kSH;
   const int gc = c0 + l;
   const size_t HW = (size_t)a.H * a.W;
-  const float* __restrict__ xp = img + plane * HW;
-  const float* __restrict__ yp = tgt + plane * HW;
+  const float* const src[2] = {img + plane * HW, tgt + plane * HW};
   const float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
   float ring[11][5];
   float ssim_sum = 0.f, l1_sum = 0.f;
-  float nx0, nx1, ny0, ny1;
-  load_row(xp, a, r0 - kLR, c0, l, nx0, nx1);
-  load_row(yp, a, r0 - kLR, c0, l, ny0, ny1);
+  RowRing<2> rq;
+  rq.fill(src, a, r0 - kLR, c0, l);
   for (int base = 0; base < kRows; base += 11) {
 #pragma unroll
     for (int sl = 0; sl < 11; ++sl) {
       const int i = base + sl;
       if (i >= kRows) break;  // uniform
-      s_x[l] = nx0;
-      s_y[l] = ny0;
+      float* sx = s_x[i & 1];
+      float* sy = s_y[i & 1];
+      sx[l] = rq.v0[0][sl];
+      sy[l] = rq.v0[1][sl];
       if (l < 2 * kLR) {
-        s_x[kSW + l] = nx1;
-        s_y[kSW + l] = ny1;
+        sx[kSW + l] = rq.v1[0][sl];
+        sy[kSW + l] = rq.v1[1][sl];
       }
-      __syncthreads();
-      if (i + 1 < kRows) {
-        load_row(xp, a, r0 - kLR + i + 1, c0, l, nx0, nx1);
-        load_row(yp, a, r0 - kLR + i + 1, c0, l, ny0, ny1);
+      if (i + 11 < kRows) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          load_row(src[m], a, r0 - kLR + i + 11, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
       }
+      lds_barrier();
       float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
 #pragma unroll
       for (int k = 0; k < 11; ++k) {
-        const float x = s_x[l + k], y = s_y[l + k], w = a.win[k];
+        const float x = sx[l + k], y = sy[l + k], w = a.win[k];
         m0 = __builtin_fmaf(w, x, m0);
         m1 = __builtin_fmaf(w, y, m1);
         m2 = __builtin_fmaf(w, x * x, m2);
@@ -102,7 +123,10 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
       ring[sl][2] = m2;
       ring[sl][3] = m3;
       ring[sl][4] = m4;
-      __syncthreads();  // the next row may overwrite s_x / s_y
+      const float xc = sx[l + kLR], yc = sy[l + kLR];
+      // |x - y| of the strip's own pixels, from the staged centre column
+      const int irow = r0 - kLR + i;
+      if (i >= kLR && i < kLR + kSH && irow < a.H && gc < a.W) l1_sum += fabsf(xc - yc);
       if (i < 2 * kLR) continue;
       const int orow = r0 + i - 2 * kLR;
       float mx = 0.f, my = 0.f, exx = 0.f, eyy = 0.f, exy = 0.f;
@@ -120,18 +144,16 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
       const float sxx = exx - mx * mx, syy = eyy - my * my, sxy = exy - mx * my;
       const float A = 2.f * mx * my + C1, Bv = 2.f * sxy + C2;
       const float Cv = mx * mx + my * my + C1, D = sxx + syy + C2;
-      const float inv = 1.0f / (Cv * D);
+      const float inv = 1.0f / (Cv * D);  // 1/Cv = D inv, 1/D = Cv inv
       const float S = A * Bv * inv;
       ssim_sum += S;
-      const size_t o = (size_t)orow * a.W + gc;
-      l1_sum += fabsf(xp[o] - yp[o]);
       if (dmaps) {
         // partials w.r.t. mu_x, sigma_xx, sigma_xy, then to the raw moments
-        const float dS_dmu = 2.f * my * Bv * inv - S * 2.f * mx / Cv;
-        const float dS_dsxx = -S / D;
+        const float dS_dmu = 2.f * my * Bv * inv - S * 2.f * mx * (D * inv);
+        const float dS_dsxx = -S * (Cv * inv);
         const float dS_dsxy = 2.f * A * inv;
         const float d1 = dS_dmu + dS_dsxx * (-2.f * mx) + dS_dsxy * (-my);
-        const size_t po = (size_t)plane * HW + o;
+        const size_t po = (size_t)plane * HW + (size_t)orow * a.W + gc;
         dmaps[po] = d1;
         dmaps[(size_t)a.C * HW + po] = dS_dsxx;
         dmaps[(size_t)2 * a.C * HW + po] = dS_dsxy;
@@ -183,7 +205,7 @@ __global__ void __launch_bounds__(kSW)
 l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float* __restrict__ tgt,
                    const float* __restrict__ dmaps, const float* __restrict__ grad_out,
                    float* __restrict__ dimg) {
-  __shared__ float s_d[3][kRowIn];
+  __shared__ float s_d[2][3][kRowIn];
   const int strip = (int)blockIdx.x % a.strips_x, chunk = (int)blockIdx.x / a.strips_x;
   const int plane = (int)blockIdx.y;
   const int l = (int)threadIdx.x;
@@ -191,37 +213,49 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
   const int gc = c0 + l;
   const size_t HW = (size_t)a.H * a.W;
   const size_t CHW = (size_t)a.C * HW;
-  const float* __restrict__ dp[3] = {dmaps + plane * HW, dmaps + CHW + plane * HW,
-                                     dmaps + 2 * CHW + plane * HW};
+  const float* const dp[3] = {dmaps + plane * HW, dmaps + CHW + plane * HW,
+                              dmaps + 2 * CHW + plane * HW};
+  const float* __restrict__ xp = img + plane * HW;
+  const float* __restrict__ yp = tgt + plane * HW;
   const float g = grad_out ? grad_out[0] : 1.0f;
   const float inv_n = (float)(1.0 / (double)CHW);
   float ring[11][3];
-  float n0[3], n1[3];
-#pragma unroll
-  for (int m = 0; m < 3; ++m) load_row(dp[m], a, r0 - kLR, c0, l, n0[m], n1[m]);
+  RowRing<3> rq;
+  rq.fill(dp, a, r0 - kLR, c0, l);
+  // x, y of the lane's pixel in image row r0 - 5 + i, loaded with input row i
+  // into slot i % 11 and used five rows later, when that row is the output
+  float qx[11], qy[11];
+  const bool col_in = gc < a.W;
   for (int base = 0; base < kRows; base += 11) {
 #pragma unroll
     for (int sl = 0; sl < 11; ++sl) {
       const int i = base + sl;
       if (i >= kRows) break;  // uniform
+      float (*sd)[kRowIn] = s_d[i & 1];
 #pragma unroll
       for (int m = 0; m < 3; ++m) {
-        s_d[m][l] = n0[m];
-        if (l < 2 * kLR) s_d[m][kSW + l] = n1[m];
+        sd[m][l] = rq.v0[m][sl];
+        if (l < 2 * kLR) sd[m][kSW + l] = rq.v1[m][sl];
       }
-      __syncthreads();
-      if (i + 1 < kRows) {
+      if (i + 11 < kRows) {
 #pragma unroll
-        for (int m = 0; m < 3; ++m) load_row(dp[m], a, r0 - kLR + i + 1, c0, l, n0[m], n1[m]);
+        for (int m = 0; m < 3; ++m)
+          load_row(dp[m], a, r0 - kLR + i + 11, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
       }
+      {
+        const int irow = r0 - kLR + i;
+        const bool in = col_in && i >= kLR && i < kLR + kSH && irow < a.H;
+        qx[sl] = in ? xp[(size_t)irow * a.W + gc] : 0.0f;
+        qy[sl] = in ? yp[(size_t)irow * a.W + gc] : 0.0f;
+      }
+      lds_barrier();
 #pragma unroll
       for (int m = 0; m < 3; ++m) {
         float h = 0.f;
 #pragma unroll
-        for (int k = 0; k < 11; ++k) h = __builtin_fmaf(a.win[k], s_d[m][l + k], h);
+        for (int k = 0; k < 11; ++k) h = __builtin_fmaf(a.win[k], sd[m][l + k], h);
         ring[sl][m] = h;
       }
-      __syncthreads();
       if (i < 2 * kLR) continue;
       const int orow = r0 + i - 2 * kLR;
       float B[3] = {0.f, 0.f, 0.f};
@@ -231,9 +265,9 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
 #pragma unroll
         for (int m = 0; m < 3; ++m) B[m] = __builtin_fmaf(a.win[k], ring[q][m], B[m]);
       }
-      if (orow >= a.H || gc >= a.W) continue;
+      const float x = qx[(sl + 6) % 11], y = qy[(sl + 6) % 11];  // loaded at row i - 5
+      if (orow >= a.H || !col_in) continue;
       const size_t o = plane * HW + (size_t)orow * a.W + gc;
-      const float x = img[o], y = tgt[o];
       const float d = x - y;
       const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
       const float dssim = B[0] + 2.f * x * B[1] + y * B[2];
