@@ -489,10 +489,11 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
 // thread: large sorts take big chunks (fewer chunks to look back over), small
 // ones smaller chunks so that more workgroups share the ranking.
 constexpr int kSortT = 512;
-// At 1M keys 16 items per thread measured 21.9 us per pass against 27.1 for
-// 4; at 200k keys 4 items measured 13.4 us against 17.4 for 16.
+// At 1M keys 8 items per thread measured about 21 us per pass (binning
+// 295-298 us against 299-301 with 16 items, 27.1 us per pass with 4); at 200k
+// keys 4 items measured 13.4 us against 17.4 for 16.
 constexpr int64_t kSortSmallN = 393216;
-static int sort_items(int64_t n) { return n > kSortSmallN ? 16 : 4; }
+static int sort_items(int64_t n) { return n > kSortSmallN ? 8 : 4; }
 static int64_t sort_chunks(int64_t n) {
   const int64_t c = (int64_t)kSortT * sort_items(n);
   return (n + c - 1) / c;
@@ -556,8 +557,8 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
     const bool to_out = ((pl.passes - 1 - pass) % 2) == 0;
     K* dk = to_out ? keys_out : tk;
     uint32_t* dv = to_out ? vals_out : tv;
-    if (items == 16)
-      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 16>), dim3((unsigned)nc), dim3(kSortT), 0,
+    if (items == 8)
+      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
                          status + (size_t)pass * nc * 256, nc, tickets + pass, err);
     else
