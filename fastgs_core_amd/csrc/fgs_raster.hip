@@ -503,6 +503,7 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
 // atomics): only the schedule depends on it.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderBuckets = 1024;
+constexpr int kOrderCached = 8;  // values kept in registers per thread (8192 tiles)
 
 __global__ void __launch_bounds__(kOrderThreads)
 tile_order_kernel(const uint32_t* __restrict__ max_contrib, int T, uint32_t* __restrict__ order) {
@@ -510,26 +511,43 @@ tile_order_kernel(const uint32_t* __restrict__ max_contrib, int T, uint32_t* __r
   __shared__ uint32_t s_tmp[kOrderThreads / kWave + 1];
   __shared__ uint32_t s_max;
   const int t = (int)threadIdx.x;
+  uint32_t mc[kOrderCached];
   uint32_t m = 0;
-  for (int i = t; i < T; i += kOrderThreads) m = max_contrib[i] > m ? max_contrib[i] : m;
+#pragma unroll
+  for (int c = 0; c < kOrderCached; ++c) {
+    const int i = t + c * kOrderThreads;
+    mc[c] = i < T ? max_contrib[i] : 0u;
+    m = mc[c] > m ? mc[c] : m;
+  }
+  for (int i = t + kOrderCached * kOrderThreads; i < T; i += kOrderThreads)
+    m = max_contrib[i] > m ? max_contrib[i] : m;
   m = wave_max_u32(m);
   if (t == 0) s_max = 0u;
   s_cnt[t] = 0u;
   __syncthreads();
   if (lane_id() == 0) atomicMax(&s_max, m);
   __syncthreads();
-  const uint64_t mx = s_max;
-  auto bucket = [mx](uint32_t v) -> uint32_t {
-    return mx == 0 ? 0u
-                   : (uint32_t)(kOrderBuckets - 1) -
-                         (uint32_t)(((uint64_t)v * (uint64_t)(kOrderBuckets - 1)) / mx);
+  // bucket 0 holds the largest values; the float scale only has to be monotone
+  const float sc = s_max ? (float)(kOrderBuckets - 1) / (float)s_max : 0.0f;
+  auto bucket = [sc](uint32_t v) -> uint32_t {
+    const uint32_t q = (uint32_t)((float)v * sc);
+    return (uint32_t)(kOrderBuckets - 1) - (q < (uint32_t)(kOrderBuckets - 1) ? q : (uint32_t)(kOrderBuckets - 1));
   };
-  for (int i = t; i < T; i += kOrderThreads) atomicAdd(&s_cnt[bucket(max_contrib[i])], 1u);
+#pragma unroll
+  for (int c = 0; c < kOrderCached; ++c)
+    if (t + c * kOrderThreads < T) atomicAdd(&s_cnt[bucket(mc[c])], 1u);
+  for (int i = t + kOrderCached * kOrderThreads; i < T; i += kOrderThreads)
+    atomicAdd(&s_cnt[bucket(max_contrib[i])], 1u);
   __syncthreads();
   const uint32_t first = block_excl_scan(s_cnt[t], s_tmp, nullptr);
   s_cnt[t] = first;
   __syncthreads();
-  for (int i = t; i < T; i += kOrderThreads)
+#pragma unroll
+  for (int c = 0; c < kOrderCached; ++c) {
+    const int i = t + c * kOrderThreads;
+    if (i < T) order[atomicAdd(&s_cnt[bucket(mc[c])], 1u)] = (uint32_t)i;
+  }
+  for (int i = t + kOrderCached * kOrderThreads; i < T; i += kOrderThreads)
     order[atomicAdd(&s_cnt[bucket(max_contrib[i])], 1u)] = (uint32_t)i;
 }
 
