@@ -76,9 +76,14 @@ __device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c,
   return make_float2(y - hy, y + hy);
 }
 
+template <bool B>
+struct FiniteTag {
+  static constexpr bool value = B;
+};
+
 // kMode bit 0: write the sampled state; bit 1: count metric hits (get_flag).
 template <int NCH, int kMode>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 5)
 raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, RasterShape sh) {
   constexpr bool kSampled = (kMode & 1) != 0;
   constexpr bool kMetric = (kMode & 2) != 0;
@@ -118,6 +123,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
     const int base = r * 256;
     const int cnt = (n - base) < 256 ? (n - base) : 256;
     const int cnt8 = (cnt + 7) & ~7;  // padded with splats of opacity 0 (never blended)
+    bool fin = true;  // the staged colour is finite
     if (base + t < n) {
       const uint32_t g = io.point_list[start + base + t];
       float4 a, b;
@@ -127,59 +133,75 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
       s_b[t] = b;
       s_c[t] = c;
       s_g[t] = g;
+      fin = __builtin_isfinite(b.z) && (NCH < 2 || __builtin_isfinite(b.w)) &&
+            (NCH < 3 || __builtin_isfinite(c));
     } else if (t < cnt8) {
       s_a[t] = make_float4(0.f, 0.f, 0.f, 0.f);
       s_b[t] = make_float4(0.f, 0.f, 0.f, 0.f);
       s_c[t] = 0.0f;
       s_g[t] = 0xFFFFFFFFu;
     }
-    __syncthreads();
+    const bool colours_finite = __syncthreads_and(fin ? 1 : 0) != 0;
     // Branch-free per splat: blend / stop / take are lane predicates and the
     // state moves by selects, so the wave runs one straight path, eight
     // splats at a time; it leaves the batch once no lane is live.  A lane
     // that stops takes nothing more, as the reference loop's break.
     bool live = !done;
-    if (__ballot(live) != 0ull) {  // wave-uniform
+    auto walk = [&](auto finite_tag) {
+      constexpr bool kFinite = decltype(finite_tag)::value;
       for (int j0 = 0; j0 < cnt8; j0 += 8) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u;
-        const int jj = base + j;
-        if (kSampled && (jj & 31) == 0 && jj < n && live) {
-          const size_t bk = (size_t)bbm0 + (size_t)(jj >> 5);
-          if ((int64_t)bk < prm.bucket_sum) {
-            io.sampled_t[bk * 256 + t] = T;
+        for (int u = 0; u < 8; ++u) {
+          const int j = j0 + u;
+          const int jj = base + j;
+          if (kSampled && (jj & 31) == 0 && jj < n && live) {
+            const size_t bk = (size_t)bbm0 + (size_t)(jj >> 5);
+            if ((int64_t)bk < prm.bucket_sum) {
+              io.sampled_t[bk * 256 + t] = T;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c)
-              io.sampled_ar[bk * (size_t)prm.num_channels * 256 + (size_t)c * 256 + t] = acc[c];
+              for (int c = 0; c < NCH; ++c)
+                io.sampled_ar[bk * (size_t)prm.num_channels * 256 + (size_t)c * 256 + t] = acc[c];
+            }
           }
+          const float4 a = s_a[j];
+          const float4 b = s_b[j];
+          const float dx = a.x - pxf;
+          const float dy = a.y - pyf;
+          const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
+          const float alpha = fminf(0.99f, b.y * det_expf(power));
+          const float test_t = T * (1.0f - alpha);
+          const bool blend = live && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
+          const bool stop = blend && test_t < 0.0001f;
+          const bool take = blend && !stop;
+          live = live && !stop;
+          // colour by fused multiply-adds (no decision depends on it).  aT is 0
+          // where the pixel does not take the splat; with a non-finite colour
+          // in the batch the colour is selected to 0 there as well (0 * inf
+          // would be NaN), otherwise c * 0 adds an exact zero.
+          const float aT = take ? alpha * T : 0.0f;
+          const float c2 = NCH > 2 ? s_c[j] : 0.0f;
+          if (kFinite) {
+            acc[0] = __builtin_fmaf(b.z, aT, acc[0]);
+            if (NCH > 1) acc[1] = __builtin_fmaf(b.w, aT, acc[1]);
+            if (NCH > 2) acc[2] = __builtin_fmaf(c2, aT, acc[2]);
+          } else {
+            acc[0] = __builtin_fmaf(take ? b.z : 0.0f, aT, acc[0]);
+            if (NCH > 1) acc[1] = __builtin_fmaf(take ? b.w : 0.0f, aT, acc[1]);
+            if (NCH > 2) acc[2] = __builtin_fmaf(take ? c2 : 0.0f, aT, acc[2]);
+          }
+          if (kMetric && take && count_metric && s_g[j] < (uint32_t)prm.num_points)
+            atomicAdd(&io.metric_count[s_g[j]], 1);
+          T = take ? test_t : T;
+          last = take ? (uint32_t)(jj + 1) : last;
         }
-        const float4 a = s_a[j];
-        const float4 b = s_b[j];
-        const float dx = a.x - pxf;
-        const float dy = a.y - pyf;
-        const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-        const float alpha = fminf(0.99f, b.y * det_expf(power));
-        const float test_t = T * (1.0f - alpha);
-        const bool blend = live && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
-        const bool stop = blend && test_t < 0.0001f;
-        const bool take = blend && !stop;
-        live = live && !stop;
-        // colour by fused multiply-adds (no decision depends on it); both
-        // factors are selected to 0 where the pixel does not take the splat,
-        // so a non-finite colour stays out of it (0 * 0 adds nothing)
-        const float aT = take ? alpha * T : 0.0f;
-        const float c2 = NCH > 2 ? s_c[j] : 0.0f;
-        acc[0] = __builtin_fmaf(take ? b.z : 0.0f, aT, acc[0]);
-        if (NCH > 1) acc[1] = __builtin_fmaf(take ? b.w : 0.0f, aT, acc[1]);
-        if (NCH > 2) acc[2] = __builtin_fmaf(take ? c2 : 0.0f, aT, acc[2]);
-        if (kMetric && take && count_metric && s_g[j] < (uint32_t)prm.num_points)
-          atomicAdd(&io.metric_count[s_g[j]], 1);
-        T = take ? test_t : T;
-        last = take ? (uint32_t)(jj + 1) : last;
-      }
         if (__ballot(live) == 0ull) break;  // uniform
       }
+    };
+    if (__ballot(live) != 0ull) {  // wave-uniform
+      if (colours_finite)
+        walk(FiniteTag<true>{});
+      else
+        walk(FiniteTag<false>{});
     }
     done = live ? 0 : 1;
     __syncthreads();
