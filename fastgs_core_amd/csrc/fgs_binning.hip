@@ -220,21 +220,8 @@ static size_t scan_ws_bytes(int64_t n) { return scan_state_bytes(n); }
 // Up to kFillSpans arrays filled with one value in one launch: 16-byte stores
 // from each array's first 16-byte boundary, single words for the ends.
 __global__ void __launch_bounds__(256) fill_spans_kernel(FillSpans f) {
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
-  const uint4 v4 = make_uint4(f.value, f.value, f.value, f.value);
-  for (int s = 0; s < f.count; ++s) {
-    uint32_t* p = f.p[s];
-    const int64_t n = f.n[s];
-    int64_t head = (int64_t)(((16u - (uint32_t)(reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) >> 2);
-    if (head > n) head = n;
-    if (tid < head) p[tid] = f.value;
-    const int64_t nv = (n - head) >> 2;
-    uint4* q = reinterpret_cast<uint4*>(p + head);
-    for (int64_t i = tid; i < nv; i += nthreads) q[i] = v4;
-    const int64_t done = head + nv * 4;
-    if (tid < n - done) p[done + tid] = f.value;
-  }
+  fill_spans_body(f, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,
+                  (int64_t)gridDim.x * blockDim.x);
 }
 
 void launch_fill_spans(const FillSpans& f, hipStream_t st) {

@@ -29,4 +29,23 @@ struct FillSpans {
 };
 void launch_fill_spans(const FillSpans& f, hipStream_t st);
 
+// The fill of FillSpans by thread tid of nthreads: a head of single words up
+// to 16-byte alignment, 16-byte stores, then the tail.
+__device__ __forceinline__ void fill_spans_body(const FillSpans& f, int64_t tid,
+                                                int64_t nthreads) {
+  const uint4 v4 = make_uint4(f.value, f.value, f.value, f.value);
+  for (int s = 0; s < f.count; ++s) {
+    uint32_t* p = f.p[s];
+    const int64_t n = f.n[s];
+    int64_t head = (int64_t)(((16u - (uint32_t)(reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) >> 2);
+    if (head > n) head = n;
+    if (tid < head) p[tid] = f.value;
+    const int64_t nv = (n - head) >> 2;
+    uint4* q = reinterpret_cast<uint4*>(p + head);
+    for (int64_t i = tid; i < nv; i += nthreads) q[i] = v4;
+    const int64_t done = head + nv * 4;
+    if (tid < n - done) p[done + tid] = f.value;
+  }
+}
+
 }  // namespace fgs

@@ -527,8 +527,8 @@ constexpr int kOrderThreads = 1024;
 constexpr int kOrderBuckets = 1024;
 constexpr int kOrderCached = 8;  // values kept in registers per thread (8192 tiles)
 
-__global__ void __launch_bounds__(kOrderThreads)
-tile_order_kernel(const uint32_t* __restrict__ max_contrib, int T, uint32_t* __restrict__ order) {
+__device__ __forceinline__ void tile_order_body(const uint32_t* __restrict__ max_contrib, int T,
+                                                uint32_t* __restrict__ order) {
   __shared__ uint32_t s_cnt[kOrderBuckets];
   __shared__ uint32_t s_tmp[kOrderThreads / kWave + 1];
   __shared__ uint32_t s_max;
@@ -571,6 +571,21 @@ tile_order_kernel(const uint32_t* __restrict__ max_contrib, int T, uint32_t* __r
   }
   for (int i = t + kOrderCached * kOrderThreads; i < T; i += kOrderThreads)
     order[atomicAdd(&s_cnt[bucket(max_contrib[i])], 1u)] = (uint32_t)i;
+}
+
+// The backward's preparation in one launch: workgroup 0 sorts the tile order
+// (when order is set) while the others clear the atomically accumulated
+// gradients.
+__global__ void __launch_bounds__(kOrderThreads)
+bwd_prep_kernel(FillSpans f, const uint32_t* __restrict__ max_contrib, int T,
+                uint32_t* __restrict__ order) {
+  const int first_fill = order ? 1 : 0;
+  if ((int)blockIdx.x < first_fill) {
+    tile_order_body(max_contrib, T, order);
+    return;
+  }
+  fill_spans_body(f, (int64_t)(blockIdx.x - first_fill) * blockDim.x + threadIdx.x,
+                  (int64_t)(gridDim.x - first_fill) * blockDim.x);
 }
 
 // dL/dmeans2d equals the first two viewspace terms: copied after the
@@ -683,20 +698,24 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   if (P > 0 && (!io->dL_dmeans2d || !io->dL_dcolors || !io->dL_dconic_opacity || !io->dL_dviewspace))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_rasterize_bwd: missing gradient tensor");
   hipStream_t st = (hipStream_t)stream;
-  if (P > 0) {  // the atomically accumulated gradients start at zero: one launch
-    FillSpans f{};
-    f.p[0] = reinterpret_cast<uint32_t*>(io->dL_dcolors);
-    f.n[0] = (int64_t)C * P;
-    f.p[1] = reinterpret_cast<uint32_t*>(io->dL_dconic_opacity);
-    f.n[1] = 4 * (int64_t)P;
-    f.p[2] = reinterpret_cast<uint32_t*>(io->dL_dviewspace);
-    f.n[2] = 4 * (int64_t)P;
-    f.count = 3;
-    f.value = 0u;
-    launch_fill_spans(f, st);
-  }
+  // the atomically accumulated gradients start at zero
+  FillSpans f{};
+  f.p[0] = reinterpret_cast<uint32_t*>(io->dL_dcolors);
+  f.n[0] = (int64_t)C * P;
+  f.p[1] = reinterpret_cast<uint32_t*>(io->dL_dconic_opacity);
+  f.n[1] = 4 * (int64_t)P;
+  f.p[2] = reinterpret_cast<uint32_t*>(io->dL_dviewspace);
+  f.n[2] = 4 * (int64_t)P;
+  f.count = P > 0 ? 3 : 0;
+  f.value = 0u;
   if (P == 0) return check_launch("rasterize_bwd");
+  const int64_t fill_words = (int64_t)(C + 8) * P;
+  int64_t fill_blocks = (fill_words / 4 + kOrderThreads - 1) / kOrderThreads;
+  if (fill_blocks < 1) fill_blocks = 1;
+  if (fill_blocks > 512) fill_blocks = 512;
   if (tiles == 0) {
+    hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)fill_blocks), dim3(kOrderThreads), 0, st, f,
+                       nullptr, 0, nullptr);
     hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
                        io->dL_dviewspace, io->dL_dmeans2d, P);
     return check_launch("copy_means2d_grad_kernel");
@@ -707,11 +726,9 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   const int NCH = C < 3 ? C : 3;
   RasterShape sh{W, H, gx, gy};
   fgs_raster_bwd_io kio = *io;
-  if (kio.tile_order && tiles <= kMaxOrderedTiles)
-    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, io->max_contrib,
-                       tiles, kio.tile_order);
-  else
-    kio.tile_order = nullptr;  // index order
+  if (!(kio.tile_order && tiles <= kMaxOrderedTiles)) kio.tile_order = nullptr;  // index order
+  hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)(fill_blocks + (kio.tile_order ? 1 : 0))),
+                     dim3(kOrderThreads), 0, st, f, io->max_contrib, tiles, kio.tile_order);
   if (NCH == 3)
     hipLaunchKernelGGL(raster_bwd_kernel<3>, dim3(tiles), dim3(64), 0, st, *p, kio, sh);
   else if (NCH == 2)
