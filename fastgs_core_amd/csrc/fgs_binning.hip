@@ -1314,10 +1314,10 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
     if (x < sg.gx && y < sg.gy) gbase = tile_start[y * sg.gx + x] + base2[(size_t)c * kWave + l];
   }
   const uint32_t soff = ci - cj;
+  const uint64_t my_tile = (uint64_t)((y0 + l / kSt) * sg.gx + x0 + (l % kSt)) << 32;
   __syncthreads();
   uint32_t cur = staged ? soff : gbase;
   for (int k = 0; k < w; ++k) cur += s_wc[k][l];
-  const uint64_t lt = lanemask_lt();
   for (uint32_t base = q0; base < q1; base += kWave) {
     const uint32_t e = base + (uint32_t)l;
     uint64_t m = 0ull;
@@ -1327,33 +1327,30 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
       g = list[e];
       db = g < (uint32_t)P ? __float_as_uint(depths[g]) : 0xFFFFFFFFu;
     }
-    // lane j: the round's entries having tile j (bit i = entry i)
+    // lane j: the round's entries having tile j (bit i = entry i).  Lane j
+    // walks them in entry (depth) order and fetches each entry's index and
+    // depth bits from its lane; the loop runs as often as the busiest tile
+    // of the round has entries.
     const uint64_t bt = transpose64(m);
-    const int bt_lo = (int)(uint32_t)bt, bt_hi = (int)(uint32_t)(bt >> 32);
-    // each lane walks its own tiles; the loop is uniform so every lane
-    // takes part in the permutes that fetch tile j's ballot and cursor
-    uint64_t mm = m;
-    while (__ballot(mm != 0ull) != 0ull) {
-      const bool act = mm != 0ull;
-      const int j = act ? (int)__builtin_ctzll(mm) : 0;
-      mm &= mm - 1ull;
-      const int src = j << 2;
-      const uint32_t blo = (uint32_t)__builtin_amdgcn_ds_bpermute(src, bt_lo);
-      const uint32_t bhi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, bt_hi);
-      const uint32_t cur_j = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)cur);
+    uint64_t b = bt;
+    uint32_t at = cur;
+    while (__ballot(b != 0ull) != 0ull) {
+      const bool act = b != 0ull;
+      const int src = act ? ((int)__builtin_ctzll(b) << 2) : 0;
+      b &= b - 1ull;
+      const uint32_t gi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)g);
+      const uint32_t dbi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)db);
       if (act) {
-        const uint64_t bj = (uint64_t)blo | ((uint64_t)bhi << 32);
-        const uint32_t at = cur_j + (uint32_t)__popcll(bj & lt);
         if (staged) {
           if (at < (uint32_t)kL2Stage) {
-            s_g[at] = g;
-            s_db[at] = db;
+            s_g[at] = gi;
+            s_db[at] = dbi;
           }
         } else if ((int64_t)at < K) {
-          const uint32_t tile = (uint32_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt));
-          keys[at] = ((uint64_t)tile << 32) | (uint64_t)db;
-          point_list[at] = g;
+          keys[at] = my_tile | (uint64_t)dbi;
+          point_list[at] = gi;
         }
+        ++at;
       }
     }
     cur += (uint32_t)__popcll(bt);  // lane j: tile j's entries in this round
