@@ -7,7 +7,9 @@
 // opacity), then every pixel blends the batch front to back.  Pixels stop at
 // T < 1e-4; a wavefront whose pixels have all stopped skips the blend loop,
 // and the workgroup leaves as soon as every pixel has stopped
-// (__syncthreads_count).  (A one-wavefront-per-tile form with per-strip row
+// (__syncthreads_count).  Batches whose colours are all finite blend without
+// the selects that keep a non-finite colour out of non-taking pixels.  (A
+// one-wavefront-per-tile form with per-strip row
 // culling measured slower: at 1M splats over 1080p most splats reach every
 // row of the tiles they touch, so culling removes little work and one
 // wavefront per tile hides less latency.)
@@ -22,7 +24,9 @@
 // skipped wave-uniformly; the pixel terms are computed without branches.  Per
 // splat, the 11 gradient terms are summed over the wave by permlane swaps and
 // DPP adds into an LDS record; each batch is flushed with global float
-// atomics whose lanes cover consecutive terms of a few splats.
+// atomics whose lanes cover consecutive terms of a few splats.  Given a
+// tile-order scratch, the tiles run heaviest first (by max_contrib), so the
+// light ones fill the end of the launch.
 #include "fgs_common.hpp"
 
 namespace fgs {
