@@ -87,7 +87,7 @@ struct FiniteTag {
 
 // kMode bit 0: write the sampled state; bit 1: count metric hits (get_flag).
 template <int NCH, int kMode>
-__global__ void __launch_bounds__(256, 5)
+__global__ void __launch_bounds__(256, 6)
 raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, RasterShape sh) {
   constexpr bool kSampled = (kMode & 1) != 0;
   constexpr bool kMetric = (kMode & 2) != 0;
