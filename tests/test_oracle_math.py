@@ -3,11 +3,15 @@
 orc_expf / orc_logf are the transcendental functions both the oracle and the
 HIP kernels implement with the same IEEE operations; here they are checked
 against float64 numpy within a few ulp.  The SH basis of orc_color_from_sh
-(fastgs_preprocess.metal:117-169) is checked for orthonormality on the
-sphere, which a dropped term, a wrong constant or a wrong coefficient index
-breaks.
+(fastgs_preprocess.metal:117-169) is checked function by function against
+scipy's spherical harmonics (which carry the Condon-Shortley phase), at the
+six axis directions, the eight cube diagonals and random directions: a
+flipped sign, a swapped index or a wrong constant of any one of the 16
+functions fails it.  Orthonormality on the sphere and the degree truncation
+are checked as well.
 """
 import numpy as np
+from scipy.special import sph_harm_y
 
 
 def test_expf_error_bound(oracle):
@@ -43,6 +47,90 @@ def _fibonacci_sphere(n):
     phi = np.arccos(1 - 2 * i / n)
     theta = np.pi * (1 + 5 ** 0.5) * i
     return np.stack([np.cos(theta) * np.sin(phi), np.sin(theta) * np.sin(phi), np.cos(phi)], 1)
+
+
+def _sh_basis_scipy(dirs):
+    """The 16 real SH functions of degree <= 3 in the coefficient order of
+    fastgs_preprocess.metal:117-169 (k = l*l + l + m, m = -l..l), from scipy's
+    complex Y_l^m (Condon-Shortley phase included):
+    sqrt(2) Im Y_l^|m| for m < 0, Y_l^0 for m = 0, sqrt(2) Re Y_l^m for m > 0."""
+    d = dirs / np.linalg.norm(dirs, axis=1, keepdims=True)
+    theta = np.arccos(np.clip(d[:, 2], -1.0, 1.0))  # polar angle from +z
+    phi = np.arctan2(d[:, 1], d[:, 0])  # azimuth from +x towards +y
+    out = np.zeros((16, d.shape[0]))
+    for l in range(4):
+        for m in range(-l, l + 1):
+            y = sph_harm_y(l, abs(m), theta, phi)
+            if m < 0:
+                v = np.sqrt(2.0) * y.imag
+            elif m == 0:
+                v = y.real
+            else:
+                v = np.sqrt(2.0) * y.real
+            out[l * l + l + m] = v
+    return out
+
+
+def _sh_basis_oracle(oracle64, dirs):
+    """Y_k(dir) read back through orc_color_from_sh: coefficient k = 0.1, the
+    others 0, colour = 0.5 + 0.1 Y_k (no clamp at |Y_k| <= 1.1)."""
+    Y = np.zeros((16, dirs.shape[0]))
+    for k in range(16):
+        dc = np.zeros(3)
+        sh = np.zeros((15, 3))
+        if k == 0:
+            dc[0] = 0.1
+        else:
+            sh[k - 1, 0] = 0.1
+        for j in range(dirs.shape[0]):
+            col, clamped = oracle64.color_from_sh(3, dirs[j], np.zeros(3), dc, sh)
+            assert not clamped.any()
+            Y[k, j] = (col[0] - 0.5) / 0.1
+    return Y
+
+
+def test_sh_basis_against_scipy(oracle64):
+    """Each of the 16 basis functions, sign included, equals scipy's at the axis
+    directions, the cube diagonals and random directions."""
+    axes = np.concatenate([np.eye(3), -np.eye(3)])
+    diag = np.array([[sx, sy, sz] for sx in (1, -1) for sy in (1, -1) for sz in (1, -1)], float)
+    rng = np.random.default_rng(7)
+    rand = rng.standard_normal((40, 3))
+    dirs = np.concatenate([axes, diag, rand])
+    got = _sh_basis_oracle(oracle64, dirs)
+    ref = _sh_basis_scipy(dirs)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-6)
+    # the check separates every pair of functions and both signs of each
+    for k in range(16):
+        assert np.abs(ref[k]).max() > 0.1
+        for j in range(16):
+            if j != k:
+                assert np.abs(ref[k] - ref[j]).max() > 0.1 and np.abs(ref[k] + ref[j]).max() > 0.1
+
+
+def test_sh_basis_known_values(oracle64):
+    """Hand-evaluated values of the degree-1 functions at the axes and of a
+    few higher ones at (1,1,1)/sqrt3, from the closed forms
+    Y_1 = -c1 y, c1 z, -c1 x with c1 = sqrt(3/(4 pi))."""
+    c1 = np.sqrt(3.0 / (4.0 * np.pi))
+    got = _sh_basis_oracle(oracle64, np.concatenate([np.eye(3), np.ones((1, 3))]))
+    np.testing.assert_allclose(got[1:4, 0], [0.0, 0.0, -c1], atol=1e-7)  # +x
+    np.testing.assert_allclose(got[1:4, 1], [-c1, 0.0, 0.0], atol=1e-7)  # +y
+    np.testing.assert_allclose(got[1:4, 2], [0.0, c1, 0.0], atol=1e-7)  # +z
+    # at (1,1,1)/sqrt3: xy = yz = xz = 1/3, 2zz - xx - yy = 0, xx - yy = 0
+    c2 = 0.5 * np.sqrt(15.0 / np.pi)
+    np.testing.assert_allclose(got[4:9, 3], [c2 / 3, -c2 / 3, 0.0, -c2 / 3, 0.0], atol=1e-7)
+    # degree 3 at (1,1,1)/sqrt3: xyz = 3^-1.5, the other six vanish or cancel
+    # except y(4zz-xx-yy) = x(4zz-xx-yy) = 2/3^1.5, y(3xx-yy) = 2/3^1.5,
+    # z(2zz-3xx-3yy) = -4/3^1.5, x(xx-3yy) = -2/3^1.5
+    s3 = 3.0 ** -1.5
+    k31 = 0.25 * np.sqrt(35.0 / (2 * np.pi))  # |m| = 3
+    k32 = 0.5 * np.sqrt(105.0 / np.pi)        # |m| = 2
+    k33 = 0.25 * np.sqrt(21.0 / (2 * np.pi))  # |m| = 1
+    k30 = 0.25 * np.sqrt(7.0 / np.pi)         # m = 0
+    want3 = [-k31 * 2 * s3, k32 * s3, -k33 * 2 * s3, k30 * -4 * s3, -k33 * 2 * s3, 0.0,
+             -k31 * -2 * s3]
+    np.testing.assert_allclose(got[9:16, 3], want3, atol=1e-7)
 
 
 def test_sh_basis_orthonormal(oracle64):
