@@ -699,11 +699,21 @@ void orc_rasterize_fwd(const orc_rparams* rp, const uint32_t* ranges, const uint
 /* the forward front to back and accumulating in reverse.                    */
 /* Gradient arrays are accumulated into (zero them first).                   */
 /* ------------------------------------------------------------------------ */
-void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint32_t* point_list,
-                       const real* means2d, const real* colors, const real* conic_opacity,
-                       const real* background, const real* final_t, const uint32_t* n_contrib,
-                       const real* dL_dout, real* dmeans2d, real* dcolors, real* dconic,
-                       real* dvsp) {
+/* mag (optional, NULL: not computed): two magnitudes of every gradient entry,
+ * accumulated in double and laid out [P][2][10 + NC], each row ordered as
+ * (means2d x, y, viewspace x, y, |x|, |y|, conic a, b, c, opacity, colours):
+ *  [0] the sum over its (pixel, splat) terms of the term's magnitude with every
+ *      sum inside the term replaced by the sum of its summands' magnitudes
+ *      (|a + b| -> |a| + |b|): an implementation that evaluates the same terms
+ *      in another order, recovers T another way or sums them in another order
+ *      differs from these gradients by a small multiple of float epsilon
+ *      times it;
+ *  [1] the sum over its terms of |term|. */
+void orc_rasterize_bwd_mag(const orc_rparams* rp, const uint32_t* ranges,
+                           const uint32_t* point_list, const real* means2d, const real* colors,
+                           const real* conic_opacity, const real* background, const real* final_t,
+                           const uint32_t* n_contrib, const real* dL_dout, real* dmeans2d,
+                           real* dcolors, real* dconic, real* dvsp, double* mag, int64_t mag_rows) {
   const int W = rp->image_width, H = rp->image_height;
   const int gx = (W + ORC_TILE - 1) / ORC_TILE;
   const int gy = (H + ORC_TILE - 1) / ORC_TILE;
@@ -725,15 +735,29 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
     if (point_list[i] + 1 > gn) gn = point_list[i] + 1;
   const int AW = 10 + NC; /* means2d 2, vsp 4, conic 4, colours NC */
   double* acc = (double*)calloc((size_t)gn * AW + 1, sizeof(double));
+  double* macc = mag ? (double*)calloc((size_t)gn * AW * 2 + 1, sizeof(double)) : NULL;
 #pragma omp parallel
   {
     int cap = 0;
     uint32_t* rec_g = NULL;
+    uint32_t* rec_j = NULL; /* the splat's position in the tile's list */
     real* rec = NULL; /* per contributing splat: alpha, G, T, dx, dy */
+    size_t tcap = 0;
+    double* tb = NULL; /* per list position: AW sums, then 2 AW magnitudes */
 #pragma omp for schedule(dynamic, 1)
     for (int tile = 0; tile < ntiles; ++tile) {
       int tx = tile % gx, ty = tile / gx;
       uint32_t start = ranges[2 * tile], end = ranges[2 * tile + 1];
+      if (end <= start) continue;
+      /* the tile's terms are summed per list position here, then added to
+       * the per-Gaussian sums once per (tile, splat) */
+      const size_t tw = (size_t)(macc ? 3 : 1) * AW;
+      const size_t tn = (size_t)(end - start) * tw;
+      if (tn > tcap) {
+        tcap = tn * 2;
+        tb = (double*)realloc(tb, tcap * sizeof(double));
+      }
+      memset(tb, 0, tn * sizeof(double));
       for (int ly = 0; ly < ORC_TILE; ++ly) {
         for (int lx = 0; lx < ORC_TILE; ++lx) {
           int px = tx * ORC_TILE + lx, py = ty * ORC_TILE + ly;
@@ -744,6 +768,7 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
           if ((int)n > cap) {
             cap = (int)n * 2;
             rec_g = (uint32_t*)realloc(rec_g, (size_t)cap * 4);
+            rec_j = (uint32_t*)realloc(rec_j, (size_t)cap * 4);
             rec = (real*)realloc(rec, (size_t)cap * 5 * sizeof(real));
           }
           real pxf = (real)px, pyf = (real)py;
@@ -760,6 +785,7 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
             real alpha = RMIN((real)0.99, co[3] * G);
             if (alpha < (real)1 / (real)255) continue;
             rec_g[m] = g;
+            rec_j[m] = j;
             rec[5 * m + 0] = alpha;
             rec[5 * m + 1] = G;
             rec[5 * m + 2] = T;
@@ -772,25 +798,59 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
           real dL[3] = {0, 0, 0};
           for (int c = 0; c < C; ++c) dL[c] = dL_dout[c * HW + pix];
           real bg_dot = 0;
-          for (int c = 0; c < C; ++c) bg_dot += background[c] * dL[c];
+          double bg_abs = 0;
+          for (int c = 0; c < C; ++c) {
+            bg_dot += background[c] * dL[c];
+            bg_abs += fabs((double)background[c] * (double)dL[c]);
+          }
           real S[3] = {0, 0, 0}; /* sum over later splats of c*alpha*T */
+          double Sm[3] = {0, 0, 0}; /* sum over later splats of |c|*alpha*T */
           for (int k = m - 1; k >= 0; --k) {
             uint32_t g = rec_g[k];
+            double* ta = tb + (size_t)rec_j[k] * tw; /* sums of this splat's terms */
+            double* tmg = ta + AW;                  /* and of their magnitudes */
             real alpha = rec[5 * k + 0], G = rec[5 * k + 1], Tj = rec[5 * k + 2];
             real dx = rec[5 * k + 3], dy = rec[5 * k + 4];
             const real* co = conic_opacity + 4 * (size_t)g;
             real rci = (real)1 / ((real)1 - alpha);
             real dL_dalpha = 0;
+            double ma = 0; /* magnitude of dL_dalpha */
             for (int c = 0; c < C; ++c) {
               real col = colors[(size_t)g * NC + c];
               real dcol = alpha * Tj * dL[c];
-#pragma omp atomic
-              acc[(size_t)g * AW + 10 + c] += (double)dcol;
+              ta[10 + c] += (double)dcol;
               dL_dalpha += (col * Tj - rci * S[c]) * dL[c];
               S[c] += col * alpha * Tj;
+              if (macc) {
+                const double adl = fabs((double)dL[c]);
+                tmg[10 + c] += (double)alpha * (double)Tj * adl;
+                tmg[AW + 10 + c] += fabs((double)dcol);
+                ma += (fabs((double)col) * (double)Tj + (double)rci * Sm[c]) * adl;
+                Sm[c] += fabs((double)col) * (double)alpha * (double)Tj;
+              }
             }
             dL_dalpha += (-Tf * rci) * bg_dot;
+            ma += fabs((double)Tf * (double)rci) * bg_abs;
             if (co[3] * G > (real)0.99) continue;
+            if (macc) {
+              const double mG = fabs((double)co[3]) * ma; /* |dL_dG| */
+              const double gx_ = fabs((double)G * (double)dx), gy_ = fabs((double)G * (double)dy);
+              const double mx = mG * (gx_ * fabs((double)co[0]) + gy_ * fabs((double)co[1])) *
+                                fabs((double)ddelx_dx);
+              const double my = mG * (gy_ * fabs((double)co[2]) + gx_ * fabs((double)co[1])) *
+                                fabs((double)ddely_dy);
+              double* b = tmg;
+              b[0] += mx;
+              b[1] += my;
+              b[2] += mx;
+              b[3] += my;
+              b[4] += mx;
+              b[5] += my;
+              b[6] += 0.5 * gx_ * fabs((double)dx) * mG;
+              b[7] += 0.5 * gx_ * fabs((double)dy) * mG;
+              b[8] += 0.5 * gy_ * fabs((double)dy) * mG;
+              b[9] += (double)G * ma;
+            }
             real dL_dG = co[3] * dL_dalpha;
             real gdx = G * dx, gdy = G * dy;
             real dG_ddelx = -gdx * co[0] - gdy * co[1];
@@ -801,33 +861,54 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
             real v1 = (real)-0.5 * gdx * dy * dL_dG;
             real v2 = (real)-0.5 * gdy * dy * dL_dG;
             real v3 = G * dL_dalpha;
-            double* a = acc + (size_t)g * AW;
-#pragma omp atomic
+            double* a = ta;
             a[0] += (double)tmp_x;
-#pragma omp atomic
             a[1] += (double)tmp_y;
-#pragma omp atomic
             a[2] += (double)tmp_x;
-#pragma omp atomic
             a[3] += (double)tmp_y;
-#pragma omp atomic
             a[4] += (double)RABS(tmp_x);
-#pragma omp atomic
             a[5] += (double)RABS(tmp_y);
-#pragma omp atomic
             a[6] += (double)v0;
-#pragma omp atomic
             a[7] += (double)v1;
-#pragma omp atomic
             a[8] += (double)v2;
-#pragma omp atomic
             a[9] += (double)v3;
+            if (macc) {
+              double* t = tmg + AW;
+              const double ax = fabs((double)tmp_x), ay = fabs((double)tmp_y);
+              t[0] += ax;
+              t[1] += ay;
+              t[2] += ax;
+              t[3] += ay;
+              t[4] += ax;
+              t[5] += ay;
+              t[6] += fabs((double)v0);
+              t[7] += fabs((double)v1);
+              t[8] += fabs((double)v2);
+              t[9] += fabs((double)v3);
+            }
           }
         }
       }
+      for (uint32_t j = 0; j < end - start; ++j) {
+        const double* ta = tb + (size_t)j * tw;
+        const uint32_t g = point_list[start + j];
+        for (int q = 0; q < AW; ++q)
+          if (ta[q] != 0.0) {
+#pragma omp atomic
+            acc[(size_t)g * AW + q] += ta[q];
+          }
+        if (macc)
+          for (int q = 0; q < 2 * AW; ++q)
+            if (ta[AW + q] != 0.0) {
+#pragma omp atomic
+              macc[(size_t)g * AW * 2 + q] += ta[AW + q];
+            }
+      }
     }
     free(rec_g);
+    free(rec_j);
     free(rec);
+    free(tb);
   }
   for (uint32_t g = 0; g < gn; ++g) {
     const double* a = acc + (size_t)g * AW;
@@ -837,7 +918,22 @@ void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint
     for (int q = 0; q < 4; ++q) dconic[4 * (size_t)g + q] += (real)a[6 + q];
     for (int c = 0; c < C; ++c) dcolors[(size_t)g * NC + c] += (real)a[10 + c];
   }
+  if (macc) {
+    const int64_t rows = (int64_t)gn < mag_rows ? (int64_t)gn : mag_rows;
+    for (int64_t g = 0; g < rows; ++g)
+      for (int q = 0; q < 2 * AW; ++q) mag[(size_t)g * AW * 2 + q] += macc[(size_t)g * AW * 2 + q];
+  }
   free(acc);
+  free(macc);
+}
+
+void orc_rasterize_bwd(const orc_rparams* rp, const uint32_t* ranges, const uint32_t* point_list,
+                       const real* means2d, const real* colors, const real* conic_opacity,
+                       const real* background, const real* final_t, const uint32_t* n_contrib,
+                       const real* dL_dout, real* dmeans2d, real* dcolors, real* dconic,
+                       real* dvsp) {
+  orc_rasterize_bwd_mag(rp, ranges, point_list, means2d, colors, conic_opacity, background,
+                        final_t, n_contrib, dL_dout, dmeans2d, dcolors, dconic, dvsp, NULL, 0);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1065,6 +1161,241 @@ void orc_preprocess_bwd(const orc_params* prm, const real* means3d, const real* 
     for (int k = 0; k < 4; ++k) dL_dvsp_in[4 * (size_t)i + k] = dL_dvsp_out[4 * (size_t)i + k];
   }
 }
+
+/* Sums of term magnitudes through the preprocess backward (orc_preprocess_bwd,
+ * fastgs_preprocess_backward.metal:60-430).  The backward is linear in its
+ * cotangents; every output entry is a sum of products of forward-derived
+ * scalars (T, the covariances, the conic's denominators, R, s, the SH
+ * coefficients and direction, ...) with cotangents.  This evaluates the same
+ * expression tree with each sum replaced by the sum of its summands'
+ * magnitudes and each product by the product of magnitudes: the forward
+ * scalars enter as |value|, the cotangents as the given magnitudes m_* (the
+ * sums of their own terms' magnitudes, from orc_rasterize_bwd_mag).  The
+ * result is, per entry, the sum of |term| over the fully expanded chain rule:
+ * the scale of the rounding differences of two evaluations of these sums
+ * that order or round them differently.  Outputs (double, accumulated with
+ * +=): the magnitudes of dL_dmeans3d, dL_ddc, dL_dsh, dL_dcolors_precomp,
+ * dL_dopacities, dL_dscales, dL_dquats, dL_dvsp_in. */
+#define AB(x) fabs((double)(x))
+void orc_preprocess_bwd_mag(const orc_params* prm, const real* means3d, const real* scales,
+                            const real* quats, const real* viewmat, const real* projmat,
+                            const real* cam_pos, const real* sh, const real* cov3d_precomp,
+                            const real* cov3d_fwd, const double* m_cov3d, const double* m_rgb,
+                            const double* m_xys, const double* m_conic, const double* m_vsp,
+                            const int32_t* radii, const uint8_t* clamped, double* o_means3d,
+                            double* o_dc, double* o_sh, double* o_colors_precomp,
+                            double* o_opacities, double* o_scales, double* o_quats,
+                            double* o_vsp) {
+  const int P = prm->P;
+  const real focal_x = (real)(0.5f * (float)prm->image_width / fmaxf(prm->tan_fovx, 1e-6f));
+  const real focal_y = (real)(0.5f * (float)prm->image_height / fmaxf(prm->tan_fovy, 1e-6f));
+#pragma omp parallel for schedule(static, 1024)
+  for (int i = 0; i < P; ++i) {
+    if (!(radii[i] > 0)) continue;
+    const real* p = means3d + 3 * (size_t)i;
+    real ph[4];
+    xform44(projmat, p[0], p[1], p[2], ph);
+    const double gx = m_xys[2 * (size_t)i + 0], gy = m_xys[2 * (size_t)i + 1];
+    const real* cov_src = (prm->use_cov3d_precomp ? cov3d_precomp : cov3d_fwd) + 6 * (size_t)i;
+    const double cg0 = m_conic[4 * (size_t)i + 0];
+    const double cg1 = m_conic[4 * (size_t)i + 1];
+    const double cg2 = m_conic[4 * (size_t)i + 2];
+    double dce[6] = {0, 0, 0, 0, 0, 0};
+    double dmc[3] = {0, 0, 0};
+    {
+      orc_cov2d cv;
+      cov2d_eval(viewmat, p, focal_x, focal_y, (real)prm->tan_fovx, (real)prm->tan_fovy, cov_src,
+                 &cv);
+      const double xg = (cv.txtz < -cv.limx || cv.txtz > cv.limx) ? 0.0 : 1.0;
+      const double yg = (cv.tytz < -cv.limy || cv.tytz > cv.limy) ? 0.0 : 1.0;
+      double T[3][3], V[3][3], Wm[3][3];
+      for (int c = 0; c < 3; ++c)
+        for (int r = 0; r < 3; ++r) {
+          T[c][r] = AB(cv.T[c][r]);
+          Wm[c][r] = AB(viewmat[4 * c + r]);
+        }
+      const double vv[6] = {AB(cov_src[0]), AB(cov_src[1]), AB(cov_src[2]),
+                            AB(cov_src[3]), AB(cov_src[4]), AB(cov_src[5])};
+      V[0][0] = vv[0]; V[0][1] = vv[1]; V[0][2] = vv[2];
+      V[1][0] = vv[1]; V[1][1] = vv[3]; V[1][2] = vv[4];
+      V[2][0] = vv[2]; V[2][1] = vv[4]; V[2][2] = vv[5];
+      const real a_ = cv.cov00 + (real)0.3, b_ = cv.cov01, c_ = cv.cov11 + (real)0.3;
+      const real den_ = a_ * c_ - b_ * b_;
+      const double a = AB(a_), b = AB(b_), c = AB(c_), den = AB(den_);
+      const double d2i = AB((real)1 / ((den_ * den_) + (real)1e-7));
+      double da = 0, db = 0, dc = 0;
+      if (d2i != 0.0) {
+        const double dm_ac = den + a * c; /* |denom| + |a c| */
+        da = d2i * (c * c * cg0 + 2 * b * c * cg1 + dm_ac * cg2);
+        dc = d2i * (a * a * cg2 + 2 * a * b * cg1 + dm_ac * cg0);
+        db = d2i * 2 * (b * c * cg0 + (den + 2 * b * b) * cg1 + a * b * cg2);
+        dce[0] = T[0][0] * T[0][0] * da + T[0][0] * T[1][0] * db + T[1][0] * T[1][0] * dc;
+        dce[3] = T[0][1] * T[0][1] * da + T[0][1] * T[1][1] * db + T[1][1] * T[1][1] * dc;
+        dce[5] = T[0][2] * T[0][2] * da + T[0][2] * T[1][2] * db + T[1][2] * T[1][2] * dc;
+        dce[1] = 2 * T[0][0] * T[0][1] * da + (T[0][0] * T[1][1] + T[0][1] * T[1][0]) * db +
+                 2 * T[1][0] * T[1][1] * dc;
+        dce[2] = 2 * T[0][0] * T[0][2] * da + (T[0][0] * T[1][2] + T[0][2] * T[1][0]) * db +
+                 2 * T[1][0] * T[1][2] * dc;
+        dce[4] = 2 * T[0][2] * T[0][1] * da + (T[0][1] * T[1][2] + T[0][2] * T[1][1]) * db +
+                 2 * T[1][1] * T[1][2] * dc;
+      }
+      double dT0[3], dT1[3];
+      for (int k = 0; k < 3; ++k) {
+        const double u0 = T[0][0] * V[k][0] + T[0][1] * V[k][1] + T[0][2] * V[k][2];
+        const double u1 = T[1][0] * V[k][0] + T[1][1] * V[k][1] + T[1][2] * V[k][2];
+        dT0[k] = 2 * u0 * da + u1 * db;
+        dT1[k] = 2 * u1 * dc + u0 * db;
+      }
+      const double dJ00 = Wm[0][0] * dT0[0] + Wm[0][1] * dT0[1] + Wm[0][2] * dT0[2];
+      const double dJ02 = Wm[2][0] * dT0[0] + Wm[2][1] * dT0[1] + Wm[2][2] * dT0[2];
+      const double dJ11 = Wm[1][0] * dT1[0] + Wm[1][1] * dT1[1] + Wm[1][2] * dT1[2];
+      const double dJ12 = Wm[2][0] * dT1[0] + Wm[2][1] * dT1[1] + Wm[2][2] * dT1[2];
+      const real tzr = (real)1 / cv.t[2];
+      const double tz = AB(tzr), tz2 = AB(tzr * tzr), tz3 = AB(tzr * tzr * tzr);
+      const double fx = AB(focal_x), fy = AB(focal_y);
+      const double dtx = xg * fx * tz2 * dJ02;
+      const double dty = yg * fy * tz2 * dJ12;
+      const double dtz = fx * tz2 * dJ00 + fy * tz2 * dJ11 + (2 * fx * AB(cv.t[0])) * tz3 * dJ02 +
+                         (2 * fy * AB(cv.t[1])) * tz3 * dJ12;
+      (void)tz;
+      for (int k = 0; k < 3; ++k)
+        dmc[k] = AB(viewmat[4 * k]) * dtx + AB(viewmat[4 * k + 1]) * dty +
+                 AB(viewmat[4 * k + 2]) * dtz;
+    }
+    const real m_w_ = (real)1 / (ph[3] + (real)1.0e-7);
+    const double mw = AB(m_w_);
+    const double mul1 = (AB(projmat[0] * p[0]) + AB(projmat[4] * p[1]) + AB(projmat[8] * p[2]) +
+                         AB(projmat[12])) * mw * mw;
+    const double mul2 = (AB(projmat[1] * p[0]) + AB(projmat[5] * p[1]) + AB(projmat[9] * p[2]) +
+                         AB(projmat[13])) * mw * mw;
+    double dm[3];
+    for (int k = 0; k < 3; ++k)
+      dm[k] = (AB(projmat[4 * k]) * mw + AB(projmat[4 * k + 3]) * mul1) * gx +
+              (AB(projmat[4 * k + 1]) * mw + AB(projmat[4 * k + 3]) * mul2) * gy + dmc[k];
+    o_opacities[i] += m_conic[4 * (size_t)i + 3];
+    if (prm->use_colors_precomp) {
+      for (int c = 0; c < 3; ++c) o_colors_precomp[3 * (size_t)i + c] += m_rgb[3 * (size_t)i + c];
+    } else {
+      double dRGB[3];
+      for (int c = 0; c < 3; ++c) dRGB[c] = clamped[3 * (size_t)i + c] ? 0.0 : m_rgb[3 * (size_t)i + c];
+      for (int c = 0; c < 3; ++c) o_dc[3 * (size_t)i + c] += AB(SH_C0) * dRGB[c];
+      const int msh = prm->max_sh_coeffs;
+      if (prm->degree > 0 && msh >= 3) {
+        real dir_orig[3] = {p[0] - cam_pos[0], p[1] - cam_pos[1], p[2] - cam_pos[2]};
+        real len = RSQRT(dir_orig[0] * dir_orig[0] + dir_orig[1] * dir_orig[1] + dir_orig[2] * dir_orig[2]);
+        const double x = AB(dir_orig[0] / len), y = AB(dir_orig[1] / len), z = AB(dir_orig[2] / len);
+        const real* sr = sh + (size_t)i * (size_t)msh * 3;
+        double* ds = o_sh + (size_t)i * (size_t)msh * 3;
+        double ex[3], ey[3], ez[3];
+        const double C1 = AB(SH_C1);
+        for (int c = 0; c < 3; ++c) {
+          ds[0 * 3 + c] += C1 * y * dRGB[c];
+          ds[1 * 3 + c] += C1 * z * dRGB[c];
+          ds[2 * 3 + c] += C1 * x * dRGB[c];
+          ex[c] = C1 * AB(sr[2 * 3 + c]);
+          ey[c] = C1 * AB(sr[0 * 3 + c]);
+          ez[c] = C1 * AB(sr[1 * 3 + c]);
+        }
+        if (prm->degree > 1 && msh >= 8) {
+          const double xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+          double C2[5], C3[7];
+          for (int k = 0; k < 5; ++k) C2[k] = AB(SH_C2[k]);
+          for (int k = 0; k < 7; ++k) C3[k] = AB(SH_C3[k]);
+          for (int c = 0; c < 3; ++c) {
+            ds[3 * 3 + c] += C2[0] * xy * dRGB[c];
+            ds[4 * 3 + c] += C2[1] * yz * dRGB[c];
+            ds[5 * 3 + c] += C2[2] * (2 * zz + xx + yy) * dRGB[c];
+            ds[6 * 3 + c] += C2[3] * xz * dRGB[c];
+            ds[7 * 3 + c] += C2[4] * (xx + yy) * dRGB[c];
+            const double s3 = AB(sr[3 * 3 + c]), s4 = AB(sr[4 * 3 + c]), s5 = AB(sr[5 * 3 + c]),
+                         s6 = AB(sr[6 * 3 + c]), s7 = AB(sr[7 * 3 + c]);
+            ex[c] += C2[0] * y * s3 + C2[2] * 2 * x * s5 + C2[3] * z * s6 + C2[4] * 2 * x * s7;
+            ey[c] += C2[0] * x * s3 + C2[1] * z * s4 + C2[2] * 2 * y * s5 + C2[4] * 2 * y * s7;
+            ez[c] += C2[1] * y * s4 + C2[2] * 4 * z * s5 + C2[3] * x * s6;
+          }
+          if (prm->degree > 2 && msh >= 15) {
+            for (int c = 0; c < 3; ++c) {
+              ds[8 * 3 + c] += C3[0] * y * (3 * xx + yy) * dRGB[c];
+              ds[9 * 3 + c] += C3[1] * xy * z * dRGB[c];
+              ds[10 * 3 + c] += C3[2] * y * (4 * zz + xx + yy) * dRGB[c];
+              ds[11 * 3 + c] += C3[3] * z * (2 * zz + 3 * xx + 3 * yy) * dRGB[c];
+              ds[12 * 3 + c] += C3[4] * x * (4 * zz + xx + yy) * dRGB[c];
+              ds[13 * 3 + c] += C3[5] * z * (xx + yy) * dRGB[c];
+              ds[14 * 3 + c] += C3[6] * x * (xx + 3 * yy) * dRGB[c];
+              const double s8 = AB(sr[8 * 3 + c]), s9 = AB(sr[9 * 3 + c]), s10 = AB(sr[10 * 3 + c]),
+                           s11 = AB(sr[11 * 3 + c]), s12 = AB(sr[12 * 3 + c]),
+                           s13 = AB(sr[13 * 3 + c]), s14 = AB(sr[14 * 3 + c]);
+              ex[c] += C3[0] * s8 * 6 * xy + C3[1] * s9 * yz + C3[2] * s10 * 2 * xy +
+                       C3[3] * s11 * 6 * xz + C3[4] * s12 * (3 * xx + 4 * zz + yy) +
+                       C3[5] * s13 * 2 * xz + C3[6] * s14 * 3 * (xx + yy);
+              ey[c] += C3[0] * s8 * 3 * (xx + yy) + C3[1] * s9 * xz +
+                       C3[2] * s10 * (3 * yy + 4 * zz + xx) + C3[3] * s11 * 6 * yz +
+                       C3[4] * s12 * 2 * xy + C3[5] * s13 * 2 * yz + C3[6] * s14 * 6 * xy;
+              ez[c] += C3[1] * s9 * xy + C3[2] * s10 * 8 * yz +
+                       C3[3] * s11 * 3 * (2 * zz + xx + yy) + C3[4] * s12 * 8 * xz +
+                       C3[5] * s13 * (xx + yy);
+            }
+          }
+        }
+        const double dd[3] = {ex[0] * dRGB[0] + ex[1] * dRGB[1] + ex[2] * dRGB[2],
+                              ey[0] * dRGB[0] + ey[1] * dRGB[1] + ey[2] * dRGB[2],
+                              ez[0] * dRGB[0] + ez[1] * dRGB[1] + ez[2] * dRGB[2]};
+        real l_ = RMAX(RSQRT(dir_orig[0] * dir_orig[0] + dir_orig[1] * dir_orig[1] + dir_orig[2] * dir_orig[2]), (real)1e-6);
+        const double l = AB(l_);
+        const double nv[3] = {AB(dir_orig[0] / l_), AB(dir_orig[1] / l_), AB(dir_orig[2] / l_)};
+        const double nd = nv[0] * dd[0] + nv[1] * dd[1] + nv[2] * dd[2];
+        for (int k = 0; k < 3; ++k) dm[k] += (dd[k] + nv[k] * nd) / l;
+      }
+    }
+    for (int k = 0; k < 3; ++k) o_means3d[3 * (size_t)i + k] += dm[k];
+    if (!prm->use_cov3d_precomp) {
+      const real* sc = scales + 3 * (size_t)i;
+      const real* q = quats + 4 * (size_t)i;
+      const real r_ = q[0], x_ = q[1], y_ = q[2], z_ = q[3];
+      real R_[3][3];
+      R_[0][0] = (real)1 - (real)2 * (y_ * y_ + z_ * z_);
+      R_[0][1] = (real)2 * (x_ * y_ - r_ * z_);
+      R_[0][2] = (real)2 * (x_ * z_ + r_ * y_);
+      R_[1][0] = (real)2 * (x_ * y_ + r_ * z_);
+      R_[1][1] = (real)1 - (real)2 * (x_ * x_ + z_ * z_);
+      R_[1][2] = (real)2 * (y_ * z_ - r_ * x_);
+      R_[2][0] = (real)2 * (x_ * z_ - r_ * y_);
+      R_[2][1] = (real)2 * (y_ * z_ + r_ * x_);
+      R_[2][2] = (real)1 - (real)2 * (x_ * x_ + y_ * y_);
+      double R[3][3], M[3][3];
+      const double s3[3] = {AB((real)prm->scale_modifier * sc[0]), AB((real)prm->scale_modifier * sc[1]),
+                            AB((real)prm->scale_modifier * sc[2])};
+      for (int c = 0; c < 3; ++c)
+        for (int rr = 0; rr < 3; ++rr) {
+          R[c][rr] = AB(R_[c][rr]);
+          M[c][rr] = AB((real)s3[rr] * R_[c][rr]);
+        }
+      double cc[6];
+      for (int k = 0; k < 6; ++k) cc[k] = (m_cov3d ? m_cov3d[6 * (size_t)i + k] : 0.0) + dce[k];
+      const double dS[3][3] = {{cc[0], 0.5 * cc[1], 0.5 * cc[2]},
+                               {0.5 * cc[1], cc[3], 0.5 * cc[4]},
+                               {0.5 * cc[2], 0.5 * cc[4], cc[5]}};
+      double dM[3][3], dMt[3][3];
+      for (int c = 0; c < 3; ++c)
+        for (int rr = 0; rr < 3; ++rr)
+          dM[c][rr] = 2 * M[0][rr] * dS[c][0] + 2 * M[1][rr] * dS[c][1] + 2 * M[2][rr] * dS[c][2];
+      for (int a = 0; a < 3; ++a)
+        for (int bb = 0; bb < 3; ++bb) dMt[a][bb] = dM[bb][a];
+      for (int a = 0; a < 3; ++a)
+        o_scales[3 * (size_t)i + a] += R[0][a] * dMt[a][0] + R[1][a] * dMt[a][1] + R[2][a] * dMt[a][2];
+      for (int a = 0; a < 3; ++a)
+        for (int bb = 0; bb < 3; ++bb) dMt[a][bb] *= s3[a];
+      const double r = AB(r_), x = AB(x_), y = AB(y_), z = AB(z_);
+      double* oq = o_quats + 4 * (size_t)i;
+      oq[0] += 2 * z * (dMt[0][1] + dMt[1][0]) + 2 * y * (dMt[2][0] + dMt[0][2]) + 2 * x * (dMt[1][2] + dMt[2][1]);
+      oq[1] += 2 * y * (dMt[1][0] + dMt[0][1]) + 2 * z * (dMt[2][0] + dMt[0][2]) + 2 * r * (dMt[1][2] + dMt[2][1]) + 4 * x * (dMt[2][2] + dMt[1][1]);
+      oq[2] += 2 * x * (dMt[1][0] + dMt[0][1]) + 2 * r * (dMt[2][0] + dMt[0][2]) + 2 * z * (dMt[1][2] + dMt[2][1]) + 4 * y * (dMt[2][2] + dMt[0][0]);
+      oq[3] += 2 * r * (dMt[0][1] + dMt[1][0]) + 2 * x * (dMt[2][0] + dMt[0][2]) + 2 * y * (dMt[1][2] + dMt[2][1]) + 4 * z * (dMt[1][1] + dMt[0][0]);
+    }
+    for (int k = 0; k < 4; ++k) o_vsp[4 * (size_t)i + k] += m_vsp[4 * (size_t)i + k];
+  }
+}
+#undef AB
 
 int orc_sizeof_real(void) { return (int)sizeof(real); }
 

@@ -24,6 +24,10 @@ Parity status of each C function (how it is pinned; see tests/test_oracle_*):
   orc_rasterize_fwd        : closed form single splat (rasterize_smoke), brute
                              force per-pixel compositing on tiny scenes.
   orc_rasterize_bwd        : central finite differences of the double build.
+  orc_rasterize_bwd_mag    : equal to the per-pixel sums of |gradient| of the
+  orc_preprocess_bwd_mag     FD-pinned backward, bound the gradients, bound the
+                             f32 vs f64 differences of ill-conditioned rows
+                             (test_oracle_mag).
   orc_preprocess_bwd       : central finite differences of the double build and
                              the preprocess_backward_validation KAT (0.01).
 """
@@ -260,7 +264,12 @@ class Oracle:
 
     def rasterize_bwd(self, ranges, point_list, means2d, colors, conic_opacity, background,
                       final_t, n_contrib, dL_dout, image_width, image_height, num_channels=3,
-                      num_tiles=None):
+                      num_tiles=None, magnitude=False):
+        """Gradients of the blend.  With ``magnitude`` also, for every gradient
+        entry, float64 arrays of the gradients' keys and shapes
+        (orc_rasterize_bwd_mag): ``g["mag_terms"]`` = sum over its (pixel,
+        splat) terms of |term|, the scale of the gradient gate; ``g["mag"]`` =
+        the same sum with every sum inside a term also taken over magnitudes."""
         gx = (image_width + TILE - 1) // TILE
         gy = (image_height + TILE - 1) // TILE
         if num_tiles is None:
@@ -275,13 +284,22 @@ class Oracle:
             "viewspace_points": np.zeros((P, 4), dt),
         }
         rp = OrcRParams(image_width, image_height, num_channels, num_tiles, 0, 0, 0)
-        self.lib.orc_rasterize_bwd(
-            ctypes.byref(rp), _ptr(np.ascontiguousarray(ranges, np.uint32)),
-            _ptr(np.ascontiguousarray(point_list, np.uint32)), _ptr(means2d),
-            _ptr(self._f(colors)), _ptr(self._f(conic_opacity)), _ptr(self._f(background, (-1,))),
-            _ptr(self._f(final_t, (-1,))), _ptr(np.ascontiguousarray(n_contrib, np.uint32)),
-            _ptr(self._f(dL_dout)), _ptr(g["means2d"]), _ptr(g["colors"]),
-            _ptr(g["conic_opacity"]), _ptr(g["viewspace_points"]))
+        aw = 10 + num_channels
+        mag = np.zeros((P, 2, aw), np.float64) if magnitude else None
+        fn = self.lib.orc_rasterize_bwd_mag
+        fn.restype = None
+        fn.argtypes = [c_void_p] * 15 + [c_int64]
+        fn(ctypes.byref(rp), _ptr(np.ascontiguousarray(ranges, np.uint32)),
+           _ptr(np.ascontiguousarray(point_list, np.uint32)), _ptr(means2d),
+           _ptr(self._f(colors)), _ptr(self._f(conic_opacity)), _ptr(self._f(background, (-1,))),
+           _ptr(self._f(final_t, (-1,))), _ptr(np.ascontiguousarray(n_contrib, np.uint32)),
+           _ptr(self._f(dL_dout)), _ptr(g["means2d"]), _ptr(g["colors"]),
+           _ptr(g["conic_opacity"]), _ptr(g["viewspace_points"]), _ptr(mag), P)
+        if magnitude:
+            for key, j in (("mag", 0), ("mag_terms", 1)):
+                m = mag[:, j]
+                g[key] = {"means2d": m[:, 0:2], "viewspace_points": m[:, 2:6],
+                          "conic_opacity": m[:, 6:10], "colors": m[:, 10:10 + num_channels]}
         return g
 
     def preprocess_bwd(self, means3d, viewmatrix, projmatrix, campos, radii, cov3d_fwd, clamped,
@@ -323,6 +341,44 @@ class Oracle:
             *[_ptr(g[k]) for k in ("means3d", "dc", "sh", "colors_precomp", "opacities", "scales",
                                    "rotations", "viewspace_points")])
         return g
+
+    def preprocess_bwd_mag(self, means3d, viewmatrix, projmatrix, campos, radii, cov3d_fwd,
+                           clamped, m_xys, m_rgb, m_conic_opacity, m_vsp, image_width,
+                           image_height, tan_fovx=1.0, tan_fovy=1.0, degree=0,
+                           scale_modifier=1.0, m_cov3d=None, sh=None, scales=None,
+                           rotations=None, cov3d_precomp=None, use_colors_precomp=False):
+        """orc_preprocess_bwd_mag: the sums of term magnitudes of every output of
+        preprocess_bwd, given the magnitudes (float64) of its cotangents."""
+        means3d = self._f(means3d)
+        P = means3d.shape[0]
+        use_cov = cov3d_precomp is not None
+        sh_arr = self._f(sh) if sh is not None else np.zeros((P, 0, 3), self.dt)
+        max_sh = sh_arr.shape[1] if sh_arr.ndim >= 2 else 0
+        prm = OrcParams(P, degree, max_sh, image_width, image_height, 0, 0, int(use_cov),
+                        int(use_colors_precomp), scale_modifier, 1.0, tan_fovx, tan_fovy)
+        d = lambda a, shape: np.ascontiguousarray(np.asarray(a, np.float64).reshape(shape))  # noqa
+        out = {
+            "means3d": np.zeros((P, 3)), "dc": np.zeros((P, 3)), "sh": np.zeros(sh_arr.shape),
+            "colors_precomp": np.zeros((P, 3)), "opacities": np.zeros(P),
+            "scales": np.zeros((P, 3)), "rotations": np.zeros((P, 4)),
+            "viewspace_points": np.zeros((P, 4)),
+        }
+        fn = self.lib.orc_preprocess_bwd_mag
+        fn.restype = None
+        fn.argtypes = [c_void_p] * 25
+        fn(ctypes.byref(prm), _ptr(means3d),
+           _ptr(self._f(scales, (P, 3)) if not use_cov else None),
+           _ptr(self._f(rotations, (P, 4)) if not use_cov else None),
+           _ptr(self._f(viewmatrix, (16,))), _ptr(self._f(projmatrix, (16,))),
+           _ptr(self._f(campos, (3,))), _ptr(sh_arr),
+           _ptr(self._f(cov3d_precomp, (P, 6)) if use_cov else None), _ptr(self._f(cov3d_fwd)),
+           _ptr(d(m_cov3d, (P, 6)) if m_cov3d is not None else None), _ptr(d(m_rgb, (P, 3))),
+           _ptr(d(m_xys, (P, 2))), _ptr(d(m_conic_opacity, (P, 4))), _ptr(d(m_vsp, (P, 4))),
+           _ptr(np.ascontiguousarray(radii, np.int32)),
+           _ptr(np.ascontiguousarray(clamped, np.uint8)),
+           *[_ptr(out[k]) for k in ("means3d", "dc", "sh", "colors_precomp", "opacities",
+                                    "scales", "rotations", "viewspace_points")])
+        return out
 
     # -- full pipeline (binding.cpp:33-282) ------------------------------
     def render(self, inputs: dict, image_width: int, image_height: int, tan_fovx=1.0,
@@ -394,10 +450,18 @@ class Oracle:
 
     def render_backward(self, inputs: dict, fwd: dict, dL_dout_color, image_width, image_height,
                         tan_fovx=1.0, tan_fovy=1.0, degree=0, scale_modifier=1.0,
-                        dL_dvsp_out=None, dL_dxys_extra=None):
+                        dL_dvsp_out=None, dL_dxys_extra=None, magnitude=False):
         """Gradients of sum(dL_dout_color * out_color) (+ optional direct cotangents of the
         preprocess outputs) w.r.t. the differentiable inputs, chained exactly as
-        FastGSRasterize::vjp -> FastGSPreprocess::vjp."""
+        FastGSRasterize::vjp -> FastGSPreprocess::vjp.
+
+        ``magnitude``: also ``g["mag_terms"]`` and ``g["mag"]`` (float64, the
+        gradients' keys and shapes): for every gradient entry the sum of the
+        magnitudes of the terms it is made of.  The blend's per-(pixel, splat)
+        terms come from rasterize_bwd; orc_preprocess_bwd_mag carries them
+        through the preprocess backward's own sums and products (each sum
+        taken over magnitudes), so an entry's value is the sum of |term| over
+        the fully expanded chain rule."""
         pre = fwd["pre"]
         P = pre["xys"].shape[0]
         dt = self.dt
@@ -406,10 +470,13 @@ class Oracle:
             g2 = self.rasterize_bwd(fwd["ranges"], fwd["point_list"], pre["xys"], pre["rgb"],
                                     pre["conic_opacity"], inputs["background"], r["final_t"],
                                     r["n_contrib"], np.asarray(dL_dout_color, dt).reshape(3, -1),
-                                    image_width, image_height, 3, fwd["num_tiles"])
+                                    image_width, image_height, 3, fwd["num_tiles"],
+                                    magnitude=magnitude)
         else:
             g2 = {"means2d": np.zeros((P, 2), dt), "colors": np.zeros((P, 3), dt),
                   "conic_opacity": np.zeros((P, 4), dt), "viewspace_points": np.zeros((P, 4), dt)}
+            if magnitude:
+                g2["mag"] = {k: np.zeros(v.shape, np.float64) for k, v in g2.items()}
         dvsp = g2["viewspace_points"].copy()
         if dL_dvsp_out is not None:
             dvsp += np.asarray(dL_dvsp_out, dt)
@@ -429,4 +496,24 @@ class Oracle:
             rotations=inputs.get("rotations") if not has_cov else None,
             cov3d_precomp=cov if has_cov else None, use_colors_precomp=has_col)
         g["raster"] = g2
+        if magnitude:
+            if "mag_terms" not in g2:
+                g2["mag_terms"] = g2["mag"]
+            for key in ("mag", "mag_terms"):
+                m2 = g2[key]
+                m_xys = m2["means2d"].copy()
+                if dL_dxys_extra is not None:
+                    m_xys += np.abs(np.asarray(dL_dxys_extra, np.float64))
+                m_vsp = m2["viewspace_points"].copy()
+                if dL_dvsp_out is not None:
+                    m_vsp += np.abs(np.asarray(dL_dvsp_out, np.float64))
+                g[key] = self.preprocess_bwd_mag(
+                    inputs["means3d"], inputs["viewmatrix"], inputs["projmatrix"],
+                    inputs["campos"], pre["radii"], pre["cov3d"], pre["clamped"], m_xys,
+                    m2["colors"], m2["conic_opacity"], m_vsp, image_width, image_height,
+                    tan_fovx, tan_fovy, degree, scale_modifier,
+                    sh=inputs.get("sh") if not has_col else None,
+                    scales=inputs.get("scales") if not has_cov else None,
+                    rotations=inputs.get("rotations") if not has_cov else None,
+                    cov3d_precomp=cov if has_cov else None, use_colors_precomp=has_col)
         return g

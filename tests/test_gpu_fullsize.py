@@ -3,43 +3,25 @@
 
 The oracle finishes this frame in a few seconds on the host, so the forward
 is checked against it exactly as the small cases are (integer outputs and
-the tile lists bit-exact, the image within 1e-4), and the backward against
-its double-summed gradients.  At this size a few gradient entries cancel to
-far below their terms (the GPU sums them with float atomics in no fixed
-order, and recovers T by division), so the gradient gate is split: all but
-1e-4 of the entries within the small cases' tolerance, and every entry
-within 1e-2 relative plus 3e-4 of the array's largest magnitude.  Size-free
-properties are checked as well: K is the sum of the tile counts, each tile's
-keys are sorted by depth, and the viewspace gradient's absolute-value terms
-bound its signed terms.
+the tile lists bit-exact, the image within 1e-4), and the gradients through
+the three gates of tests.helpers.check_backward_stages (the rasterize
+backward's outputs, the preprocess backward on identical inputs, and end to
+end, each against the sum of its terms' magnitudes).  Size-free properties are
+checked as well: K is the sum of the tile counts, each tile's keys are sorted
+by depth, and the viewspace gradient's absolute-value terms bound its signed
+terms.
 """
 import numpy as np
 import pytest
 
 from fastgs_core_amd import synthetic as syn
 
-from tests.helpers import GRAD_AFLOOR, GRAD_RTOL, IMAGE_ATOL, to_np, to_torch
+from tests.helpers import (IMAGE_ATOL, capture_2d_gradients, check_backward_stages, to_np,
+                           to_torch)
 
 
 def _say(*a):
     print("[gpu-test]", *a, flush=True)
-
-
-def _grad_gate(name, got, ref):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    assert got.shape == ref.shape, (name, got.shape, ref.shape)
-    scale = float(np.max(np.abs(ref)))
-    err = np.abs(got - ref)
-    tol = GRAD_RTOL * np.abs(ref) + GRAD_AFLOOR * scale
-    frac = float(np.mean(err > tol))
-    i = int(np.argmax(err - (10 * GRAD_RTOL * np.abs(ref) + 3e-4 * scale)))
-    info = (f"{name}: {frac:.2e} of {ref.size} entries outside tolerance; worst flat index {i}: "
-            f"got {got.flat[i]!r} ref {ref.flat[i]!r} (scale {scale:.3e}, max abs err "
-            f"{err.max():.3e})")
-    print("[gpu-test]", info, flush=True)
-    assert frac <= 1e-4, info
-    assert np.all(err <= 10 * GRAD_RTOL * np.abs(ref) + 3e-4 * scale), info
 
 
 @pytest.mark.gpu
@@ -77,16 +59,12 @@ def test_cfg3_full_size_forward_and_backward(oracle):
     rng = np.random.default_rng(11)
     dL = rng.standard_normal((3, W * H)).astype(np.float32)
     _say("cfg3 full size backward")
-    rg = oracle.render_backward(inp, ref, dL, W, H, cam.tan_fovx, cam.tan_fovy, 3)
+    rg = oracle.render_backward(inp, ref, dL, W, H, cam.tan_fovx, cam.tan_fovy, 3,
+                                magnitude=True)
+    seen = capture_2d_gradients(out)
     loss = (out["out_color"] * torch.from_numpy(dL).cuda()).sum()
     loss.backward()
-    failures = []
-    for k in req:
-        try:
-            _grad_gate(k, to_np(tin[k].grad), rg[k])
-        except AssertionError as e:
-            failures.append(str(e))
-    assert not failures, failures
+    check_backward_stages(oracle, inp, ref, rg, tin, seen, W, H, cam, 3)
     vg = to_np(tin["viewspace_points"].grad).astype(np.float64)
     slack = 1e-5 * np.abs(vg).max()
     assert np.all(vg[:, 2] >= np.abs(vg[:, 0]) - slack)

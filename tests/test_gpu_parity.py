@@ -3,7 +3,7 @@ the reference Metal kernels), through the fastgs_core API and C ABI.
 
 Gates: radii / tiles_touched / sorted keys+values / ranges / bucket arrays /
 n_contrib / max_contrib bit-exact; image within 1e-4 absolute; gradients
-within 1e-3 relative (helpers.assert_grad_close).
+within 1e-3 of the sum of their terms' magnitudes (helpers.assert_grad_gate).
 """
 import sys
 
@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 
 from fastgs_core_amd import synthetic as syn
-from tests.helpers import IMAGE_ATOL, assert_grad_close, scene_small, to_np, to_torch
+from tests.helpers import (IMAGE_ATOL, assert_grad_gate, capture_2d_gradients,
+                           check_backward_stages, scene_small, to_np, to_torch)
 
 pytestmark = pytest.mark.gpu
 
@@ -152,29 +153,27 @@ def test_backward_parity(oracle, case):
     rng = np.random.default_rng(11)
     dL = rng.standard_normal((3, cam.width * cam.height)).astype(np.float32)
     rg = oracle.render_backward(inp, ref, dL, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy,
-                                degree)
+                                degree, magnitude=True)
     req = ("means3d", "scales", "rotations", "opacities", "dc", "sh", "viewspace_points")
     tin = to_torch(inp, requires_grad=req)
     out = fastgs_core.rasterize_gaussians(tin, cam.width, cam.height, 16, 16, cam.tan_fovx,
                                           cam.tan_fovy, degree)
+    seen = capture_2d_gradients(out)
     loss = (out["out_color"] * torch.from_numpy(dL).cuda()).sum()
     loss.backward()
-    for k, rk in (("means3d", "means3d"), ("scales", "scales"), ("rotations", "rotations"),
-                  ("opacities", "opacities"), ("dc", "dc"), ("sh", "sh"),
-                  ("viewspace_points", "viewspace_points")):
-        assert_grad_close(k, to_np(tin[k].grad), rg[rk])
+    check_backward_stages(oracle, inp, ref, rg, tin, seen, cam.width, cam.height, cam, degree)
     # the viewspace dummy carries (x, y) = dL/dmeans2d exactly
-    np.testing.assert_allclose(to_np(tin["viewspace_points"].grad)[:, :2],
-                               rg["raster"]["means2d"], rtol=1e-3,
-                               atol=1e-5 * np.abs(rg["raster"]["means2d"]).max())
+    assert_grad_gate("viewspace (x, y) vs dL/dmeans2d", to_np(tin["viewspace_points"].grad)[:, :2],
+                     rg["raster"]["means2d"], rg["raster"]["mag_terms"]["means2d"])
 
 
-def _assert_nonfinite_pattern_and_close(name, got, ref):
+def _assert_nonfinite_pattern_and_close(name, got, ref, mag):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     fin = np.isfinite(ref)
     np.testing.assert_array_equal(np.isfinite(got), fin, err_msg=f"{name}: non-finite pattern")
-    assert_grad_close(name, np.where(fin, got, 0.0), np.where(fin, ref, 0.0))
+    assert_grad_gate(name, np.where(fin, got, 0.0), np.where(fin, ref, 0.0),
+                     np.where(fin, mag, 0.0))
 
 
 def test_rasterize_backward_nonfinite_inputs(oracle):
@@ -200,7 +199,7 @@ def test_rasterize_backward_nonfinite_inputs(oracle):
     _say("rasterize backward non-finite inputs, inf colour on", hot)
     g = oracle.rasterize_bwd(ref["ranges"], ref["point_list"], pre["xys"], colors,
                              pre["conic_opacity"], inp["background"], r["final_t"], r["n_contrib"],
-                             dL, W, H)
+                             dL, W, H, magnitude=True)
     assert np.isnan(g["means2d"]).any() and np.isfinite(g["means2d"]).any()
     dev = torch.device("cuda")
     P = pre["xys"].shape[0]
@@ -217,7 +216,7 @@ def test_rasterize_backward_nonfinite_inputs(oracle):
     for name, t, rk in (("means2d", m2, "means2d"), ("colors", col, "colors"),
                         ("conic_opacity", co, "conic_opacity"),
                         ("viewspace", vsp, "viewspace_points")):
-        _assert_nonfinite_pattern_and_close(name, to_np(t.grad), g[rk])
+        _assert_nonfinite_pattern_and_close(name, to_np(t.grad), g[rk], g["mag_terms"][rk])
 
 
 def test_rasterize_forward_standalone_closed_form():
@@ -410,13 +409,14 @@ def test_cov3d_precomp_colors_path_backward(oracle):
     inp["colors_precomp"] = rng.uniform(0, 1, (P, 3)).astype(np.float32)
     ref = oracle.render(inp, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, 0)
     dL = rng.standard_normal((3, cam.width * cam.height)).astype(np.float32)
-    rg = oracle.render_backward(inp, ref, dL, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, 0)
+    rg = oracle.render_backward(inp, ref, dL, cam.width, cam.height, cam.tan_fovx, cam.tan_fovy, 0,
+                                magnitude=True)
     tin = to_torch(inp, requires_grad=("means3d", "colors_precomp", "opacities", "cov3d_precomp"))
     out = fastgs_core.rasterize_gaussians(tin, cam.width, cam.height, 16, 16, cam.tan_fovx,
                                           cam.tan_fovy, 0)
     np.testing.assert_allclose(to_np(out["out_color"]), ref["out_color"], atol=IMAGE_ATOL)
     (out["out_color"] * torch.from_numpy(dL).cuda()).sum().backward()
-    assert_grad_close("means3d", to_np(tin["means3d"].grad), rg["means3d"])
-    assert_grad_close("colors_precomp", to_np(tin["colors_precomp"].grad), rg["colors_precomp"])
-    assert_grad_close("opacities", to_np(tin["opacities"].grad), rg["opacities"])
+    assert_grad_gate("means3d", to_np(tin["means3d"].grad), rg["means3d"], rg["mag_terms"]["means3d"])
+    assert_grad_gate("colors_precomp", to_np(tin["colors_precomp"].grad), rg["colors_precomp"], rg["mag_terms"]["colors_precomp"])
+    assert_grad_gate("opacities", to_np(tin["opacities"].grad), rg["opacities"], rg["mag_terms"]["opacities"])
     assert float(tin["cov3d_precomp"].grad.abs().sum()) == 0.0
