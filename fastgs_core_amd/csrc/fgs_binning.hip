@@ -19,6 +19,10 @@
 // order in LDS and writes each digit run contiguously to HBM.
 #include "fgs_common.hpp"
 
+#include <atomic>
+#include <cstdio>
+#include <mutex>
+
 namespace fgs {
 
 constexpr int kThreads = 256;
@@ -207,9 +211,10 @@ chained_scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict_
 }
 
 // Zero-initialised state of one chained scan: status words, ticket, error.
-static size_t scan_state_bytes(int64_t n) {
-  const int64_t nc = (n + kChunk - 1) / kChunk;
-  return (size_t)(((nc < 1 ? 1 : nc) * 8 + 16 + 255) & ~(int64_t)255);
+static constexpr size_t scan_state_bytes(int64_t n) {
+  return (size_t)(((((n + kChunk - 1) / kChunk) < 1 ? 1 : ((n + kChunk - 1) / kChunk)) * 8 + 16 +
+                   255) &
+                  ~(int64_t)255);
 }
 static size_t scan_ws_bytes(int64_t n) { return scan_state_bytes(n); }
 
@@ -1482,6 +1487,70 @@ extern "C" int32_t fgs_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int
   if (!in || !out || !workspace)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_inclusive_scan_u32: null pointer");
   return launch_scan(in, out, n, workspace, true, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free inclusive scan: the scan's state (one status word per
+// 4096-element chunk, the chunk ticket, the wait-error word) lives in a
+// file-scope device array instead of a caller workspace.  Each device holds its
+// own copy; its address is looked up once per device with that device current
+// and cached.  The state is cleared by the scan's fill kernel on every call
+// (graph-safe), so a call needs no initial contents; calls that overlap on one
+// device share the array and race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocMaxN = (int64_t)1 << 28;
+constexpr int64_t kNoAllocChunks = kNoAllocMaxN / kChunk;  // 65536
+constexpr size_t kNoAllocScratchBytes = scan_state_bytes(kNoAllocMaxN);  // 512.25 KiB
+static_assert(kNoAllocScratchBytes == (size_t)kNoAllocChunks * 8 + 256, "scan state size");
+static __device__ __align__(256) uint64_t scratch[kNoAllocScratchBytes / 8];
+
+constexpr int kNoAllocMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kNoAllocMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (host code never uses the array's
+// name as an address: it is a host-side stand-in).
+static int32_t noalloc_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices)
+    return set_error(FGS_ERR_LAUNCH, "fgs_inclusive_scan_u32_noalloc: no current HIP device");
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        char msg[256];
+        std::snprintf(msg, sizeof(msg),
+                      "fgs_inclusive_scan_u32_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                      dev, hipGetErrorString(e));
+        return set_error(FGS_ERR_LAUNCH, msg);
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FGS_OK;
+}
+
+extern "C" int32_t fgs_inclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n,
+                                                  void* stream) {
+  if (n < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_inclusive_scan_u32_noalloc: n < 0");
+  if (n > kNoAllocMaxN) {
+    char msg[160];
+    std::snprintf(msg, sizeof(msg),
+                  "fgs_inclusive_scan_u32_noalloc: n = %lld exceeds the maximum of %lld elements",
+                  (long long)n, (long long)kNoAllocMaxN);
+    return set_error(FGS_ERR_INVALID_ARGUMENT, msg);
+  }
+  if (n == 0) return FGS_OK;
+  if (!in || !out)
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_inclusive_scan_u32_noalloc: null pointer");
+  void* state = nullptr;
+  const int32_t e = noalloc_scratch(&state);
+  if (e != FGS_OK) return e;
+  return launch_scan(in, out, n, state, true, (hipStream_t)stream);
 }
 
 extern "C" int32_t fgs_fill_u32(uint32_t* dst, uint32_t value, int64_t n, void* stream) {

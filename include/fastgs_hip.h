@@ -5,7 +5,9 @@
  *
  * Ownership: the caller allocates every output and workspace buffer (sizes
  * from the *_workspace_bytes queries); the library never allocates, frees or
- * retains device memory and never synchronises the stream.  Every output
+ * retains device memory and never synchronises the stream.  The one exception
+ * is fgs_inclusive_scan_u32_noalloc, whose state is a static device array of
+ * the library (512.25 KiB per device).  Every output
  * element the reference zero-fills is written by the library on the stream
  * (kernels, never host memsets and never hipMemsetAsync).
  *
@@ -37,7 +39,8 @@ extern "C" {
 /* Thread-local message of the last error ("" if none). */
 const char* fgs_last_error(void);
 
-/* ABI version of this header (bumped on any struct/signature change). */
+/* ABI version of this header (bumped on any struct/signature change or
+ * addition). */
 int32_t fgs_abi_version(void);
 
 /* ------------------------------------------------------------------------ */
@@ -155,6 +158,16 @@ size_t fgs_scan_workspace_bytes(int64_t n);
  * (binding.cpp:153,211).  in and out may alias. */
 int32_t fgs_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
                                void* stream);
+
+/* fgs_inclusive_scan_u32 without a workspace: the scan's state lives in a
+ * device array of the library (512.25 KiB per device, held until the process
+ * ends), so the call allocates nothing and takes no workspace.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  n <= 2^28 (FGS_ERR_INVALID_ARGUMENT above).  Every call on a
+ * device shares that device's array: calls that overlap on one device (other
+ * streams, other threads) race and must be ordered by the caller. */
+int32_t fgs_inclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n, void* stream);
 
 /* Gaussian-order duplication: for each Gaussian with tiles_touched > 0, the
  * keys (tile_id << 32 | float_bits(depth)) and values (index) of its touched
