@@ -20,6 +20,7 @@ from .train import (  # noqa: F401
     expon_lr_func,
 )
 from .rasterizer import (  # noqa: F401
+    WaitError,
     binning_forward,
     dummy_add,
     dummy_array_size,

@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class PreprocessParams(Structure):
@@ -55,7 +55,7 @@ class BinningIO(Structure):
     ] + [(n, c_void_p) for n in (
         "xys", "depths", "conic_opacity", "tiles_touched", "point_list_keys", "point_list",
         "ranges", "bucket_count", "bucket_offsets", "workspace", "depth_order", "st_base",
-        "st_masks")]
+        "st_masks", "wait_status")]
 
 
 class RasterParams(Structure):
@@ -118,14 +118,16 @@ SIGNATURES = {
     "fgs_preprocess_fwd": (c_int32, [POINTER(PreprocessParams), POINTER(PreprocessFwdIO), c_void_p]),
     "fgs_preprocess_bwd": (c_int32, [POINTER(PreprocessParams), POINTER(PreprocessBwdIO), c_void_p]),
     "fgs_scan_workspace_bytes": (c_size_t, [c_int64]),
-    "fgs_inclusive_scan_u32": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
-    "fgs_inclusive_scan_u32_noalloc": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "fgs_set_wait_spin_limit": (c_uint32, [c_uint32]),
+    "fgs_inclusive_scan_u32": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
+                                         c_void_p]),
+    "fgs_inclusive_scan_u32_noalloc": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "fgs_duplicate_with_keys": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
                                           c_void_p, c_float, c_int32, c_int32, c_int64, c_void_p,
                                           c_void_p, c_void_p]),
     "fgs_sort_workspace_bytes": (c_size_t, [c_int64]),
     "fgs_sort_pairs_u64": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
-                                     c_int32, c_void_p, c_void_p]),
+                                     c_int32, c_void_p, c_void_p, c_void_p]),
     "fgs_tile_ranges": (c_int32, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p]),
     "fgs_binning_workspace_bytes": (c_size_t, [c_int32, c_int64, c_int32]),
     "fgs_binning_sorted": (c_int32, [POINTER(BinningIO), c_void_p]),

@@ -50,7 +50,14 @@ __device__ __forceinline__ int pad_idx(int i) { return i + (i >> 4); }
 
 constexpr uint32_t kFlagAggregate = 1u;
 constexpr uint32_t kFlagPrefix = 2u;
-constexpr uint32_t kSpinLimit = 1u << 24;
+constexpr uint32_t kSpinLimit = 1u << 24;  // default polls of one bounded wait
+// Bits of a wait-status word: which kind of bounded wait gave up.
+constexpr uint32_t kWaitScan = 1u;      // a scan chunk summing its predecessors
+constexpr uint32_t kWaitLookBack = 2u;  // a radix-pass chunk looking back
+
+__device__ __forceinline__ void wait_gave_up(uint32_t* err, uint32_t bit) {
+  __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ void status_store(uint64_t* p, uint32_t flag, uint32_t value) {
   __hip_atomic_store(p, ((uint64_t)flag << 32) | (uint64_t)value, __ATOMIC_RELAXED,
@@ -62,20 +69,28 @@ __device__ __forceinline__ void status_store(uint64_t* p, uint32_t flag, uint32_
 // predecessor is polled alone (with a short sleep) until it has published;
 // the 16 predecessors below it are then read at once (independent loads in
 // flight) and walked from the nearest, adding aggregates until an inclusive
-// prefix is met or an unpublished one is reached.
+// prefix is met or an unpublished one is reached.  After spin_limit polls of
+// one predecessor the wait gives up: kWaitLookBack is set in *err and the
+// partial prefix (never above the true one, so every position stays in
+// bounds) is used.  spin_limit == 0 gives up at once without polling.
 __device__ __forceinline__ uint32_t look_back(const uint64_t* status, int64_t chunk,
-                                              int64_t stride, uint32_t* err) {
+                                              int64_t stride, uint32_t* err,
+                                              uint32_t spin_limit) {
   constexpr int kWin = 16;
   uint32_t excl = 0;
   uint32_t spins = 0;
   int64_t c = chunk - 1;
+  if (spin_limit == 0u) {
+    if (c >= 0) wait_gave_up(err, kWaitLookBack);
+    return 0u;
+  }
   while (c >= 0) {
     const uint64_t w0 = __hip_atomic_load(status + c * stride, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t f0 = (uint32_t)(w0 >> 32);
     if (f0 == 0u) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (++spins > spin_limit) {
+        wait_gave_up(err, kWaitLookBack);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -117,16 +132,23 @@ __device__ __forceinline__ uint32_t look_back(const uint64_t* status, int64_t ch
 // its predecessors publish (status[c], flag kFlagAggregate): the threads of
 // the workgroup take predecessors t, t + blockDim, ... (polling each until
 // published), then one block reduction.  All loads are in flight at once, so
-// there is no chain of waits.  Called by every thread of the workgroup.
+// there is no chain of waits.  Called by every thread of the workgroup.  A
+// predecessor still unpublished after spin_limit polls counts as 0 and sets
+// kWaitScan in *err; spin_limit == 0 gives up at once without polling.
 __device__ __forceinline__ uint32_t block_sum_predecessors(const uint64_t* status, int64_t chunk,
-                                                           uint32_t* err, uint32_t* s_tmp) {
+                                                           uint32_t* err, uint32_t* s_tmp,
+                                                           uint32_t spin_limit) {
+  if (spin_limit == 0u) {  // uniform
+    if (chunk > 0 && threadIdx.x == 0) wait_gave_up(err, kWaitScan);
+    return 0u;
+  }
   uint32_t acc = 0;
   for (int64_t c = threadIdx.x; c < chunk; c += blockDim.x) {
     uint64_t w = __hip_atomic_load(status + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t spins = 0;
     while ((uint32_t)(w >> 32) == 0u) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (++spins > spin_limit) {
+        wait_gave_up(err, kWaitScan);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -154,7 +176,7 @@ template <bool kGather>
 __global__ void __launch_bounds__(kThreads)
 chained_scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict__ order,
                     int64_t n_in, uint32_t* __restrict__ out, int64_t n, int inclusive,
-                    uint64_t* status, uint32_t* ticket, uint32_t* err) {
+                    uint64_t* status, uint32_t* ticket, uint32_t* err, uint32_t spin_limit) {
   __shared__ uint32_t s_data[kChunk + kChunk / 16];
   __shared__ uint32_t s_tmp[kWavesPerBlock + 1];
   __shared__ uint32_t s_slot;
@@ -186,7 +208,7 @@ chained_scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict_
   uint32_t total;
   const uint32_t texcl = block_excl_scan(tsum, s_tmp, &total);
   if (threadIdx.x == 0) status_store(status + chunk, kFlagAggregate, total);
-  const uint32_t excl = block_sum_predecessors(status, chunk, err, s_tmp);
+  const uint32_t excl = block_sum_predecessors(status, chunk, err, s_tmp, spin_limit);
   uint32_t run = texcl + excl;
 #pragma unroll
   for (int k = 0; k < kItems; ++k) {
@@ -249,25 +271,47 @@ static void launch_fill(uint32_t* dst, uint32_t v, int64_t n, hipStream_t st) {
   launch_fill_spans(f, st);
 }
 
+// Polls of one bounded wait before it gives up (fgs_set_wait_spin_limit).
+static std::atomic<uint32_t> g_spin_limit{kSpinLimit};
+
 // Scan with its state at `state` (scan_state_bytes(n), zeroed here unless
-// the caller has zeroed it already).
+// the caller has zeroed it already).  A wait that gives up sets kWaitScan in
+// *werr when werr is given (cleared here first, by the same fill), else in the
+// state's own error word.
 template <bool kGather>
 static int32_t launch_chained_scan(const uint32_t* in, const uint32_t* order, int64_t n_in,
                                    uint32_t* out, int64_t n, void* state, bool inclusive,
-                                   bool zeroed, hipStream_t st) {
-  if (n <= 0) return FGS_OK;
+                                   bool zeroed, hipStream_t st, uint32_t* werr = nullptr) {
+  if (n <= 0) {
+    if (werr) launch_fill(werr, 0u, 1, st);
+    return FGS_OK;
+  }
   const int64_t nc = (n + kChunk - 1) / kChunk;
   uint64_t* status = (uint64_t*)state;
   uint32_t* ticket = (uint32_t*)(status + nc);
-  if (!zeroed) launch_fill((uint32_t*)state, 0u, (int64_t)(scan_state_bytes(n) / 4), st);
+  uint32_t* err = werr ? werr : ticket + 1;
+  if (!zeroed || werr) {
+    FillSpans f{};
+    f.value = 0u;
+    if (!zeroed) {
+      f.p[f.count] = (uint32_t*)state;
+      f.n[f.count++] = (int64_t)(scan_state_bytes(n) / 4);
+    }
+    if (werr) {
+      f.p[f.count] = werr;
+      f.n[f.count++] = 1;
+    }
+    launch_fill_spans(f, st);
+  }
   hipLaunchKernelGGL(chained_scan_kernel<kGather>, dim3((unsigned)nc), dim3(kThreads), 0, st, in,
-                     order, n_in, out, n, inclusive ? 1 : 0, status, ticket, ticket + 1);
+                     order, n_in, out, n, inclusive ? 1 : 0, status, ticket, err,
+                     g_spin_limit.load(std::memory_order_relaxed));
   return check_launch("chained_scan");
 }
 
 static int32_t launch_scan(const uint32_t* in, uint32_t* out, int64_t n, void* ws, bool inclusive,
-                           hipStream_t st) {
-  return launch_chained_scan<false>(in, nullptr, n, out, n, ws, inclusive, false, st);
+                           hipStream_t st, uint32_t* werr = nullptr) {
+  return launch_chained_scan<false>(in, nullptr, n, out, n, ws, inclusive, false, st, werr);
 }
 
 template <typename K>
@@ -360,7 +404,7 @@ __global__ void __launch_bounds__(kT)
 radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                   K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift,
                   int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
-                  int64_t nchunks, uint32_t* ticket, uint32_t* err) {
+                  int64_t nchunks, uint32_t* ticket, uint32_t* err, uint32_t spin_limit) {
   constexpr int kW = kT / kWave;
   constexpr int kC = kT * kIt;
   __shared__ uint32_t s_wh[kW][256];
@@ -448,7 +492,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
         status_store(st, kFlagPrefix, tot);
       } else {
         status_store(st + chunk * 256, kFlagAggregate, tot);
-        excl = look_back(st, chunk, 256, err);
+        excl = look_back(st, chunk, 256, err, spin_limit);
         status_store(st + chunk * 256, kFlagPrefix, excl + tot);
       }
       s_goff[t] = gbase + excl;
@@ -472,8 +516,12 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     const K k = s_keys[j];
     const uint32_t d = (uint32_t)(k >> shift) & mask;
     const uint32_t g = s_goff[d] + ((uint32_t)j - s_dstart[d]);
-    keys_out[g] = k;
-    vals_out[g] = s_vals[j];
+    // always below n unless an earlier wait gave up and left this pass keys
+    // the digit histogram did not count
+    if ((int64_t)g < n) {
+      keys_out[g] = k;
+      vals_out[g] = s_vals[j];
+    }
   }
 }
 
@@ -499,6 +547,16 @@ static size_t sort_state_bytes(int64_t n, int passes) {
                   ~(int64_t)255);
 }
 
+// The error word inside a sort workspace (tmp keys, tmp values, then the state:
+// histograms, tickets, error word).
+template <typename K>
+static uint32_t* sort_err_word(void* ws, int64_t n) {
+  char* p = (char*)ws;
+  p += ((size_t)n * sizeof(K) + 255) & ~(size_t)255;
+  p += ((size_t)n * 4 + 255) & ~(size_t)255;
+  return (uint32_t*)(p + 8 * 256 * 4) + 8;
+}
+
 template <typename K>
 static size_t sort_ws_bytes(int64_t n, int passes = (int)sizeof(K)) {
   size_t b = 0;
@@ -516,14 +574,18 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
                                 uint32_t* vals_out, int64_t n, int begin, int end, void* ws,
                                 hipStream_t st, const float* depths = nullptr,
                                 const uint32_t* tiles_touched = nullptr,
-                                uint32_t* dkeys_out = nullptr) {
-  if (n <= 0) return FGS_OK;
+                                uint32_t* dkeys_out = nullptr, uint32_t* werr = nullptr) {
+  if (n <= 0) {
+    if (werr) launch_fill(werr, 0u, 1, st);
+    return FGS_OK;
+  }
   const SortPlan pl = sort_plan(begin, end);
   if (pl.passes == 0) {
     int64_t blocks = (n + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(copy_pairs_kernel<K>, dim3((unsigned)blocks), dim3(256), 0, st, keys_in,
                        vals_in, keys_out, vals_out, n);
+    if (werr) launch_fill(werr, 0u, 1, st);
     return check_launch("copy_pairs");
   }
   const int64_t nc = sort_chunks(n);
@@ -535,9 +597,22 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   p += ((size_t)n * 4 + 255) & ~(size_t)255;
   uint32_t* hist = (uint32_t*)p;
   uint32_t* tickets = hist + 8 * 256;
-  uint32_t* err = tickets + 8;
+  uint32_t* err = werr ? werr : tickets + 8;
   uint64_t* status = (uint64_t*)(p + 8 * 256 * 4 + 64);
-  launch_fill(hist, 0u, (int64_t)(sort_state_bytes(n, pl.passes) / 4), st);
+  {
+    FillSpans f{};
+    f.value = 0u;
+    f.p[0] = hist;
+    f.n[0] = (int64_t)(sort_state_bytes(n, pl.passes) / 4);
+    f.count = 1;
+    if (werr) {
+      f.p[1] = werr;
+      f.n[1] = 1;
+      f.count = 2;
+    }
+    launch_fill_spans(f, st);
+  }
+  const uint32_t spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   const int64_t hn = (n + kChunk - 1) / kChunk;  // histogram workgroups: 4096 keys each
   const int64_t hb = hn < 1024 ? hn : 1024;
   hipLaunchKernelGGL((radix_hist_kernel<K, kDepthKeys>), dim3((unsigned)hb), dim3(kThreads), 0, st,
@@ -552,11 +627,11 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
     if (items == 8)
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, nc, tickets + pass, err);
+                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit);
     else
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 4>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, nc, tickets + pass, err);
+                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit);
     const int32_t e2 = check_launch("radix_pass");
     if (e2 != FGS_OK) return e2;
     shift += pl.bits[pass];
@@ -708,12 +783,31 @@ __global__ void bucket_count_kernel(int32_t T, const uint32_t* __restrict__ rang
   bucket_count[t] = (uint32_t)((n + 31) / 32);
 }
 
+// The wait status of a binning call: the OR of the error words of the waits it
+// (and the depth order it consumes) ran, written by the call's last kernel
+// (one workgroup, after every wait in stream order).  Unused words are NULL.
+struct WaitWords {
+  const uint32_t* w[3];
+  uint32_t* out;
+};
+__device__ __forceinline__ void report_waits(const WaitWords& ww) {
+  if (threadIdx.x == 0 && ww.out) {
+    uint32_t v = 0u;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      if (ww.w[k]) v |= __hip_atomic_load(ww.w[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *ww.out = v;
+  }
+}
+
 // Bucket counts (ceil(n / 32) per tile) and their inclusive scan, by one
 // 1024-thread workgroup walking the tiles in chunks of 1024.
 __global__ void __launch_bounds__(1024)
 bucket_scan_kernel(int32_t T, const uint32_t* __restrict__ ranges,
-                   uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets) {
+                   uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets,
+                   WaitWords ww) {
   __shared__ uint32_t s_tmp[1024 / kWave + 1];
+  report_waits(ww);
   uint32_t carry = 0;
   for (int base = 0; base < T; base += 1024) {
     const int t = base + (int)threadIdx.x;
@@ -1213,8 +1307,10 @@ __device__ __forceinline__ int tpad(int i) { return i + (i >> 5); }
 __global__ void __launch_bounds__(1024)
 l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
                     uint32_t* __restrict__ tile_start, uint32_t* __restrict__ ranges,
-                    uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets) {
+                    uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets,
+                    WaitWords ww) {
   __shared__ uint32_t s_tmp[1024 / kWave + 1];
+  report_waits(ww);
   __shared__ uint32_t s_v[kTileLds];
   const int t = (int)threadIdx.x;
   const int t0 = t * kTilesPer;
@@ -1413,6 +1509,11 @@ static DepthLayout depth_layout(int32_t P) {
   return D;
 }
 
+// The error word of the depth sort in a depth workspace.
+static const uint32_t* depth_err_word(const char* dws, int32_t P) {
+  return sort_err_word<uint32_t>((void*)(dws + depth_layout(P).sort), P);
+}
+
 // The P Gaussians by depth bits, culled ones last (keys made inside the
 // histogram kernel); the order lands at D.order of dws.
 static int32_t run_depth_order(int32_t P, const float* depths, const uint32_t* tiles_touched,
@@ -1480,13 +1581,14 @@ using namespace fgs;
 
 extern "C" size_t fgs_scan_workspace_bytes(int64_t n) { return scan_ws_bytes(n < 1 ? 1 : n); }
 
+extern "C" uint32_t fgs_set_wait_spin_limit(uint32_t limit) { return g_spin_limit.exchange(limit); }
+
 extern "C" int32_t fgs_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n,
-                                          void* workspace, void* stream) {
+                                          void* workspace, uint32_t* wait_status, void* stream) {
   if (n < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_inclusive_scan_u32: n < 0");
-  if (n == 0) return FGS_OK;
-  if (!in || !out || !workspace)
+  if (n > 0 && (!in || !out || !workspace))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_inclusive_scan_u32: null pointer");
-  return launch_scan(in, out, n, workspace, true, (hipStream_t)stream);
+  return launch_scan(in, out, n, workspace, true, (hipStream_t)stream, wait_status);
 }
 
 // ---------------------------------------------------------------------------
@@ -1535,7 +1637,7 @@ static int32_t noalloc_scratch(void** out) {
 }
 
 extern "C" int32_t fgs_inclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n,
-                                                  void* stream) {
+                                                  uint32_t* wait_status, void* stream) {
   if (n < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_inclusive_scan_u32_noalloc: n < 0");
   if (n > kNoAllocMaxN) {
     char msg[160];
@@ -1544,13 +1646,16 @@ extern "C" int32_t fgs_inclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* 
                   (long long)n, (long long)kNoAllocMaxN);
     return set_error(FGS_ERR_INVALID_ARGUMENT, msg);
   }
-  if (n == 0) return FGS_OK;
+  if (n == 0) {
+    if (wait_status) launch_fill(wait_status, 0u, 1, (hipStream_t)stream);
+    return wait_status ? check_launch("fgs_inclusive_scan_u32_noalloc") : FGS_OK;
+  }
   if (!in || !out)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_inclusive_scan_u32_noalloc: null pointer");
   void* state = nullptr;
   const int32_t e = noalloc_scratch(&state);
   if (e != FGS_OK) return e;
-  return launch_scan(in, out, n, state, true, (hipStream_t)stream);
+  return launch_scan(in, out, n, state, true, (hipStream_t)stream, wait_status);
 }
 
 extern "C" int32_t fgs_fill_u32(uint32_t* dst, uint32_t value, int64_t n, void* stream) {
@@ -1587,16 +1692,20 @@ extern "C" size_t fgs_sort_workspace_bytes(int64_t n) { return sort_ws_bytes<uin
 extern "C" int32_t fgs_sort_pairs_u64(const uint64_t* keys_in, const uint32_t* values_in,
                                       uint64_t* keys_out, uint32_t* values_out, int64_t n,
                                       int32_t begin_bit, int32_t end_bit, void* workspace,
-                                      void* stream) {
+                                      uint32_t* wait_status, void* stream) {
   if (n < 0 || begin_bit < 0 || end_bit > 64 || begin_bit > end_bit)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_sort_pairs_u64: bad arguments");
-  if (n == 0) return FGS_OK;
+  if (n == 0) {
+    if (wait_status) launch_fill(wait_status, 0u, 1, (hipStream_t)stream);
+    return wait_status ? check_launch("fgs_sort_pairs_u64") : FGS_OK;
+  }
   if (n > 0xFFFFFFFFll)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_sort_pairs_u64: n exceeds 2^32-1");
   if (!keys_in || !keys_out || !values_out || !workspace)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_sort_pairs_u64: null pointer");
   return radix_sort_pairs<uint64_t>(keys_in, values_in, keys_out, values_out, n, begin_bit, end_bit,
-                                    workspace, (hipStream_t)stream);
+                                    workspace, (hipStream_t)stream, nullptr, nullptr, nullptr,
+                                    wait_status);
 }
 
 extern "C" int32_t fgs_tile_ranges(const uint64_t* keys, int64_t num_rendered, int32_t num_tiles,
@@ -1658,6 +1767,10 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   const StGrid sg = st_grid(io->grid_x, io->grid_y);
   char* ws = (char*)io->workspace;
+  WaitWords ww{};
+  ww.out = io->wait_status;
+  if (io->depth_order) ww.w[0] = depth_err_word((const char*)io->depth_order, P);
+  else if (K > 0 && P > 0) ww.w[0] = depth_err_word(ws, P);
   // Gaussians by depth bits: from the caller's depth workspace, or sorted here
   // into the front of the binning workspace
   const char* dws = io->depth_order ? (const char*)io->depth_order : ws;
@@ -1705,7 +1818,7 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     hipLaunchKernelGGL(l2_st_scan_kernel, dim3(sg.S), dim3(kWave), 0, st, sg, chunk_first, cnt2,
                        base2, tile_total, L.max_chunks);
     hipLaunchKernelGGL(l2_tile_scan_kernel, dim3(1), dim3(1024), 0, st, T, tile_total, tile_start,
-                       io->ranges, io->bucket_count, io->bucket_offsets);
+                       io->ranges, io->bucket_count, io->bucket_offsets, ww);
     hipLaunchKernelGGL(l2_emit_kernel, dim3(nch), dim3(kL1Group), 0, st, sg, list, st_start,
                        chunk_first, chunk_st, nchunks, masks, cnt2, base2, tile_start, P,
                        io->depths, K, io->point_list_keys, io->point_list);
@@ -1726,6 +1839,7 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     int32_t e = launch_chained_scan<true>(io->tiles_touched, order, P, cnt, P, ws + L.scanP, false, false,
                                   st);
     if (e != FGS_OK) return e;
+    ww.w[1] = (const uint32_t*)((const uint64_t*)(ws + L.scanP) + (P + kChunk - 1) / kChunk) + 1;
     hipLaunchKernelGGL(duplicate_sorted_kernel, dim3(gP), dim3(256), 0, st, P, order, cnt, io->xys,
                        io->conic_opacity, io->tiles_touched, io->mult, io->grid_x, io->grid_y, K,
                        tkeys, tvals);
@@ -1733,12 +1847,15 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     e = radix_sort_pairs<uint32_t>(tkeys, tvals, tkeys_s, io->point_list, K, 0, bits_for(T),
                                    ws + L.sortK, st);
     if (e != FGS_OK) return e;
+    if (bits_for(T) > 0) ww.w[2] = sort_err_word<uint32_t>(ws + L.sortK, K);
     hipLaunchKernelGGL(finalize_keys_ranges_kernel, dim3(ceil_div_u(K, 256)), dim3(256), 0, st, K,
                        T, P, tkeys_s, io->point_list, io->depths, io->point_list_keys,
                        io->ranges);
   }
   if (T > 0)
     hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, st, T, io->ranges,
-                       io->bucket_count, io->bucket_offsets);
+                       io->bucket_count, io->bucket_offsets, ww);
+  else if (io->wait_status)
+    launch_fill(io->wait_status, 0u, 1, st);
   return check_launch("binning_sorted");
 }

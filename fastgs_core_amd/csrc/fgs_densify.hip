@@ -171,7 +171,10 @@ densify_compact_kernel(int32_t P2, const uint32_t* __restrict__ keep,
                        const uint32_t* __restrict__ keep_incl, int32_t* __restrict__ rows) {
   const int r = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (r >= P2 || !keep[r]) return;
-  rows[keep_incl[r] - 1u] = r;
+  // rows holds keep_incl[P2 - 1] entries; a scan whose wait gave up can leave
+  // other prefixes above it, which are dropped
+  const uint32_t at = keep_incl[r] - 1u;
+  if (at < keep_incl[P2 - 1]) rows[at] = r;
 }
 
 // Final rows: row f comes from pre-prune row rows[f] (identity when NULL),

@@ -39,7 +39,7 @@ from typing import Callable, Dict, List, Optional, Sequence
 import torch
 
 from . import _lib
-from .rasterizer import _p, _stream
+from .rasterizer import _p, _stream, check_wait
 from .train import FastGSOptimizerPolicy, expon_lr_func
 
 PARAM_NAMES = ("means3d", "features_dc", "features_rest", "opacity_logits", "log_scales",
@@ -103,7 +103,9 @@ def _u32(n, dev):
 
 
 class _Scanner:
-    """Inclusive u32 scans and last-element reads on one device."""
+    """Inclusive u32 scans and last-element reads on one device.  Each scan's
+    output is the head of an (n + 1)-word buffer whose last word receives the
+    scan's wait status, read back together with the total by ``last``."""
 
     def __init__(self, dev):
         self.dev = dev
@@ -111,17 +113,36 @@ class _Scanner:
 
     def incl(self, flags: torch.Tensor) -> torch.Tensor:
         n = flags.numel()
-        out = torch.empty(n, dtype=torch.int32, device=self.dev)
-        if n:
-            ws = torch.empty(int(self.lib.fgs_scan_workspace_bytes(n)), dtype=torch.uint8,
-                             device=self.dev)
-            _check(self.lib.fgs_inclusive_scan_u32(_p(flags), _p(out), n, _p(ws),
-                                                   _stream(self.dev)))
-        return out
+        buf = torch.empty(n + 1, dtype=torch.int32, device=self.dev)
+        ws = torch.empty(int(self.lib.fgs_scan_workspace_bytes(max(n, 1))), dtype=torch.uint8,
+                         device=self.dev)
+        _check(self.lib.fgs_inclusive_scan_u32(_p(flags), _p(buf[:n]) if n else None, n, _p(ws),
+                                               _p(buf[n:]), _stream(self.dev)))
+        return buf[:n]
 
     @staticmethod
     def last(t: torch.Tensor) -> int:
-        return int(t[-1].item()) & 0xFFFFFFFF if t.numel() else 0
+        """The total (last element) of an ``incl`` result, after checking the
+        scan's wait status stored in the word that follows it."""
+        n = t.numel()
+        pair = torch.as_strided(t, (2,), (1,), t.storage_offset() + n - 1) if n else \
+            torch.as_strided(t, (1,), (1,), t.storage_offset())
+        a = pair.cpu().numpy()
+        check_wait(int(a[-1]) & 0xFFFFFFFF, "densification scan")
+        return int(a[0]) & 0xFFFFFFFF if n else 0
+
+
+def _sort_rows_by_key(lib, keys, P, dev, st):
+    """Rows in ascending order of their 32-bit keys (stable), through
+    fgs_sort_pairs_u64, with its wait status checked."""
+    skeys = torch.empty(P, dtype=torch.int64, device=dev)
+    srows = _u32(P, dev)
+    ws = torch.empty(int(lib.fgs_sort_workspace_bytes(P)), dtype=torch.uint8, device=dev)
+    status = torch.empty(1, dtype=torch.int32, device=dev)
+    _check(lib.fgs_sort_pairs_u64(_p(keys), None, _p(skeys), _p(srows), P, 0, 32, _p(ws),
+                                  _p(status), st))
+    check_wait(int(status.item()) & 0xFFFFFFFF, "densification sort")
+    return srows
 
 
 class GaussianTrainState:
@@ -384,12 +405,7 @@ class GaussianTrainState:
         rows = None
         P_new = P2
         if k > 0:
-            lib_ws = torch.empty(int(lib.fgs_sort_workspace_bytes(P2)), dtype=torch.uint8,
-                                 device=dev)
-            skeys = torch.empty_like(keys)
-            srows = _u32(P2, dev)
-            _check(lib.fgs_sort_pairs_u64(_p(keys), None, _p(skeys), _p(srows), P2, 0, 32,
-                                          _p(lib_ws), st))
+            srows = _sort_rows_by_key(lib, keys, P2, dev, st)
             keep = _u32(P2, dev)
             _check(lib.fgs_densify_select(P2, k, _p(srows), _p(keep), st))
             kincl = sc.incl(keep)
@@ -423,11 +439,7 @@ class GaussianTrainState:
         min_keep = min(max(int(min_gaussians), 0), P)
         keep = _u32(P, dev)
         if P - requested < min_keep:
-            ws = torch.empty(int(lib.fgs_sort_workspace_bytes(P)), dtype=torch.uint8, device=dev)
-            skeys = torch.empty_like(keys)
-            srows = _u32(P, dev)
-            _check(lib.fgs_sort_pairs_u64(_p(keys), None, _p(skeys), _p(srows), P, 0, 32, _p(ws),
-                                          st))
+            srows = _sort_rows_by_key(lib, keys, P, dev, st)
             _check(lib.fgs_densify_keep_first(P, min_keep, _p(srows), _p(keep), st))
         else:
             _check(lib.fgs_invert_flags(P, _p(prune), _p(keep), st))

@@ -325,15 +325,18 @@ class _Rasterize(torch.autograd.Function):
 # stage helpers shared by the public functions
 # ---------------------------------------------------------------------------
 def _inclusive_scan_i32(x: torch.Tensor) -> torch.Tensor:
+    """Inclusive scan of x into the first n words of an (n + 1)-word buffer; the
+    last word receives the scan's wait status, so one copy of the final two
+    words reads the total and the status together."""
     lib = _lib.load()
     n = x.numel()
-    out = torch.empty(n, dtype=torch.int32, device=x.device)
-    if n == 0:
-        return out
-    ws = torch.empty(int(lib.fgs_scan_workspace_bytes(n)), dtype=torch.uint8, device=x.device)
+    buf = torch.empty(n + 1, dtype=torch.int32, device=x.device)
+    ws = torch.empty(int(lib.fgs_scan_workspace_bytes(max(n, 1))), dtype=torch.uint8,
+                     device=x.device)
     with _stage("scan"):
-        _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(out), n, _p(ws), _stream(x.device)))
-    return out
+        _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(buf[:n]) if n else None, n, _p(ws),
+                                              _p(buf[n:]), _stream(x.device)))
+    return buf
 
 
 def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: float,
@@ -346,28 +349,41 @@ def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: f
     T = gx * gy
     keys = torch.empty(K, dtype=torch.int64, device=dev)
     plist = torch.empty(K, dtype=torch.int32, device=dev)
-    tbuf = torch.empty(4 * T, dtype=torch.int32, device=dev)  # ranges, counts, offsets
+    # ranges, counts, offsets, then the wait status next to the last offset (B)
+    tbuf = torch.empty(4 * T + 1, dtype=torch.int32, device=dev)
     ranges = tbuf[: 2 * T].view(T, 2)
     bucket_count = tbuf[2 * T: 3 * T]
-    bucket_offsets = tbuf[3 * T:]
+    bucket_offsets = tbuf[3 * T: 4 * T]
     ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
     io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
                         _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws),
-                        _p(depth_ws), _p(st_base), _p(st_masks))
+                        _p(depth_ws), _p(st_base), _p(st_masks), _p(tbuf[4 * T:]))
     with _stage("binning"):
         _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
-    return keys, plist, ranges, bucket_count, bucket_offsets
+    return keys, plist, ranges, bucket_count, bucket_offsets, tbuf
 
 
-def _last_u32(t: torch.Tensor) -> int:
-    """read_last_u32 (binding.cpp:25-31): one blocking 4-byte read."""
-    if t.numel() == 0:
-        return 0
-    return int(t[-1].item()) & 0xFFFFFFFF
+class WaitError(RuntimeError):
+    """A bounded wait of a scan or sort gave up (see fgs_set_wait_spin_limit);
+    the results of that call are invalid."""
+
+
+def check_wait(status: int, what: str) -> None:
+    if status:
+        kinds = [k for b, k in ((1, "scan"), (2, "radix look-back")) if status & b]
+        raise WaitError(f"{what}: a bounded wait gave up ({', '.join(kinds) or 'unknown'}, "
+                        f"wait status {status:#x}); its outputs are invalid")
+
+
+def _value_and_status(buf: torch.Tensor, i: int):
+    """One blocking read of buf[i] (read_last_u32, binding.cpp:25-31) and of the
+    wait status stored at buf[i + 1]."""
+    a = buf[i:i + 2].cpu().numpy()
+    return int(a[0]) & 0xFFFFFFFF, int(a[1]) & 0xFFFFFFFF
 
 
 class _ReadSlots(threading.local):
-    """Per-thread pinned 4-byte slots and events for the asynchronous reads,
+    """Per-thread pinned 8-byte slots and events for the asynchronous reads,
     reused from call to call (two can be in flight: K and B)."""
 
     def __init__(self):
@@ -377,42 +393,46 @@ class _ReadSlots(threading.local):
 _READ_SLOTS = _ReadSlots()
 
 
-def _last_u32_async(t: torch.Tensor):
-    """read_last_u32 split in two: the 4-byte copy to pinned host memory and an
-    event are queued now, the value is read by _wait_u32. Work queued in
-    between runs on the GPU while the host waits."""
+def _read_async(buf: torch.Tensor, i: int):
+    """read_last_u32 split in two: the copy of buf[i] and the wait status at
+    buf[i + 1] to pinned host memory and an event are queued now, the values
+    are read by _wait_read.  Work queued in between runs on the GPU while the
+    host waits."""
     if _READ_SLOTS.free:
         host, view, ev = _READ_SLOTS.free.pop()
     else:
-        host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        host = torch.empty(2, dtype=torch.int32, pin_memory=True)
         view, ev = host.numpy(), torch.cuda.Event()
-    host.copy_(t[-1:], non_blocking=True)
-    ev.record(torch.cuda.current_stream(t.device))
+    host.copy_(buf[i:i + 2], non_blocking=True)
+    ev.record(torch.cuda.current_stream(buf.device))
     return host, view, ev
 
 
-def _wait_u32(pending) -> int:
+def _wait_read(pending):
     _, view, ev = pending
     ev.synchronize()
-    v = int(view[0]) & 0xFFFFFFFF
+    v, st = int(view[0]) & 0xFFFFFFFF, int(view[1]) & 0xFFFFFFFF
     _READ_SLOTS.free.append(pending)
-    return v
+    return v, st
 
 
-def _count_and_depth_order(point_offsets, depths, tiles):
-    """K = point_offsets[P-1] (binding.cpp:153-154) and the depth order of the
-    Gaussians, the first stage of the binning. The depth sort needs only P, so
-    it is queued between the copy of K and the wait for it."""
+def _count_and_depth_order(scan_buf, depths, tiles):
+    """K = point_offsets[P-1] (binding.cpp:153-154), read with the scan's wait
+    status, and the depth order of the Gaussians, the first stage of the
+    binning.  The depth sort needs only P, so it is queued between the copy of
+    K and the wait for it."""
     P = tiles.numel()
     if P == 0:
         return 0, None
     lib = _lib.load()
     dev = tiles.device
-    pending = _last_u32_async(point_offsets)
+    pending = _read_async(scan_buf, P - 1)
     dws = torch.empty(int(lib.fgs_depth_order_workspace_bytes(P)), dtype=torch.uint8, device=dev)
     with _stage("binning"):
         _lib.check(lib.fgs_depth_order(P, _p(depths), _p(tiles), _p(dws), _stream(dev)))
-    return _wait_u32(pending), dws
+    K, status = _wait_read(pending)
+    check_wait(status, "rasterize_gaussians_forward (scan of tiles_touched)")
+    return K, dws
 
 
 # ---------------------------------------------------------------------------
@@ -527,32 +547,35 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     P = xys.shape[0]
     gx, gy = cfg["gx"], cfg["gy"]
     T = gx * gy
-    point_offsets = _inclusive_scan_i32(tiles)
+    scan_buf = _inclusive_scan_i32(tiles)  # point_offsets, then the scan's wait status
+    point_offsets = scan_buf[:P]
     # the zero-count metric array is made before the wait for K: the host work
     # between K's arrival and the binning launch is on the GPU's critical path
     metric_count = torch.zeros(P if get_flag else 0, dtype=torch.int32, device=dev)
     background = _to(inputs["background"], dev, torch.float32)
     metric_map = _to(inputs["metric_map"], dev, torch.int32)
-    K, depth_ws = _count_and_depth_order(point_offsets, depths.detach(), tiles)
+    K, depth_ws = _count_and_depth_order(scan_buf, depths.detach(), tiles)
     point_list_keys = point_list = ranges = bucket_count = bucket_offsets = None
     bucket_to_tile = sampled_t = sampled_ar = final_t = n_contrib = max_contrib = None
     pixel_colors = out_color = None
     B = 0
     if K > 0:
         with torch.no_grad():
-            point_list_keys, point_list, ranges, bucket_count, bucket_offsets = _binning_sorted(
-                xys.detach(), depths.detach(), conic.detach(), tiles, K, gx, gy, float(mult),
-                depth_ws, cfg["st_base"], cfg["st_masks"])
+            (point_list_keys, point_list, ranges, bucket_count, bucket_offsets,
+             tbuf) = _binning_sorted(xys.detach(), depths.detach(), conic.detach(), tiles, K, gx,
+                                     gy, float(mult), depth_ws, cfg["st_base"], cfg["st_masks"])
         ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
         if ws:
             # the sampled state is B * 256 entries: B is needed before the launch
-            B = _last_u32(bucket_offsets)
+            B, status = _value_and_status(tbuf, 4 * T - 1)
+            check_wait(status, "rasterize_gaussians_forward (binning)")
             pending_b = None
         else:
             # B = sum over tiles of ceil(n_t / 32) <= (K + 31 T) / 32: bucket_to_tile
             # is sized by that bound and cut to B once the value arrives, which
-            # is waited for after the rasterize launch
-            pending_b = _last_u32_async(bucket_offsets)
+            # is waited for after the rasterize launch (with the binning's wait
+            # status, the word after it)
+            pending_b = _read_async(tbuf, 4 * T - 1)
             B = (K + 31 * T) // 32
         if B > 0:
             rcfg = dict(W=cfg["W"], H=cfg["H"], C=3, T=T, B=B, get_flag=bool(get_flag),
@@ -562,7 +585,8 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
                 rcfg, ranges, point_list, bucket_offsets, xys, rgb, conic, background, radii,
                 metric_map, metric_count, vsp_out)
         if pending_b is not None:
-            B = _wait_u32(pending_b)
+            B, status = _wait_read(pending_b)
+            check_wait(status, "rasterize_gaussians_forward (binning)")
             if bucket_to_tile is not None:
                 bucket_to_tile = bucket_to_tile[:B]
     if point_list is None or final_t is None:  # nothing rendered: the reference's empty outputs

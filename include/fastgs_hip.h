@@ -149,15 +149,32 @@ int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p, const fgs_preprocess_
 
 /* ------------------------------------------------------------------------ */
 /* Scan / binning / sort / tile ranges.                                      */
+/*                                                                            */
+/* Bounded waits.  The scans and radix-sort passes are one-pass: each        */
+/* 4096-element chunk waits for its predecessors' published sums (chunks are */
+/* numbered in start order, so every wait ends).  Each wait is bounded as a  */
+/* backstop; one that gives up uses a partial sum, which keeps every write   */
+/* in bounds but makes the results invalid, and reports it in a wait-status  */
+/* word: bit 0 a scan chunk, bit 1 a radix-pass look-back.  The entry points */
+/* below take that word as `wait_status` (device, optional: NULL keeps it    */
+/* inside the workspace); the call writes it (0 when every wait completed)   */
+/* on the stream, and the caller reads it back with the results.             */
 /* ------------------------------------------------------------------------ */
+
+/* Polls of one bounded wait before it gives up (default 2^24); returns the
+ * previous value.  A process-wide setting read when a call is issued.  0 makes
+ * every wait give up at once without polling: every chunk after the first
+ * reports it, so a test can drive the error path deterministically while
+ * every kernel still runs to its end.  No reference counterpart. */
+uint32_t fgs_set_wait_spin_limit(uint32_t limit);
 
 /* Workspace for fgs_inclusive_scan_u32 over n elements. */
 size_t fgs_scan_workspace_bytes(int64_t n);
 
 /* out[i] = sum(in[0..i]) mod 2^32.  Replaces mx::cumsum(..., inclusive)
- * (binding.cpp:153,211).  in and out may alias. */
+ * (binding.cpp:153,211).  in and out may alias.  wait_status: see above. */
 int32_t fgs_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
-                               void* stream);
+                               uint32_t* wait_status, void* stream);
 
 /* fgs_inclusive_scan_u32 without a workspace: the scan's state lives in a
  * device array of the library (512.25 KiB per device, held until the process
@@ -167,7 +184,8 @@ int32_t fgs_inclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, voi
  * hipMalloc).  n <= 2^28 (FGS_ERR_INVALID_ARGUMENT above).  Every call on a
  * device shares that device's array: calls that overlap on one device (other
  * streams, other threads) race and must be ordered by the caller. */
-int32_t fgs_inclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n, void* stream);
+int32_t fgs_inclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, int64_t n,
+                                       uint32_t* wait_status, void* stream);
 
 /* Gaussian-order duplication: for each Gaussian with tiles_touched > 0, the
  * keys (tile_id << 32 | float_bits(depth)) and values (index) of its touched
@@ -186,10 +204,12 @@ size_t fgs_sort_workspace_bytes(int64_t n);
 
 /* Stable ascending LSD radix sort of (key, value) pairs on key bits
  * [begin_bit, end_bit).  Output in keys_out/values_out.  Replaces
- * mx::argsort + 2x mx::take (binding.cpp:195-197); ties keep input order. */
+ * mx::argsort + 2x mx::take (binding.cpp:195-197); ties keep input order.
+ * values_in NULL: the values are the input positions.  wait_status: see
+ * above. */
 int32_t fgs_sort_pairs_u64(const uint64_t* keys_in, const uint32_t* values_in, uint64_t* keys_out,
                            uint32_t* values_out, int64_t n, int32_t begin_bit, int32_t end_bit,
-                           void* workspace, void* stream);
+                           void* workspace, uint32_t* wait_status, void* stream);
 
 /* ranges[T][2] and bucket_count[T] from (sorted) 64-bit keys with the exact
  * semantics of fastgs_identify_tile_ranges_kernel and
@@ -228,6 +248,10 @@ typedef struct {
    * Gaussians (same grid): Gaussians with a record skip their tile walks. */
   const uint32_t* st_base;
   const uint64_t* st_masks;
+  /* NULL, or a device word the call writes with the wait status (see above)
+   * of its own waits and of the depth order it consumes (depth_order, or the
+   * one it runs itself), after them in stream order. */
+  uint32_t* wait_status;
 } fgs_binning_io;
 
 size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, int32_t num_tiles);
@@ -240,7 +264,9 @@ int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream);
  * the host waits; the result is passed as fgs_binning_io.depth_order.  No
  * reference counterpart of its own: it is the depth half of the argsort at
  * binding.cpp:195-197.  depth_workspace: fgs_depth_order_workspace_bytes(P),
- * 256-byte aligned, no initial contents required. */
+ * 256-byte aligned, no initial contents required.  The sort's wait status
+ * stays in the workspace and is reported by the fgs_binning_sorted call that
+ * consumes it. */
 size_t fgs_depth_order_workspace_bytes(int32_t P);
 int32_t fgs_depth_order(int32_t P, const float* depths, const uint32_t* tiles_touched,
                         void* depth_workspace, void* stream);

@@ -42,10 +42,22 @@ def test_workspace_queries_and_error_path():
     rc = lib.fgs_preprocess_fwd(None, None, None)
     assert rc == _lib.FGS_ERR_INVALID_ARGUMENT
     assert b"null" in lib.fgs_last_error()
-    rc = lib.fgs_inclusive_scan_u32(None, None, -1, None, None)
+    rc = lib.fgs_inclusive_scan_u32(None, None, -1, None, None, None)
     assert rc == _lib.FGS_ERR_INVALID_ARGUMENT
     with pytest.raises(ValueError):
         _lib.check(rc)
+
+
+def test_wait_spin_limit_setting():
+    """fgs_set_wait_spin_limit swaps the process-wide poll bound (default 2^24)
+    and returns the previous value; it touches no GPU."""
+    lib = _lib.load()
+    prev = lib.fgs_set_wait_spin_limit(7)
+    try:
+        assert prev == 1 << 24
+        assert lib.fgs_set_wait_spin_limit(0) == 7
+    finally:
+        assert lib.fgs_set_wait_spin_limit(prev) == 0
 
 
 def _inputs():

@@ -314,9 +314,10 @@ def test_binning_sorted_depth_order_entry(oracle, grid):
     _lib.check(lib.fgs_depth_order(P, g["geom_depths"].data_ptr(), tiles.data_ptr(),
                                    dws.data_ptr(), rasterizer._stream(dev)))
     for depth_ws in (None, dws):
-        keys, plist, ranges, bcount, boffs = rasterizer._binning_sorted(
+        keys, plist, ranges, bcount, boffs, tbuf = rasterizer._binning_sorted(
             g["geom_means2d"], g["geom_depths"], g["geom_conic_opacity"], tiles, K, gx, gy, 1.0,
             depth_ws)
+        assert int(tbuf[-1].item()) == 0  # wait status: every wait completed
         np.testing.assert_array_equal(to_np(keys).view(np.uint64), ref["point_list_keys"])
         np.testing.assert_array_equal(to_np(plist).view(np.uint32), ref["point_list"])
         np.testing.assert_array_equal(to_np(ranges).view(np.uint32).reshape(-1, 2),

@@ -32,18 +32,21 @@ def test_noalloc_scan_matches_workspace_scan_twice():
         ref = torch.empty(n, dtype=torch.int32, device=dev)
         got = torch.full((n,), -1, dtype=torch.int32, device=dev)
         ws = torch.empty(int(lib.fgs_scan_workspace_bytes(n)), dtype=torch.uint8, device=dev)
+        status = torch.full((2,), -1, dtype=torch.int32, device=dev)
         _lib.check(lib.fgs_inclusive_scan_u32(xin.data_ptr(), ref.data_ptr(), n, ws.data_ptr(),
-                                              stream))
-        _lib.check(lib.fgs_inclusive_scan_u32_noalloc(xin.data_ptr(), got.data_ptr(), n, stream))
+                                              status.data_ptr(), stream))
+        _lib.check(lib.fgs_inclusive_scan_u32_noalloc(xin.data_ptr(), got.data_ptr(), n,
+                                                      status[1:].data_ptr(), stream))
         torch.cuda.synchronize()
         g = got.cpu().numpy().view(np.uint32)
         np.testing.assert_array_equal(g, ref.cpu().numpy().view(np.uint32))
         np.testing.assert_array_equal(g, np.cumsum(x, dtype=np.uint64).astype(np.uint32))
+        assert status.cpu().tolist() == [0, 0]  # every wait completed
 
 
 def test_noalloc_scan_rejects_sizes_above_its_maximum():
     lib = _lib.load()
-    rc = lib.fgs_inclusive_scan_u32_noalloc(None, None, (1 << 28) + 1, None)
+    rc = lib.fgs_inclusive_scan_u32_noalloc(None, None, (1 << 28) + 1, None, None)
     assert rc == -1
     assert b"exceeds the maximum" in lib.fgs_last_error()
-    assert lib.fgs_inclusive_scan_u32_noalloc(None, None, 0, None) == 0
+    assert lib.fgs_inclusive_scan_u32_noalloc(None, None, 0, None, None) == 0
