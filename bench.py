@@ -368,9 +368,22 @@ def measured_traffic(config, stage):
         return None
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, sc, cams, seed=0):
-    """The C oracle (float build, OpenMP over host cores) on one pose of the same workload:
-    full forward + L1/SSIM loss gradient (torch CPU) + backward."""
+    """The C oracle (float build, OpenMP) on pose 0 of the same workload: full
+    forward + L1/SSIM loss gradient (torch CPU) + backward, the protocol of the
+    CPU baseline: the median of 3 steps on every host thread this process may
+    use, and one step on a single thread (OpenMP and torch both limited)."""
     import torch
     import torch.nn.functional as F
 
@@ -378,24 +391,46 @@ def cpu_baseline(cfg, sc, cams, seed=0):
     from oracle.oracle import Oracle
 
     orc = Oracle()
-    cores = int(orc.lib.orc_num_threads())
+    try:
+        ncpu = len(os.sched_getaffinity(0))
+    except AttributeError:
+        ncpu = os.cpu_count() or 1
     cam = cams[0]
     W, H = cfg["W"], cfg["H"]
     inp = syn.make_inputs(sc, cam)
     rng = np.random.default_rng(seed + 7)
     target = torch.from_numpy(rng.uniform(0, 1, (3, H, W)).astype(np.float32))
     win = gaussian_window(torch)
-    t0 = time.perf_counter()
-    fwd = orc.render(inp, W, H, cam.tan_fovx, cam.tan_fovy, cfg["degree"])
-    img = torch.from_numpy(fwd["out_color"].reshape(3, H, W).copy()).requires_grad_(True)
-    loss = (img - target).abs().mean() + 0.2 * (1 - ssim(torch, F, img, target, win))
-    loss.backward()
-    orc.render_backward(inp, fwd, img.grad.numpy().reshape(3, -1), W, H, cam.tan_fovx,
-                        cam.tan_fovy, cfg["degree"])
-    dt = time.perf_counter() - t0
-    return {"value": 1.0 / dt, "unit": "iters/s", "cores": cores, "kind": "port",
-            "sample": f"1 full training step (pose 0) of {cfg['desc']}; C oracle, "
-                      f"{cores} OpenMP threads; {dt:.2f} s"}
+
+    def one_step():
+        t0 = time.perf_counter()
+        fwd = orc.render(inp, W, H, cam.tan_fovx, cam.tan_fovy, cfg["degree"])
+        img = torch.from_numpy(fwd["out_color"].reshape(3, H, W).copy()).requires_grad_(True)
+        loss = (img - target).abs().mean() + 0.2 * (1 - ssim(torch, F, img, target, win))
+        loss.backward()
+        orc.render_backward(inp, fwd, img.grad.numpy().reshape(3, -1), W, H, cam.tan_fovx,
+                            cam.tan_fovy, cfg["degree"])
+        return time.perf_counter() - t0
+
+    torch_threads = torch.get_num_threads()
+    orc.lib.orc_set_num_threads(ncpu)
+    torch.set_num_threads(ncpu)
+    multi = sorted(one_step() for _ in range(3))
+    orc.lib.orc_set_num_threads(1)
+    torch.set_num_threads(1)
+    single = one_step()
+    orc.lib.orc_set_num_threads(ncpu)
+    torch.set_num_threads(torch_threads)
+    dt = multi[1]
+    model = _cpu_model()
+    return {"value": 1.0 / dt, "unit": "iters/s", "cores": ncpu, "kind": "port",
+            "model": model, "single_thread": {"value": 1.0 / single, "unit": "iters/s",
+                                              "cores": 1, "seconds": single},
+            "sample": f"pose 0 of {cfg['desc']}: full training step (forward, L1+SSIM loss "
+                      f"gradient, backward) of the C oracle (CPU restatement of the reference "
+                      f"Metal semantics); median of 3 steps on {ncpu} threads of {model} "
+                      f"({', '.join(f'{x:.2f}' for x in multi)} s), and 1 step on 1 thread "
+                      f"({single:.2f} s)"}
 
 
 def main():
@@ -451,7 +486,7 @@ def main():
     metric_map = torch.zeros(W * H, dtype=torch.int32, device=dev)
     win = gaussian_window(torch).to(dev)
 
-    def render(i, train=True):
+    def render(i, train=True, count_iterations=False):
         c = cam_t[i % len(cam_t)]
         vsp = torch.zeros((P, 4), device=dev, requires_grad=train)
         # activations (sigmoid / exp / quaternion normalise): one fused kernel each way
@@ -461,8 +496,9 @@ def main():
                   "opacities": opac, "dc": raw["dc"], "sh": raw["sh"], "background": background,
                   "metric_map": metric_map, "viewmatrix": c["viewmatrix"],
                   "projmatrix": c["projmatrix"], "campos": c["campos"], "viewspace_points": vsp}
-        out = fastgs_core.rasterize_gaussians(inputs, W, H, 16, 16, c["tan_fovx"], c["tan_fovy"],
-                                              deg)
+        out = fastgs_core.rasterize_gaussians_forward(inputs, W, H, 16, 16, c["tan_fovx"],
+                                                      c["tan_fovy"], deg,
+                                                      count_iterations=count_iterations)
         return out, vsp
 
     def step(i):
@@ -527,21 +563,35 @@ def main():
                           int(nc.to(torch.int64).sum()) if nc.numel() else 0))
         times = timer.collect()
         rasterizer.set_stage_timer(None)
+        # N_f: iterations of the reference blend loop (the stop iteration
+        # included), from the forward's counting mode in an untimed pass
+        nfs = []
+        with torch.no_grad():
+            for i in range(len(cam_t)):
+                o, _ = render(i, train=False, count_iterations=True)
+                it = o["img_n_iter"]
+                nfs.append(int(it.to(torch.int64).sum()) if it.numel() else 0)
         K = float(np.median([s[0] for s in stats]))
         B = float(np.median([s[1] for s in stats]))
         Pv = float(np.median([s[2] for s in stats]))
         Nb = float(np.median([s[3] for s in stats]))
+        Nf = float(np.median(nfs))
         T = ((W + 15) // 16) * ((H + 15) // 16)
         S = 12 * ((deg + 1) ** 2 - 1)
         stages = {}
         for name, v in times.items():
             ms = float(np.median(v))
-            b, f = algorithmic_work(name, K, P, Pv, T, W * H, S, B, Nb, Nb)
+            b, f = algorithmic_work(name, K, P, Pv, T, W * H, S, B, Nf, Nb)
             stages[name] = roofline_entry(name, ms, b, f)
+            mb = measured_traffic(args.config, name)
+            if mb is not None:  # FETCH_SIZE + WRITE_SIZE of the stage's kernels
+                stages[name]["measured_bytes"] = mb
+                stages[name]["measured_GBps"] = mb / (ms * 1e-3) / 1e9
         dom = max(stages, key=lambda k: stages[k]["ms"])
         d = stages[dom]
         result["stages"] = stages
-        result["counts"] = {"K": K, "B": B, "P_visible": Pv, "N_contrib": Nb, "tiles": T}
+        result["counts"] = {"K": K, "B": B, "P_visible": Pv, "N_contrib": Nb, "N_iter": Nf,
+                            "tiles": T}
         result["roofline"] = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
                               "peak": d["peak"], "unit": d["unit"], "frac": d["frac"],
                               "traffic": measured_traffic(args.config, dom)}

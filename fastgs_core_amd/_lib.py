@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class PreprocessParams(Structure):
@@ -70,7 +70,7 @@ class RasterFwdIO(Structure):
     _fields_ = [(n, c_void_p) for n in (
         "ranges", "point_list", "bucket_offsets", "means2d", "colors", "conic_opacity",
         "background", "metric_map", "bucket_to_tile", "sampled_t", "sampled_ar", "final_t",
-        "n_contrib", "max_contrib", "pixel_colors", "out_color", "metric_count")]
+        "n_contrib", "max_contrib", "pixel_colors", "out_color", "metric_count", "n_iter")]
 
 
 class RasterBwdIO(Structure):

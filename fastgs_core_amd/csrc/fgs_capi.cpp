@@ -30,4 +30,4 @@ int32_t check_launch(const char* what) {
 
 extern "C" const char* fgs_last_error(void) { return g_last_error; }
 
-extern "C" int32_t fgs_abi_version(void) { return 8; }
+extern "C" int32_t fgs_abi_version(void) { return 9; }

@@ -85,12 +85,16 @@ struct FiniteTag {
   static constexpr bool value = B;
 };
 
-// kMode bit 0: write the sampled state; bit 1: count metric hits (get_flag).
+// kMode bit 0: write the sampled state; bit 1: count metric hits (get_flag);
+// bit 2: write each pixel's loop iterations under the reference loop (the
+// splats it visits, the one it stops at included: the stop index + 1, or the
+// tile's list length if it never stops), a measurement output.
 template <int NCH, int kMode>
 __global__ void __launch_bounds__(256, 6)
 raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, RasterShape sh) {
   constexpr bool kSampled = (kMode & 1) != 0;
   constexpr bool kMetric = (kMode & 2) != 0;
+  constexpr bool kIters = (kMode & 4) != 0;
   __shared__ float4 s_a[256];
   __shared__ float4 s_b[256];
   __shared__ float s_c[256];
@@ -119,6 +123,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
   const float pxf = (float)px, pyf = (float)py;
   float T = 1.0f;
   uint32_t last = 0;
+  uint32_t iters = 0;  // kIters: the stop index + 1 once the pixel stops
   float acc[3] = {0.0f, 0.0f, 0.0f};
   int done = inside ? 0 : 1;
   const int rounds = (n + 255) / 256;
@@ -133,6 +138,10 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
       float4 a, b;
       float c;
       stage_splat<NCH>(g, (uint32_t)prm.num_points, io.means2d, io.colors, prm.num_channels, io.conic_opacity, a, b, c);
+      // staged as (x, y, -a/2, b) and (-c/2, o, ...): halving is exact, so
+      // (-a/2 dx) dx + (-c/2 dy) dy is -1/2 (a dx dx + c dy dy) bit for bit
+      a.z = -0.5f * a.z;
+      b.x = -0.5f * b.x;
       s_a[t] = a;
       s_b[t] = b;
       s_c[t] = c;
@@ -171,7 +180,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           const float4 b = s_b[j];
           const float dx = a.x - pxf;
           const float dy = a.y - pyf;
-          const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
+          const float power = (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
           const float alpha = fminf(0.99f, b.y * det_expf(power));
           const float test_t = T * (1.0f - alpha);
           const bool blend = live && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
@@ -197,6 +206,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
             atomicAdd(&io.metric_count[s_g[j]], 1);
           T = take ? test_t : T;
           last = take ? (uint32_t)(jj + 1) : last;
+          if (kIters) iters = stop ? (uint32_t)(jj + 1) : iters;
         }
         if (__ballot(live) == 0ull) break;  // uniform
       }
@@ -213,6 +223,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
   if (inside) {
     io.final_t[pix] = T;
     io.n_contrib[pix] = last;
+    if (kIters) io.n_iter[pix] = iters ? iters : (uint32_t)n;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       io.pixel_colors[(size_t)c * HW + pix] = acc[c];
@@ -613,7 +624,11 @@ static void launch_fwd(int mode, dim3 grid, dim3 block, hipStream_t st,
     case 0: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 0>), grid, block, 0, st, p, io, sh); break;
     case 1: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 1>), grid, block, 0, st, p, io, sh); break;
     case 2: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 2>), grid, block, 0, st, p, io, sh); break;
-    default: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 3>), grid, block, 0, st, p, io, sh);
+    case 3: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 3>), grid, block, 0, st, p, io, sh); break;
+    case 4: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 4>), grid, block, 0, st, p, io, sh); break;
+    case 5: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 5>), grid, block, 0, st, p, io, sh); break;
+    case 6: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 6>), grid, block, 0, st, p, io, sh); break;
+    default: hipLaunchKernelGGL((raster_fwd_kernel<NCH, 7>), grid, block, 0, st, p, io, sh);
   }
 }
 
@@ -670,6 +685,7 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
     // Pixels of tiles beyond num_tiles are never rendered: clear them.
     span(io->final_t, HW);
     span(io->n_contrib, HW);
+    if (io->n_iter) span(io->n_iter, HW);
     span(io->pixel_colors, C * HW);
     span(io->out_color, C * HW);
   }
@@ -677,7 +693,8 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
   if (f.count) launch_fill_spans(f, st);
   if (tiles == 0) return check_launch("rasterize_fwd");
   RasterShape sh{W, H, gx, gy};
-  const int mode = (p->write_sampled && p->bucket_sum > 0 ? 1 : 0) | (p->get_flag ? 2 : 0);
+  const int mode = (p->write_sampled && p->bucket_sum > 0 ? 1 : 0) | (p->get_flag ? 2 : 0) |
+                   (io->n_iter ? 4 : 0);
   const dim3 grid(tiles), block(256);
   if (NCH == 3) launch_fwd<3>(mode, grid, block, st, *p, *io, sh);
   else if (NCH == 2) launch_fwd<2>(mode, grid, block, st, *p, *io, sh);

@@ -274,11 +274,14 @@ class _Rasterize(torch.autograd.Function):
             raise ValueError(f"metric_count has {mc.numel()} entries, get_flag needs one per "
                              f"Gaussian ({P})")
         prm = _lib.RasterParams(W, H, C, T, B, int(get_flag), int(ws), P, point_list.numel())
+        # optional measurement output (count_iterations): handed back through cfg
+        n_iter = torch.empty(HW, dtype=torch.int32, device=dev) if cfg.get("count_iter") else None
+        cfg["n_iter"] = n_iter
         io = _lib.RasterFwdIO(
             _p(ranges), _p(point_list), _p(bucket_offsets), _p(means2d), _p(colors),
             _p(conic_opacity), _p(background), _p(metric_map), _p(bucket_to_tile),
             _p(sampled_t), _p(sampled_ar), _p(final_t), _p(n_contrib), _p(max_contrib),
-            _p(pixel_colors), _p(out_color), _p(mc))
+            _p(pixel_colors), _p(out_color), _p(mc), _p(n_iter))
         with _stage("rasterize_fwd"):
             _lib.check(lib.fgs_rasterize_fwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
         ctx.cfg = cfg
@@ -535,10 +538,15 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
                                 tan_fovy: float = 1.0, degree: int = 0,
                                 scale_modifier: float = 1.0, mult: float = 1.0,
                                 prefiltered: bool = False, get_flag: bool = False,
-                                *, write_sampled: Optional[bool] = None) -> Dict[str, Any]:
+                                *, write_sampled: Optional[bool] = None,
+                                count_iterations: bool = False) -> Dict[str, Any]:
     """Full forward (binding.cpp:33-282): preprocess -> scan -> binning/sort ->
     tile ranges -> bucket offsets -> rasterize.  The two 4-byte reads of the
-    reference (K and B) are waited for while the GPU has queued work."""
+    reference (K and B) are waited for while the GPU has queued work.
+
+    ``count_iterations`` (measurement, no reference counterpart) adds
+    ``img_n_iter``: each pixel's iterations of the reference blend loop
+    (fastgs_rasterize.metal:100-131, the stop iteration included)."""
     fn = "rasterize_gaussians_forward"
     outs, cfg, dev = _run_preprocess(inputs, fn, _RG_NAMES, image_width, image_height, block_x,
                                      block_y, tan_fovx, tan_fovy, degree, scale_modifier, mult,
@@ -579,7 +587,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
             B = (K + 31 * T) // 32
         if B > 0:
             rcfg = dict(W=cfg["W"], H=cfg["H"], C=3, T=T, B=B, get_flag=bool(get_flag),
-                        write_sampled=ws)
+                        write_sampled=ws, count_iter=bool(count_iterations))
             (bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib, max_contrib,
              pixel_colors, out_color, metric_count) = _Rasterize.apply(
                 rcfg, ranges, point_list, bucket_offsets, xys, rgb, conic, background, radii,
@@ -606,7 +614,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
         max_contrib = torch.zeros(0, **i32)
         pixel_colors = torch.zeros(0, **f32)
         out_color = torch.zeros(0, **f32)
-    return {
+    result = {
         "rendered": K, "num_buckets": B, "out_color": out_color, "radii": radii,
         "point_offsets": point_offsets, "ranges": ranges, "bucket_count": bucket_count,
         "bucket_offsets": bucket_offsets, "point_list_keys": point_list_keys,
@@ -617,6 +625,10 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
         "img_final_t": final_t, "img_n_contrib": n_contrib, "img_max_contrib": max_contrib,
         "img_pixel_colors": pixel_colors,
     }
+    if count_iterations:
+        result["img_n_iter"] = (rcfg["n_iter"] if K > 0 and B > 0 and final_t.numel()
+                                else torch.zeros(0, dtype=torch.int32, device=dev))
+    return result
 
 
 rasterize_gaussians = rasterize_gaussians_forward

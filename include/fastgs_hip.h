@@ -306,6 +306,10 @@ typedef struct {
   float* pixel_colors;             /* [C,H*W] */
   float* out_color;                /* [C,H*W] */
   int32_t* metric_count;           /* [P] (zeroed and accumulated when get_flag) */
+  /* NULL, or [H*W]: each pixel's loop iterations under the reference loop
+   * (fastgs_rasterize.metal:100-131: the splats it visits, the one it stops
+   * at included), a measurement output with no reference counterpart. */
+  uint32_t* n_iter;
 } fgs_raster_fwd_io;
 
 /* Replaces FastGSRasterize::eval_gpu (fastgs_rasterize.cpp:91-169) /

@@ -1400,6 +1400,14 @@ void orc_preprocess_bwd_mag(const orc_params* prm, const real* means3d, const re
 int orc_sizeof_real(void) { return (int)sizeof(real); }
 
 /* Threads the OpenMP loops use (1 without OpenMP). */
+void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+  omp_set_num_threads(n > 0 ? n : 1);
+#else
+  (void)n;
+#endif
+}
+
 int orc_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();
