@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class PreprocessParams(Structure):
@@ -119,6 +119,7 @@ SIGNATURES = {
     "fgs_preprocess_bwd": (c_int32, [POINTER(PreprocessParams), POINTER(PreprocessBwdIO), c_void_p]),
     "fgs_scan_workspace_bytes": (c_size_t, [c_int64]),
     "fgs_set_wait_spin_limit": (c_uint32, [c_uint32]),
+    "fgs_set_launch_events": (c_int32, [c_char_p, c_void_p, c_void_p]),
     "fgs_inclusive_scan_u32": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
                                          c_void_p]),
     "fgs_inclusive_scan_u32_noalloc": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),

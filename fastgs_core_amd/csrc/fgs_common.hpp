@@ -16,6 +16,21 @@ int32_t set_error(int32_t code, const char* msg);
 // Checks hipGetLastError() after a launch; returns FGS_OK or FGS_ERR_LAUNCH.
 int32_t check_launch(const char* what);
 
+// Main kernels whose launches can be bracketed by caller events
+// (fgs_set_launch_events); launch_mark(k, st, 0) goes directly before the
+// launch, launch_mark(k, st, 1) directly after it.  Returns FGS_OK, or an
+// error code when recording an event fails.
+enum LaunchKind {
+  kLaunchPreprocessFwd,
+  kLaunchRasterFwd,
+  kLaunchRasterBwd,
+  kLaunchPreprocessBwd,
+  kLaunchLossFwd,
+  kLaunchLossBwd,
+  kLaunchKinds
+};
+int32_t launch_mark(LaunchKind k, hipStream_t st, int after);
+
 inline unsigned ceil_div_u(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
 // Up to kFillSpans 32-bit arrays set to one value by a single kernel launch

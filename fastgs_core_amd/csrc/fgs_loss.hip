@@ -378,8 +378,11 @@ extern "C" int32_t fgs_l1_ssim_fwd(const float* img, const float* tgt, int32_t C
   const LossArgs a = make_args(C, H, W, w_l1, w_ssim);
   const int nt = a.strips_x * a.chunks_y;
   hipStream_t st = (hipStream_t)stream;
+  if (const int32_t e = launch_mark(kLaunchLossFwd, st, 0)) return e;
   hipLaunchKernelGGL(l1_ssim_fwd_kernel, dim3(nt, C), dim3(kSW), 0, st, a, img, tgt, dmaps,
                      (float*)workspace);
+  if (check_launch("l1_ssim_fwd") != FGS_OK) return FGS_ERR_LAUNCH;
+  if (const int32_t e = launch_mark(kLaunchLossFwd, st, 1)) return e;
   hipLaunchKernelGGL(l1_ssim_reduce_kernel, dim3(1), dim3(256), 0, st, (const float*)workspace,
                      nt * C, w_l1, w_ssim, 1.0 / ((double)C * H * W), loss);
   return check_launch("l1_ssim_fwd");
@@ -394,9 +397,12 @@ extern "C" int32_t fgs_l1_ssim_bwd(const float* img, const float* tgt, const flo
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_l1_ssim_bwd: null pointer");
   const LossArgs a = make_args(C, H, W, w_l1, w_ssim);
   const int nt = a.strips_x * a.chunks_y;
-  hipLaunchKernelGGL(l1_ssim_bwd_kernel, dim3(nt, C), dim3(kSW), 0, (hipStream_t)stream, a, img,
-                     tgt, dmaps, grad_out, dimg);
-  return check_launch("l1_ssim_bwd");
+  hipStream_t st = (hipStream_t)stream;
+  if (const int32_t e = launch_mark(kLaunchLossBwd, st, 0)) return e;
+  hipLaunchKernelGGL(l1_ssim_bwd_kernel, dim3(nt, C), dim3(kSW), 0, st, a, img, tgt, dmaps,
+                     grad_out, dimg);
+  if (check_launch("l1_ssim_bwd") != FGS_OK) return FGS_ERR_LAUNCH;
+  return launch_mark(kLaunchLossBwd, st, 1);
 }
 
 extern "C" size_t fgs_pointwise_loss_workspace_bytes(int64_t n) {

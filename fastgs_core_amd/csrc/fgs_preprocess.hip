@@ -645,6 +645,7 @@ extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
   // 16-byte loads; the direct path reads 4-byte elements 180 bytes apart.
   const hipStream_t st = (hipStream_t)stream;
   const dim3 grid(blocks), block(256);
+  if (const int32_t e = launch_mark(kLaunchPreprocessFwd, st, 0)) return e;
   switch (staged_sh_row(p, io->sh, io->sh)) {
     case 9:
       hipLaunchKernelGGL(preprocess_fwd_kernel<9>, grid, block, 256 * 9 * sizeof(float), st, *p,
@@ -661,7 +662,8 @@ extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
     default:
       hipLaunchKernelGGL(preprocess_fwd_kernel<0>, grid, block, 0, st, *p, *io, fx, fy);
   }
-  return check_launch("preprocess_fwd_kernel");
+  if (check_launch("preprocess_fwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
+  return launch_mark(kLaunchPreprocessFwd, st, 1);
 }
 
 extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
@@ -682,6 +684,7 @@ extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
   const unsigned blocks = (unsigned)((p->P + 255) / 256);
   const hipStream_t st = (hipStream_t)stream;
   const dim3 grid(blocks), block(256);
+  if (const int32_t e = launch_mark(kLaunchPreprocessBwd, st, 0)) return e;
   switch (staged_sh_row(p, io->sh, io->dL_dsh)) {
     case 9:
       hipLaunchKernelGGL(preprocess_bwd_kernel<9>, grid, block, 256 * 9 * sizeof(float), st, *p,
@@ -698,5 +701,6 @@ extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
     default:
       hipLaunchKernelGGL(preprocess_bwd_kernel<0>, grid, block, 0, st, *p, *io, fx, fy);
   }
-  return check_launch("preprocess_bwd_kernel");
+  if (check_launch("preprocess_bwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
+  return launch_mark(kLaunchPreprocessBwd, st, 1);
 }

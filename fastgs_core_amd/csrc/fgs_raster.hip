@@ -699,10 +699,12 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
   const int mode = (p->write_sampled && p->bucket_sum > 0 ? 1 : 0) | (p->get_flag ? 2 : 0) |
                    (io->n_iter ? 4 : 0);
   const dim3 grid(tiles), block(256);
+  if (const int32_t e = launch_mark(kLaunchRasterFwd, st, 0)) return e;
   if (NCH == 3) launch_fwd<3>(mode, grid, block, st, *p, *io, sh);
   else if (NCH == 2) launch_fwd<2>(mode, grid, block, st, *p, *io, sh);
   else launch_fwd<1>(mode, grid, block, st, *p, *io, sh);
-  return check_launch("raster_fwd_kernel");
+  if (check_launch("raster_fwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
+  return launch_mark(kLaunchRasterFwd, st, 1);
 }
 
 // Grids above this many tiles run in index order (one workgroup sorts the
@@ -753,6 +755,7 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   if (!(kio.tile_order && tiles <= kMaxOrderedTiles)) kio.tile_order = nullptr;  // index order
   hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)(fill_blocks + (kio.tile_order ? 1 : 0))),
                      dim3(kOrderThreads), 0, st, f, io->max_contrib, tiles, kio.tile_order);
+  if (const int32_t e = launch_mark(kLaunchRasterBwd, st, 0)) return e;
   if (NCH == 3)
     hipLaunchKernelGGL(raster_bwd_kernel<3>, dim3(tiles), dim3(64), 0, st, *p, kio, sh);
   else if (NCH == 2)
@@ -760,6 +763,7 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   else
     hipLaunchKernelGGL(raster_bwd_kernel<1>, dim3(tiles), dim3(64), 0, st, *p, kio, sh);
   if (check_launch("raster_bwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
+  if (const int32_t e = launch_mark(kLaunchRasterBwd, st, 1)) return e;
   hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
                      io->dL_dviewspace, io->dL_dmeans2d, P);
   return check_launch("copy_means2d_grad_kernel");

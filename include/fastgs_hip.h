@@ -43,6 +43,19 @@ const char* fgs_last_error(void);
  * addition). */
 int32_t fgs_abi_version(void);
 
+/* Launch events (measurement; no reference counterpart).  Asks the library
+ * to record the caller's events `start` and `stop` (hipEvent_t, as void*) on
+ * the launch stream directly before and after every launch of one kernel,
+ * so that the kernel's own duration can be read with hipEventElapsedTime,
+ * without the small kernels an entry point launches around it.  `kernel`
+ * names the main kernel of one stage: "preprocess_fwd", "rasterize_fwd",
+ * "rasterize_bwd", "preprocess_bwd", "loss_fwd" or "loss_bwd" (the SSIM map
+ * kernels of fgs_l1_ssim_fwd / fgs_l1_ssim_bwd).  Both events NULL clears the
+ * entry; one of them NULL, or an unknown name, is FGS_ERR_INVALID_ARGUMENT.
+ * A process-wide setting read at each launch; the events must stay valid
+ * until it is cleared. */
+int32_t fgs_set_launch_events(const char* kernel, void* start, void* stop);
+
 /* ------------------------------------------------------------------------ */
 /* Preprocess.                                                               */
 /* Replaces PreprocessParams/PreprocessKernelParams                          */

@@ -60,6 +60,23 @@ def test_wait_spin_limit_setting():
         assert lib.fgs_set_wait_spin_limit(prev) == 0
 
 
+def test_launch_events_argument_checks():
+    """fgs_set_launch_events validates its arguments without touching a GPU:
+    unknown names and a single event are rejected; clearing (both NULL) is
+    accepted for every named kernel."""
+    lib = _lib.load()
+    assert lib.fgs_set_launch_events(b"no_such_kernel", None, None) == \
+        _lib.FGS_ERR_INVALID_ARGUMENT
+    assert b"unknown" in lib.fgs_last_error()
+    assert lib.fgs_set_launch_events(None, None, None) == _lib.FGS_ERR_INVALID_ARGUMENT
+    assert lib.fgs_set_launch_events(b"rasterize_bwd", ctypes.c_void_p(16), None) == \
+        _lib.FGS_ERR_INVALID_ARGUMENT
+    assert b"both" in lib.fgs_last_error()
+    for name in (b"preprocess_fwd", b"rasterize_fwd", b"rasterize_bwd", b"preprocess_bwd",
+                 b"loss_fwd", b"loss_bwd"):
+        assert lib.fgs_set_launch_events(name, None, None) == _lib.FGS_OK
+
+
 def _inputs():
     sc = syn.scene_config1(0, 64)
     cam = syn.config1_camera(32, 32)
