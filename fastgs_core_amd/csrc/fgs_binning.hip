@@ -419,6 +419,9 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   const int lane = lane_id();
   const uint32_t mask = (1u << nbits) - 1u;
   for (int i = t; i < kW * 256; i += kT) (&s_wh[0][0])[i] = 0;
+  // the pass's global digit count, loaded now: its latency overlaps the
+  // ticket, the key loads and the ranking
+  const uint32_t gcount = (uint32_t)t <= mask ? hist[t] : 0u;
   const int64_t chunk = take_ticket(ticket, &s_slot);  // includes a barrier
   const int64_t base = chunk * kC + (int64_t)w * (kC / kW);
   const uint64_t lt = lanemask_lt();
@@ -472,8 +475,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
       c[k] = dig ? s_wh[k][t] : 0u;
       tot += c[k];
     }
-    const uint32_t g = dig ? hist[t] : 0u;
-    const uint32_t gbase = block_excl_scan(g, s_tmp, nullptr);
+    const uint32_t gbase = block_excl_scan(gcount, s_tmp, nullptr);
     uint32_t total;
     const uint32_t ds = block_excl_scan(tot, s_tmp, &total);
     if (t < 256) {

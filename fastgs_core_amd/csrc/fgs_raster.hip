@@ -59,9 +59,10 @@ __device__ __forceinline__ void stage_splat(uint32_t g, uint32_t P, const float*
 // Rows [lo, hi] outside which no pixel of a splat can reach alpha >= 1/255.
 // alpha >= 1/255 needs o*exp(power) >= 1/255, i.e. q(d) = d^T Conic d <= tau =
 // 2 ln(255 o).  The row extent of {q <= tau} is sqrt(tau * a / det).  Margins:
-// the float power of a pixel differs from -q/2 by at most ~7e-7 (a dx^2 +
-// c dy^2) <= 7e-7 q (1 + |rho|) / (1 - |rho|) < 3e-3 q for the conics culled
-// here (det > 1e-3 a c, rho = b / sqrt(a c)); the exp, the hardware log and
+// the float power of a pixel (splat_power) differs from -q/2 by at most
+// 3 * 2^-24 (a dx^2 + c dy^2) <= 1.8e-7 q (1 + |rho|) / (1 - |rho|) < 8e-4 q
+// for the conics culled here (det > 1e-3 a c, rho = b / sqrt(a c)); the exp
+// (blend_expf, relative error < 4.3e-7 on [-5.5, 0]), the hardware log and
 // the product o*G move the threshold by ~1e-6; det loses at most ~6e-5 to
 // cancellation.  tau' = 1.01 tau + 0.05 and hy * 1.001 + 0.25 px cover all of
 // these several times over.  Ill-conditioned or non-positive conics, NaN
@@ -141,9 +142,10 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
       float4 a, b;
       float c;
       stage_splat<NCH>(g, (uint32_t)prm.num_points, io.means2d, io.colors, prm.num_channels, io.conic_opacity, a, b, c);
-      // staged as (x, y, -a/2, b) and (-c/2, o, ...): halving is exact, so
-      // (-a/2 dx) dx + (-c/2 dy) dy is -1/2 (a dx dx + c dy dy) bit for bit
+      // staged as (x, y, A, B) and (C, o, ...) with A = -a/2, B = -b,
+      // C = -c/2, the operands of splat_power
       a.z = -0.5f * a.z;
+      a.w = -a.w;
       b.x = -0.5f * b.x;
       s_a[t] = a;
       s_b[t] = b;
@@ -183,8 +185,8 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           const float4 b = s_b[j];
           const float dx = a.x - pxf;
           const float dy = a.y - pyf;
-          const float power = (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-          const float alpha = fminf(0.99f, b.y * det_expf(power));
+          const float power = splat_power(a.z, a.w, b.x, dx, dy);
+          const float alpha = fminf(0.99f, b.y * blend_expf(power));
           const float test_t = T * (1.0f - alpha);
           const bool blend = live && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
           const bool stop = blend && test_t < 0.0001f;
@@ -332,14 +334,18 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
   bool any = false;
   const float dx = a.x - pxf;
   const float dxdx = dx * dx;
+  // the forward's power, with its per-splat parts kept for the four strips
+  const float Bdx = -a.w * dx;
+  const float Adxdx = (-0.5f * a.z * dx) * dx;
+  const float Cc = -0.5f * b.x;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     if (jj >= nc_max[k]) continue;  // every pixel of the strip ends before this splat
     const float strip_lo = ty0 + (float)(4 * k);
     if (!(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;  // wave-uniform
     const float dy = a.y - (pyf0 + (float)(4 * k));
-    const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-    const float G = det_expf(power);
+    const float power = splat_power_rows(Bdx, Adxdx, Cc, dy);
+    const float G = blend_expf(power);
     const float oG = b.y * G;
     const float alpha = fminf(0.99f, oG);
     const bool act = jj < nc[k] && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);

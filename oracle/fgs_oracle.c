@@ -38,6 +38,8 @@ typedef double real;
 #define RMIN(a, b) fmin(a, b)
 #define RMAX(a, b) fmax(a, b)
 #define REXP(x) exp(x)
+#define RBEXP(x) exp(x)
+#define RFMA(a, b, c) fma(a, b, c)
 #define RLOG(x) log(x)
 #else
 typedef float real;
@@ -48,6 +50,8 @@ typedef float real;
 #define RMIN(a, b) fminf(a, b)
 #define RMAX(a, b) fmaxf(a, b)
 #define REXP(x) orc_expf(x)
+#define RBEXP(x) orc_blend_expf(x)
+#define RFMA(a, b, c) fmaf(a, b, c)
 #define RLOG(x) orc_logf(x)
 #endif
 
@@ -77,6 +81,27 @@ float orc_expf(float x) {
   q = fmaf(q, r, 1.0f);
   const float p = fmaf(r, q, 1.0f);
   return ldexpf(p, (int)n);
+}
+
+/* exp of a blend exponent (the rasterizer's G = exp(power)): 2^t with
+ * t = x*log2(e) rounded to float, n = floor(t), f = t - n (exact) in [0, 1);
+ * 2^f = 1 + f*q(f), q of degree 4 fitted to the relative error at 400
+ * Chebyshev nodes on [0, 1] by iteratively reweighted least squares, Horner
+ * with correctly rounded fused multiply-adds; scaled by ldexp (exact).  x is
+ * clamped at -87.  Relative error at most 2e-7 plus 0.35 ulp of t and
+ * 1.34e-8 |x| (the roundings of t and of log2(e)); tests/test_oracle_math.py
+ * pins it against float64 exp. */
+float orc_blend_expf(float x) {
+  x = fmaxf(x, -87.0f);
+  const float t = x * 1.44269504088896341f;
+  const float n = floorf(t);
+  const float f = t - n;
+  float q = 0x1.e86492p-10f;
+  q = fmaf(q, f, 0x1.279248p-7f);
+  q = fmaf(q, f, 0x1.c925b2p-5f);
+  q = fmaf(q, f, 0x1.ebd92ep-3f);
+  q = fmaf(q, f, 0x1.62e4d4p-1f);
+  return ldexpf(fmaf(f, q, 1.0f), (int)n);
 }
 
 /* ln(x) for float x: x = m*2^e with m in [sqrt(1/2), sqrt(2)), then
@@ -118,6 +143,24 @@ static inline int32_t orc_f2i(real v) {
   if (v >= (real)2147483648.0) return INT32_MAX;
   if (v <= (real)-2147483648.0) return INT32_MIN;
   return (int32_t)v;
+}
+
+/* Exponent of a splat at offset (dx, dy) from its centre (the blend loops of
+ * fastgs_rasterize.metal:105-106 and fastgs_rasterize_backward.metal:189-190:
+ * power = -1/2 (a dx^2 + c dy^2) - b dx dy for the conic (a, b, c)), written
+ * as A dx^2 + B dx dy + C dy^2 with A = -a/2, B = -b, C = -c/2 (each exact)
+ * and evaluated as fma(dy, fma(C, dy, B dx), (A dx) dx), the HIP kernels'
+ * operation order. */
+static inline real splat_power(const real* co, real dx, real dy) {
+  const real A = (real)-0.5 * co[0], B = -co[1], C = (real)-0.5 * co[2];
+  return RFMA(dy, RFMA(C, dy, B * dx), (A * dx) * dx);
+}
+
+/* splat_power of the conic (a, b, c) at (dx, dy), exported for its error-bound
+ * test (inputs and result converted to and from real). */
+double orc_splat_power(double a, double b, double c, double dx, double dy) {
+  const real co[4] = {(real)a, (real)b, (real)c, (real)0};
+  return (double)splat_power(co, (real)dx, (real)dy);
 }
 
 static inline int imin(int a, int b) { return a < b ? a : b; }
@@ -666,9 +709,9 @@ void orc_rasterize_fwd(const orc_rparams* rp, const uint32_t* ranges, const uint
           real dx = means2d[2 * (size_t)g] - pxf;
           real dy = means2d[2 * (size_t)g + 1] - pyf;
           const real* co = conic_opacity + 4 * (size_t)g;
-          real power = (real)-0.5 * (co[0] * dx * dx + co[2] * dy * dy) - co[1] * dx * dy;
+          real power = splat_power(co, dx, dy);
           if (power > (real)0) continue;
-          real alpha = RMIN((real)0.99, co[3] * REXP(power));
+          real alpha = RMIN((real)0.99, co[3] * RBEXP(power));
           if (alpha < (real)1 / (real)255) continue;
           real test_t = T * ((real)1 - alpha);
           if (test_t < (real)0.0001) break;
@@ -779,9 +822,9 @@ void orc_rasterize_bwd_mag(const orc_rparams* rp, const uint32_t* ranges,
             real dx = means2d[2 * (size_t)g] - pxf;
             real dy = means2d[2 * (size_t)g + 1] - pyf;
             const real* co = conic_opacity + 4 * (size_t)g;
-            real power = (real)-0.5 * (co[0] * dx * dx + co[2] * dy * dy) - co[1] * dx * dy;
+            real power = splat_power(co, dx, dy);
             if (power > (real)0) continue;
-            real G = REXP(power);
+            real G = RBEXP(power);
             real alpha = RMIN((real)0.99, co[3] * G);
             if (alpha < (real)1 / (real)255) continue;
             rec_g[m] = g;

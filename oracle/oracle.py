@@ -11,7 +11,9 @@ of ``rasterize_gaussians_forward`` (reference binding.cpp:33-282) and
 then fastgs_preprocess.cpp:191-206).
 
 Parity status of each C function (how it is pinned; see tests/test_oracle_*):
-  orc_expf / orc_logf      : error bounds against numpy float64 exp/log.
+  orc_expf / orc_logf /    : error bounds against numpy float64 exp/log.
+  orc_blend_expf
+  splat_power              : error bound against the float64 quadratic form.
   orc_preprocess_fwd       : closed forms (identity camera cov2D = J J^T + 0.3),
                              reference KAT (preprocess_smoke: all zero), and the
                              double build's finite differences through it.
@@ -35,7 +37,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_float, c_int32, c_int64, c_uint32, c_void_p
+from ctypes import POINTER, c_double, c_float, c_int32, c_int64, c_uint32, c_void_p
 
 import numpy as np
 
@@ -101,6 +103,10 @@ class Oracle:
         L = self.lib
         L.orc_expf.restype = c_float
         L.orc_expf.argtypes = [c_float]
+        L.orc_blend_expf.restype = c_float
+        L.orc_blend_expf.argtypes = [c_float]
+        L.orc_splat_power.restype = c_double
+        L.orc_splat_power.argtypes = [c_double] * 5
         L.orc_logf.restype = c_float
         L.orc_logf.argtypes = [c_float]
         L.orc_sizeof_real.restype = c_int32
@@ -117,6 +123,12 @@ class Oracle:
 
     def expf(self, x: float) -> float:
         return self.lib.orc_expf(float(x))
+
+    def blend_expf(self, x: float) -> float:
+        return self.lib.orc_blend_expf(float(x))
+
+    def splat_power(self, a, b, c, dx, dy) -> float:
+        return self.lib.orc_splat_power(float(a), float(b), float(c), float(dx), float(dy))
 
     def logf(self, x: float) -> float:
         return self.lib.orc_logf(float(x))

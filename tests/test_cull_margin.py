@@ -4,8 +4,9 @@ strip that holds a pixel with alpha >= 1/255 would corrupt that pixel's
 transmittance recovery, so the extent must contain every such pixel.
 
 This CPU test restates the kernel's float32 arithmetic with numpy (power
-as the forward computes it, no FMA contraction; the exp and the hardware log
-perturbed by several times their error) on splats from isotropic to the most
+as splat_power computes it, fused multiply-adds emulated in float64; the exp
+and the hardware log perturbed by at least their error) on splats from
+isotropic to the most
 elongated the extent is used for (det just above 1e-3 a c), and checks that
 every pixel that blends lies inside the extent, and that the extent is not
 loose by more than its stated margins.
@@ -13,6 +14,20 @@ loose by more than its stated margins.
 import numpy as np
 
 f32 = np.float32
+
+
+EXP_ERR = 4.5e-7  # blend_expf's relative error on [-5.5, 0] is below 4.3e-7
+
+
+def _fma32(x, y, z):
+    return f32(np.float64(x) * np.float64(y) + np.float64(z))
+
+
+def _power32(a, b, c, dx, dy):
+    """splat_power: fma(dy, fma(C, dy, B dx), (A dx) dx), A = -a/2, B = -b,
+    C = -c/2, in float32 (works elementwise on arrays)."""
+    A, B, C = f32(-0.5) * a, -b, f32(-0.5) * c
+    return _fma32(dy, _fma32(C, dy, f32(B * dx)), f32(f32(A * dx) * dx))
 
 
 def _rows(y, a, b, c, o, log_err):
@@ -53,7 +68,7 @@ def _splats(rng, n):
 
 def _active_rows(x, y, a, b, c, o, rng):
     """Rows of pixels (integer coordinates) whose alpha >= 1/255, with the
-    kernel's float32 power and an exp perturbed by +-3e-7."""
+    kernel's float32 power and an exp raised by EXP_ERR."""
     det = np.float64(a) * np.float64(c) - np.float64(b) ** 2
     tau = 2.0 * np.log(255.0 * np.float64(o))
     ry = np.sqrt(max(tau, 0.0) * np.float64(a) / det) + 3
@@ -65,10 +80,8 @@ def _active_rows(x, y, a, b, c, o, rng):
     X, Y = np.meshgrid(px, py)
     dx = f32(x) - X
     dy = f32(y) - Y
-    t1 = (a * dx) * dx
-    t2 = (c * dy) * dy
-    power = f32(-0.5) * (t1 + t2) - (b * dx) * dy
-    G = np.exp(power.astype(np.float64)) * (1.0 + 3e-7)
+    power = _power32(a, b, c, dx, dy).astype(np.float32)
+    G = np.exp(power.astype(np.float64)) * (1.0 + EXP_ERR)
     alpha = np.minimum(0.99, np.float64(o) * G)
     act = (alpha >= 1.0 / 255.0) & ~(power > 0)
     return Y[act]
@@ -108,8 +121,8 @@ def test_row_extent_at_the_ellipse_tip():
                 x = f32(-sgn * dx * (1 - eps))
                 y = f32(-sgn * dy * (1 - eps))
                 fx, fy = f32(x - f32(0.0)), f32(y - f32(0.0))
-                power = f32(-0.5) * ((a * fx) * fx + (c * fy) * fy) - (b * fx) * fy
-                alpha = min(0.99, np.float64(o) * np.exp(np.float64(power)) * (1 + 3e-7))
+                power = _power32(a, b, c, fx, fy)
+                alpha = min(0.99, np.float64(o) * np.exp(np.float64(power)) * (1 + EXP_ERR))
                 if not (alpha >= 1.0 / 255.0) or power > 0:
                     continue
                 for log_err in (-3e-6, 3e-6):
