@@ -642,9 +642,12 @@ def main():
                 stages[name]["measured_GBps"] = mb / (ms * 1e-3) / 1e9
             if name in ktimes:  # the stage's main kernel alone
                 stages[name]["kernel_ms"] = float(np.median(ktimes[name]))
-        dom = max(stages, key=lambda k: stages[k]["ms"])
-        # roofline of the dominant stage's main kernel over its own launch time
-        kms = stages[dom].get("kernel_ms", stages[dom]["ms"])
+        # roofline of the dominant kernel: the longest of the stages' main
+        # kernels (the binning stage is a chain of kernels and has none), over
+        # its own launch time
+        dom = max((k for k in stages if "kernel_ms" in stages[k]),
+                  key=lambda k: stages[k]["kernel_ms"])
+        kms = stages[dom]["kernel_ms"]
         b, f = algorithmic_work(dom, K, P, Pv, T, W * H, S, B, Nf, Nb)
         d = roofline_entry(dom, kms, b, f)
         result["stages"] = stages

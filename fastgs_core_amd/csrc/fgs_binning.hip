@@ -1367,16 +1367,23 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
 }
 
 // Level 2e: every entry's tiles written at tile start + entries of the tile
-// in earlier chunks + rank in this chunk (list order).  Four wavefronts take
-// 128 entries each.  Per round of 64 entries, a 64x64 bit transpose gives
-// lane j the ballot of the entries having tile j; each lane then walks the
-// set bits of its own mask, fetching tile j's ballot (its rank: the entries
-// below it) and lane j's cursor (its base) with ds_bpermute.  The chunk's
-// output is staged in LDS grouped by tile and written run by run
-// (consecutive lanes, consecutive positions; wavefront w writes tiles
-// j = w mod 4); a chunk with more than kL2Stage outputs writes straight to
-// its positions.
+// in earlier chunks + rank in this chunk (list order).
+//
+// A chunk whose output fits the LDS stage (at most kL2Stage entries): four
+// wavefronts take 128 entries each.  Per round of 64 entries, a 64x64 bit
+// transpose gives lane j the ballot of the entries having tile j; each lane
+// then walks the set bits of its own mask, fetching the entry's index and
+// depth bits with ds_bpermute.  The output is staged in LDS grouped by tile
+// and written run by run (consecutive lanes, consecutive positions;
+// wavefront w writes tiles j = w mod 4).
+//
+// A larger chunk (wide Gaussians, whose masks are dense) is written tile by
+// tile: every wavefront holds the chunk's 512 entries in registers (eight per
+// lane) and takes tiles j = w mod 4; per tile and round of 64 entries, the
+// ballot of "has tile j" and the lane's rank below it place the entries at
+// consecutive positions, so each store is one contiguous run.
 constexpr int kL2Stage = 4608;
+constexpr int kL2PerLane = kL2Chunk / kWave;  // 8 entries per lane on the tile-by-tile path
 __global__ void __launch_bounds__(kL1Group)
 l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
                const uint32_t* __restrict__ st_start, const uint32_t* __restrict__ chunk_first,
@@ -1394,9 +1401,52 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
   const uint32_t s = chunk_st[c];
   const uint32_t e0 = st_start[s] + (c - chunk_first[s]) * kL2Chunk;
   const uint32_t e1 = (uint32_t)imin(imin((int)st_start[s + 1], (int)(e0 + kL2Chunk)), (int)K);
+  const int x0 = (int)(s % (uint32_t)sg.sgx) * kSt, y0 = (int)(s / (uint32_t)sg.sgx) * kSt;
+  // lane j: tile j's chunk count, staging offset and global base
+  const uint32_t cj = cnt2[(size_t)c * kWave + l];
+  const uint32_t ci = wave_incl_scan(cj);
+  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)ci, kWave - 1);
+  uint32_t gbase = 0;
+  {
+    const int x = x0 + (l % kSt), y = y0 + (l / kSt);
+    if (x < sg.gx && y < sg.gy) gbase = tile_start[y * sg.gx + x] + base2[(size_t)c * kWave + l];
+  }
+  if (total > (uint32_t)kL2Stage) {  // uniform: the tile-by-tile path
+    uint64_t em[kL2PerLane];
+    uint32_t eg[kL2PerLane], edb[kL2PerLane];
+#pragma unroll
+    for (int r = 0; r < kL2PerLane; ++r) {
+      const uint32_t e = e0 + (uint32_t)(r * kWave + l);
+      const bool valid = e < e1;
+      em[r] = valid ? masks[e] : 0ull;
+      eg[r] = valid ? list[e] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < kL2PerLane; ++r)
+      edb[r] = (em[r] != 0ull && eg[r] < (uint32_t)P) ? __float_as_uint(depths[eg[r]]) : 0xFFFFFFFFu;
+    for (int j = w; j < kWave; j += kWavesPerBlock) {
+      const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
+      if (nj == 0u) continue;
+      uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)gbase, j);
+      const uint32_t end = pos + nj;
+      const uint64_t tile = (uint64_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt)) << 32;
+#pragma unroll
+      for (int r = 0; r < kL2PerLane; ++r) {
+        const bool has = ((em[r] >> j) & 1ull) != 0ull;
+        const uint64_t bal = __ballot(has);
+        const uint32_t at = pos + (uint32_t)__popcll(bal & lanemask_lt());
+        // positions stay inside tile j's range of this chunk
+        if (has && at < end && (int64_t)at < K) {
+          keys[at] = tile | (uint64_t)edb[r];
+          point_list[at] = eg[r];
+        }
+        pos += (uint32_t)__popcll(bal);
+      }
+    }
+    return;
+  }
   const uint32_t q0 = e0 + (uint32_t)w * (kL2Chunk / kWavesPerBlock);
   const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
-  const int x0 = (int)(s % (uint32_t)sg.sgx) * kSt, y0 = (int)(s / (uint32_t)sg.sgx) * kSt;
   // this wavefront's entries per tile (lane j)
   {
     uint32_t cnt = 0;
@@ -1406,20 +1456,9 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
     }
     s_wc[w][l] = cnt;
   }
-  // lane j: tile j's chunk count, staging offset and global base
-  const uint32_t cj = cnt2[(size_t)c * kWave + l];
-  const uint32_t ci = wave_incl_scan(cj);
-  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)ci, kWave - 1);
-  const bool staged = total <= (uint32_t)kL2Stage;
-  uint32_t gbase = 0;
-  {
-    const int x = x0 + (l % kSt), y = y0 + (l / kSt);
-    if (x < sg.gx && y < sg.gy) gbase = tile_start[y * sg.gx + x] + base2[(size_t)c * kWave + l];
-  }
   const uint32_t soff = ci - cj;
-  const uint64_t my_tile = (uint64_t)((y0 + l / kSt) * sg.gx + x0 + (l % kSt)) << 32;
   __syncthreads();
-  uint32_t cur = staged ? soff : gbase;
+  uint32_t cur = soff;
   for (int k = 0; k < w; ++k) cur += s_wc[k][l];
   for (uint32_t base = q0; base < q1; base += kWave) {
     const uint32_t e = base + (uint32_t)l;
@@ -1443,22 +1482,14 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
       b &= b - 1ull;
       const uint32_t gi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)g);
       const uint32_t dbi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)db);
-      if (act) {
-        if (staged) {
-          if (at < (uint32_t)kL2Stage) {
-            s_g[at] = gi;
-            s_db[at] = dbi;
-          }
-        } else if ((int64_t)at < K) {
-          keys[at] = my_tile | (uint64_t)dbi;
-          point_list[at] = gi;
-        }
-        ++at;
+      if (act && at < (uint32_t)kL2Stage) {
+        s_g[at] = gi;
+        s_db[at] = dbi;
       }
+      if (act) ++at;
     }
     cur += (uint32_t)__popcll(bt);  // lane j: tile j's entries in this round
   }
-  if (!staged) return;  // uniform
   __syncthreads();
   for (int j = w; j < kWave; j += kWavesPerBlock) {
     const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
