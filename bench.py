@@ -635,13 +635,17 @@ def main():
         for name, v in times.items():
             ms = float(np.median(v))
             b, f = algorithmic_work(name, K, P, Pv, T, W * H, S, B, Nf, Nb)
-            stages[name] = roofline_entry(name, ms, b, f)
+            # achieved / frac over the main kernel's own time where the stage
+            # has one (the binning is a chain of kernels: its stage time)
+            kms = float(np.median(ktimes[name])) if name in ktimes else None
+            stages[name] = roofline_entry(name, kms if kms is not None else ms, b, f)
+            stages[name]["ms"] = ms
+            if kms is not None:
+                stages[name]["kernel_ms"] = kms
             mb = measured_traffic(args.config, name)
-            if mb is not None:  # FETCH_SIZE + WRITE_SIZE of the stage's kernels
+            if mb is not None:  # FETCH_SIZE + WRITE_SIZE of the stage's main kernel(s)
                 stages[name]["measured_bytes"] = mb
-                stages[name]["measured_GBps"] = mb / (ms * 1e-3) / 1e9
-            if name in ktimes:  # the stage's main kernel alone
-                stages[name]["kernel_ms"] = float(np.median(ktimes[name]))
+                stages[name]["measured_GBps"] = mb / ((kms if kms is not None else ms) * 1e-3) / 1e9
         # roofline of the dominant kernel: the longest of the stages' main
         # kernels (the binning stage is a chain of kernels and has none), over
         # its own launch time
