@@ -82,6 +82,20 @@ __device__ __forceinline__ float splat_power(float A, float B, float C, float dx
   return splat_power_rows(B * dx, (A * dx) * dx, C, dy);
 }
 
+// XCD-aware workgroup order.  The GPU hands the workgroups of a launch to its
+// 8 XCDs round robin in dispatch order (linear id L goes to XCD L % 8), and
+// each XCD has its own L2.  xcd_local_order(L, N) maps the N linear ids onto
+// logical indices so that every XCD runs one contiguous range of them:
+// workgroups that are neighbours in the logical order (and read overlapping
+// data) then run on the same XCD, at about the same time, and share its L2.
+// A bijection of [0, N).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_local_order(int L, int N) {
+  const int x = L % kXcds, k = L / kXcds;
+  const int q = N / kXcds, r = N % kXcds;
+  return x * q + (x < r ? x : r) + k;
+}
+
 // ln(x): x = m*2^e with m in [sqrt(1/2), sqrt(2)); ln(m) = 2*atanh(s),
 // s = (m-1)/(m+1), Taylor series to s^19 in double, rounded to float.
 __device__ __forceinline__ float det_logf(float x) {

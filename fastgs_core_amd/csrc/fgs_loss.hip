@@ -77,8 +77,12 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
                    float* __restrict__ dmaps, float* __restrict__ partials) {
   __shared__ float s_x[2][kRowIn];
   __shared__ float s_y[2][kRowIn];
-  const int strip = (int)blockIdx.x % a.strips_x, chunk = (int)blockIdx.x / a.strips_x;
-  const int plane = (int)blockIdx.y;
+  // strips in XCD-local order: a strip and its neighbours (whose halo rows
+  // and columns it shares) run on one XCD
+  const int nt = (int)gridDim.x;
+  const int lid = xcd_local_order((int)(blockIdx.x + blockIdx.y * gridDim.x), nt * (int)gridDim.y);
+  const int plane = lid / nt, idx = lid - plane * nt;
+  const int strip = idx % a.strips_x, chunk = idx / a.strips_x;
   const int l = (int)threadIdx.x;
   const int c0 = strip * kSW, r0 = chunk * kSH;
   const int gc = c0 + l;
@@ -167,7 +171,7 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
     l1_sum += __shfl_xor(l1_sum, o, kWave);
   }
   if (l == 0) {
-    const size_t b = (size_t)plane * gridDim.x + blockIdx.x;
+    const size_t b = (size_t)lid;  // plane * nt + idx
     partials[2 * b + 0] = ssim_sum;
     partials[2 * b + 1] = l1_sum;
   }
@@ -206,8 +210,10 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
                    const float* __restrict__ dmaps, const float* __restrict__ grad_out,
                    float* __restrict__ dimg) {
   __shared__ float s_d[2][3][kRowIn];
-  const int strip = (int)blockIdx.x % a.strips_x, chunk = (int)blockIdx.x / a.strips_x;
-  const int plane = (int)blockIdx.y;
+  const int nt = (int)gridDim.x;
+  const int lid = xcd_local_order((int)(blockIdx.x + blockIdx.y * gridDim.x), nt * (int)gridDim.y);
+  const int plane = lid / nt, idx = lid - plane * nt;
+  const int strip = idx % a.strips_x, chunk = idx / a.strips_x;
   const int l = (int)threadIdx.x;
   const int c0 = strip * kSW, r0 = chunk * kSH;
   const int gc = c0 + l;
