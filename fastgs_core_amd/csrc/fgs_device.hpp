@@ -162,20 +162,30 @@ struct HasRect : std::false_type {};
 template <typename E>
 struct HasRect<E, std::void_t<decltype(std::declval<E&>().rect(0, 0, 0, 0))>> : std::true_type {};
 
-// The walk restricted to the tile window [wx0, wx1) x [wy0, wy1): lines u
-// outside the window's range on the walked axis are not visited, and the
-// line state at the first visited line is the one the full walk reaches
-// there (the previous line's far edge, u*16, is always intersected), so every
-// emitted span is bit-identical to the full walk's.  Spans are not clipped on
-// the other axis.
+// The walk's set-up: the bounding box of the ellipse, its tile rectangle
+// (emit.rect is called with it) and the swept axis.  Axis 0 is the swept one
+// after the swap (is_y: the walk runs over tile rows).  empty: a degenerate
+// conic or an empty rectangle (the walk touches nothing).
+struct WalkSetup {
+  float disc, t;
+  float am1, aM1;                  // the bounding box's argmin / argmax on the other axis
+  float bmin0, bmax0, bmin1, bmax1;
+  int rmin0, rmax0, rmin1, rmax1;  // tile rectangle, axis 0 swept
+  bool is_y;
+  bool empty;
+};
+
 template <typename Emit>
-__device__ __forceinline__ uint32_t tiles_walk_window(float px, float py, float4 co, int gx, int gy,
-                                                      float mult, int wx0, int wx1, int wy0,
-                                                      int wy1, Emit&& emit) {
-  const float disc = co.y * co.y - co.x * co.z;
-  if (co.x <= 0.0f || co.z <= 0.0f || disc >= 0.0f) return 0u;
+__device__ __forceinline__ WalkSetup walk_setup(float px, float py, float4 co, int gx, int gy,
+                                                float mult, Emit& emit) {
+  WalkSetup w;
+  w.empty = true;
+  w.disc = co.y * co.y - co.x * co.z;
+  if (co.x <= 0.0f || co.z <= 0.0f || w.disc >= 0.0f) return w;
+  const float disc = w.disc;
   float t = 2.0f * det_logf(co.w * 255.0f);
   t = mult * t;
+  w.t = t;
   float x_term = __builtin_sqrtf(-(co.y * co.y * t) / (disc * co.x));
   x_term = (co.y < 0.0f) ? x_term : -x_term;
   float y_term = __builtin_sqrtf(-(co.y * co.y * t) / (disc * co.z));
@@ -198,7 +208,7 @@ __device__ __forceinline__ uint32_t tiles_walk_window(float px, float py, float4
   int rmax1 = imax(0, imin(gy, f2i(bmax1 / 16.0f + 1.0f)));
   const int y_span = rmax1 - rmin1;
   const int x_span = rmax0 - rmin0;
-  if (y_span * x_span == 0) return 0u;
+  if (y_span * x_span == 0) return w;
   if constexpr (HasRect<std::remove_reference_t<Emit>>::value) emit.rect(rmin0, rmax0, rmin1, rmax1);
   const bool is_y = y_span < x_span;
   if (is_y) {
@@ -211,46 +221,68 @@ __device__ __forceinline__ uint32_t tiles_walk_window(float px, float py, float4
     tf = am0; am0 = am1; am1 = tf;
     tf = aM0; aM0 = aM1; aM1 = tf;
   }
-  int u0 = rmin0, u1 = rmax0;
-  if (is_y) {
-    u0 = imax(u0, wy0);
-    u1 = imin(u1, wy1);
-  } else {
-    u0 = imax(u0, wx0);
-    u1 = imin(u1, wx1);
-  }
+  w.am1 = am1;
+  w.aM1 = aM1;
+  w.bmin0 = bmin0;
+  w.bmax0 = bmax0;
+  w.bmin1 = bmin1;
+  w.bmax1 = bmax1;
+  w.rmin0 = rmin0;
+  w.rmax0 = rmax0;
+  w.rmin1 = rmin1;
+  w.rmax1 = rmax1;
+  w.is_y = is_y;
+  w.empty = false;
+  return w;
+}
+
+// One line's tile interval [vmin, vmax) on the other axis, from the line's
+// near-edge intersection il and far-edge intersection iM.
+__device__ __forceinline__ void walk_line_span(const WalkSetup& w, float min_line, float max_line,
+                                               float il0, float il1, float iM0, float iM1,
+                                               int& vmin, int& vmax) {
+  float e_min, e_max;
+  if (min_line <= w.am1 && w.am1 < max_line)
+    e_min = w.bmin1;
+  else
+    e_min = fminf(il0, iM0);
+  if (min_line <= w.aM1 && w.aM1 < max_line)
+    e_max = w.bmax1;
+  else
+    e_max = fmaxf(il1, iM1);
+  vmin = imax(w.rmin1, imin(w.rmax1, f2i(e_min / 16.0f)));
+  vmax = imin(w.rmax1, imax(w.rmin1, f2i(e_max / 16.0f + 1.0f)));
+}
+
+// The line loop of the walk over lines [u0, u1) of the swept axis (u0 >=
+// rmin0).  The line state at u0 is the one the full walk reaches there: the
+// previous line's far edge u0*16 is always intersected.
+template <typename Emit>
+__device__ __forceinline__ uint32_t walk_lines(const WalkSetup& w, float px, float py, float4 co,
+                                               int u0, int u1, Emit&& emit) {
   uint32_t count = 0;
-  float il0, il1;            // intersect_min_line
-  float iM0 = bmax1, iM1 = bmin1;  // intersect_max_line
+  float il0, il1;                      // intersect_min_line
+  float iM0 = w.bmax1, iM1 = w.bmin1;  // intersect_max_line
   float min_line = (float)u0 * 16.0f;
-  if (u0 > rmin0) {
+  if (u0 > w.rmin0) {
     // the full walk's line u0-1 intersected its far edge u0*16 (u0*16 <= bmax0)
-    ellipse_isect(co, disc, t, px, py, is_y, min_line, il0, il1);
+    ellipse_isect(co, w.disc, w.t, px, py, w.is_y, min_line, il0, il1);
     iM0 = il0;
     iM1 = il1;
-  } else if (bmin0 <= min_line) {
-    ellipse_isect(co, disc, t, px, py, is_y, (float)rmin0 * 16.0f, il0, il1);
+  } else if (w.bmin0 <= min_line) {
+    ellipse_isect(co, w.disc, w.t, px, py, w.is_y, (float)w.rmin0 * 16.0f, il0, il1);
   } else {
     il0 = iM0;
     il1 = iM1;
   }
   for (int u = u0; u < u1; ++u) {
     const float max_line = min_line + 16.0f;
-    if (max_line <= bmax0) ellipse_isect(co, disc, t, px, py, is_y, max_line, iM0, iM1);
-    float e_min, e_max;
-    if (min_line <= am1 && am1 < max_line)
-      e_min = bmin1;
-    else
-      e_min = fminf(il0, iM0);
-    if (min_line <= aM1 && aM1 < max_line)
-      e_max = bmax1;
-    else
-      e_max = fmaxf(il1, iM1);
-    const int min_tile_v = imax(rmin1, imin(rmax1, f2i(e_min / 16.0f)));
-    const int max_tile_v = imin(rmax1, imax(rmin1, f2i(e_max / 16.0f + 1.0f)));
+    if (max_line <= w.bmax0) ellipse_isect(co, w.disc, w.t, px, py, w.is_y, max_line, iM0, iM1);
+    int min_tile_v, max_tile_v;
+    walk_line_span(w, min_line, max_line, il0, il1, iM0, iM1, min_tile_v, max_tile_v);
     if (max_tile_v > min_tile_v) {
       count += (uint32_t)(max_tile_v - min_tile_v);
-      emit(u, min_tile_v, max_tile_v, is_y);
+      emit(u, min_tile_v, max_tile_v, w.is_y);
     }
     il0 = iM0;
     il1 = iM1;
@@ -259,10 +291,97 @@ __device__ __forceinline__ uint32_t tiles_walk_window(float px, float py, float4
   return count;
 }
 
+// The walk restricted to the tile window [wx0, wx1) x [wy0, wy1): lines u
+// outside the window's range on the walked axis are not visited, and the
+// line state at the first visited line is the one the full walk reaches
+// there (the previous line's far edge, u*16, is always intersected), so every
+// emitted span is bit-identical to the full walk's.  Spans are not clipped on
+// the other axis.
+template <typename Emit>
+__device__ __forceinline__ uint32_t tiles_walk_window(float px, float py, float4 co, int gx, int gy,
+                                                      float mult, int wx0, int wx1, int wy0,
+                                                      int wy1, Emit&& emit) {
+  const WalkSetup w = walk_setup(px, py, co, gx, gy, mult, emit);
+  if (w.empty) return 0u;
+  int u0 = w.rmin0, u1 = w.rmax0;
+  if (w.is_y) {
+    u0 = imax(u0, wy0);
+    u1 = imin(u1, wy1);
+  } else {
+    u0 = imax(u0, wx0);
+    u1 = imin(u1, wx1);
+  }
+  return walk_lines(w, px, py, co, u0, u1, emit);
+}
+
 template <typename Emit>
 __device__ __forceinline__ uint32_t tiles_walk(float px, float py, float4 co, int gx, int gy,
                                                float mult, Emit&& emit) {
   return tiles_walk_window(px, py, co, gx, gy, mult, 0, gx, 0, gy, emit);
+}
+
+// The full walk of one Gaussian by a whole wavefront: every lane passes the
+// same (px, py, co); lane l takes lines rmin0 + l, rmin0 + l + 64, ... and
+// computes each line's span as walk_lines does.  The state walk_lines carries
+// from line to line is rebuilt per line: the far edge (u+1)*16 is intersected
+// while it is at most bmax0 (a prefix of the lines), later lines keep the
+// last such intersection, and a line's near-edge state is the previous line's
+// far-edge state (the lane below, or the previous round's last lane).  Each
+// lane's spans go to its own emit; the return value is the wavefront's total
+// (the same on every lane).  Called by all 64 lanes with uniform inputs.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, kWave);
+  return v;
+}
+
+template <typename Emit>
+__device__ __forceinline__ uint32_t tiles_walk_wave(float px, float py, float4 co, int gx, int gy,
+                                                    float mult, Emit&& emit) {
+  const WalkSetup w = walk_setup(px, py, co, gx, gy, mult, emit);
+  if (w.empty) return 0u;  // uniform
+  const int u0 = w.rmin0, u1 = w.rmax0;
+  const int l = (int)(threadIdx.x & (kWave - 1));
+  // far-edge state before the first line, and the near-edge state of line u0
+  float last0 = w.bmax1, last1 = w.bmin1;
+  float prev0 = last0, prev1 = last1;
+  if (w.bmin0 <= (float)u0 * 16.0f)
+    ellipse_isect(co, w.disc, w.t, px, py, w.is_y, (float)w.rmin0 * 16.0f, prev0, prev1);
+  uint32_t count = 0;
+  for (int base = u0; base < u1; base += kWave) {
+    const int u = base + l;
+    const bool in = u < u1;
+    const float min_line = (float)u * 16.0f;
+    const float max_line = min_line + 16.0f;
+    const bool far = in && max_line <= w.bmax0;
+    float iM0 = 0.0f, iM1 = 0.0f;
+    if (far) ellipse_isect(co, w.disc, w.t, px, py, w.is_y, max_line, iM0, iM1);
+    const int nf = __popcll(__ballot(far));  // the far lanes are lanes [0, nf)
+    if (nf > 0) {
+      last0 = __shfl(iM0, nf - 1, kWave);
+      last1 = __shfl(iM1, nf - 1, kWave);
+    }
+    if (!far) {
+      iM0 = last0;
+      iM1 = last1;
+    }
+    float il0 = __shfl_up(iM0, 1, kWave), il1 = __shfl_up(iM1, 1, kWave);
+    if (l == 0) {
+      il0 = prev0;
+      il1 = prev1;
+    }
+    if (in) {
+      int vmin, vmax;
+      walk_line_span(w, min_line, max_line, il0, il1, iM0, iM1, vmin, vmax);
+      if (vmax > vmin) {
+        count += (uint32_t)(vmax - vmin);
+        emit(u, vmin, vmax, w.is_y);
+      }
+    }
+    prev0 = __shfl(iM0, kWave - 1, kWave);
+    prev1 = __shfl(iM1, kWave - 1, kWave);
+  }
+  return wave_sum_u32(count);
 }
 
 struct NoEmit {
@@ -377,6 +496,19 @@ struct EmitStRecord {
   __device__ __forceinline__ uint32_t word() const {
     if (fits) return (uint32_t)bx | ((uint32_t)by << 12) | kStRecFits;
     return set_ok ? kStRecSet : 0u;
+  }
+  // OR of the four words over the wavefront (after tiles_walk_wave)
+  __device__ __forceinline__ void wave_or() {
+    uint32_t v[8] = {(uint32_t)m0, (uint32_t)(m0 >> 32), (uint32_t)m1, (uint32_t)(m1 >> 32),
+                     (uint32_t)m2, (uint32_t)(m2 >> 32), (uint32_t)m3, (uint32_t)(m3 >> 32)};
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] |= (uint32_t)__shfl_xor((int)v[k], o, kWave);
+    m0 = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+    m1 = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
+    m2 = (uint64_t)v[4] | ((uint64_t)v[5] << 32);
+    m3 = (uint64_t)v[6] | ((uint64_t)v[7] << 32);
   }
 };
 

@@ -163,6 +163,11 @@ __device__ __forceinline__ void store_sh_rows(const float* __restrict__ s_sh, in
   if (t < n) dst[t] = s_sh[t];
 }
 
+// Tile walks longer than this many lines are taken by the whole wavefront
+// (tiles_walk_wave), so one wide Gaussian does not hold its 63 neighbours
+// for its full walk.
+constexpr int kWaveWalkLines = 16;
+
 // kRow = 0: SH rows are read from global memory where needed; kRow > 0: the
 // rows (kRow = 3 * max_sh_coeffs floats) of the block are staged through LDS.
 template <int kRow>
@@ -174,8 +179,10 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   const int row = kRow > 0 ? kRow : prm.max_sh_coeffs * 3;
   if constexpr (kRow > 0) stage_sh_rows<kRow>(io.sh, prm.P, s_sh);
   const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (i >= prm.P) return;
-  const size_t I = (size_t)i;
+  // every lane stays to the end: the wide Gaussians' walks below take the
+  // whole wavefront
+  const bool live = i < prm.P;
+  const size_t I = live ? (size_t)i : 0;
   const float mx = io.means3d[3 * I + 0];
   const float my = io.means3d[3 * I + 1];
   const float mz = io.means3d[3 * I + 2];
@@ -189,11 +196,17 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   float4 vsp = make_float4(0.f, 0.f, 0.f, 0.f);
   float c3[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   EmitStRecord st(prm.grid_x, prm.grid_y);  // super-tile record, built by the tile walk
+  // a walk longer than kWaveWalkLines lines is left to the wavefront (below):
+  // its lane keeps the walk's inputs and takes the rest of the path as if the
+  // Gaussian touched a tile, undone there if it touches none
+  bool wide = false;
+  float wpx = 0.f, wpy = 0.f;
+  float4 wco = make_float4(0.f, 0.f, 0.f, 0.f);
   // p_view (in_frustum, :96-115)
   const float pv0 = V.m[0] * mx + V.m[4] * my + V.m[8] * mz + V.m[12];
   const float pv1 = V.m[1] * mx + V.m[5] * my + V.m[9] * mz + V.m[13];
   const float pv2 = V.m[2] * mx + V.m[6] * my + V.m[10] * mz + V.m[14];
-  if (pv2 > 0.2f) {
+  if (live && pv2 > 0.2f) {
     const Mat16 Pm = load_mat(io.projmatrix);
     const float ph0 = Pm.m[0] * mx + Pm.m[4] * my + Pm.m[8] * mz + Pm.m[12];
     const float ph1 = Pm.m[1] * mx + Pm.m[5] * my + Pm.m[9] * mz + Pm.m[13];
@@ -224,7 +237,19 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
       const float px = ((pp0 + 1.0f) * (float)prm.image_width - 1.0f) * 0.5f;
       const float py = ((pp1 + 1.0f) * (float)prm.image_height - 1.0f) * 0.5f;
       const float4 con_o = make_float4(conic0, conic1, conic2, io.opacities[I]);
-      const uint32_t n = tiles_walk(px, py, con_o, prm.grid_x, prm.grid_y, prm.mult, st);
+      const WalkSetup ws = walk_setup(px, py, con_o, prm.grid_x, prm.grid_y, prm.mult, st);
+      uint32_t n = 0u;
+      if (!ws.empty) {
+        if (ws.rmax0 - ws.rmin0 > kWaveWalkLines) {
+          wide = true;
+          wpx = px;
+          wpy = py;
+          wco = con_o;
+          n = 1u;  // provisional
+        } else {
+          n = walk_lines(ws, px, py, con_o, ws.rmin0, ws.rmax0, st);
+        }
+      }
       if (n != 0u) {
         if (prm.use_colors_precomp) {
 #pragma unroll
@@ -273,6 +298,33 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
       }
     }
   }
+  // the wide Gaussians of this wavefront, one at a time by all its lanes
+  for (uint64_t wm = __ballot(wide); wm != 0ull; wm &= wm - 1ull) {  // uniform
+    const int src = __builtin_ctzll(wm);
+    const float sx = __shfl(wpx, src, kWave), sy = __shfl(wpy, src, kWave);
+    const float4 sco = make_float4(__shfl(wco.x, src, kWave), __shfl(wco.y, src, kWave),
+                                   __shfl(wco.z, src, kWave), __shfl(wco.w, src, kWave));
+    EmitStRecord sw(prm.grid_x, prm.grid_y);
+    const uint32_t nw = tiles_walk_wave(sx, sy, sco, prm.grid_x, prm.grid_y, prm.mult, sw);
+    sw.wave_or();
+    if (lane_id() == src) {
+      st = sw;
+      cnt = nw;
+      if (nw == 0u) {  // it touches no tile: the outputs of a Gaussian that touches none
+        radius = 0;
+        depth = 0.f;
+        xy0 = xy1 = 0.f;
+        co = make_float4(0.f, 0.f, 0.f, 0.f);
+        vsp = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          col[c] = 0.f;
+          clamp[c] = 0;
+        }
+      }
+    }
+  }
+  if (!live) return;
   io.radii[I] = radius;
   io.tiles_touched[I] = cnt;
   io.depths[I] = depth;
