@@ -326,7 +326,7 @@ __device__ __forceinline__ void wave_reduce_terms(float (&v)[kGradTerms], float*
 template <int NCH, bool kSafe>
 __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, const float4 cu,
                                                 const float4 h, const int jj, const float pxf,
-                                                const float pyf0, const float ty0,
+                                                const float pyf0, const uint32_t reach,
                                                 const int (&nc)[4], const int (&nc_max)[4],
                                                 float (&T)[4],
                                                 float (&SdL)[4], const float (&dL)[4][3],
@@ -341,8 +341,7 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     if (jj >= nc_max[k]) continue;  // every pixel of the strip ends before this splat
-    const float strip_lo = ty0 + (float)(4 * k);
-    if (!(cu.y >= strip_lo && cu.x <= strip_lo + 3.0f)) continue;  // wave-uniform
+    if (!((reach >> k) & 1u)) continue;  // outside the splat's rows (scalar test)
     const float dy = a.y - (pyf0 + (float)(4 * k));
     const float power = splat_power_rows(Bdx, Adxdx, Cc, dy);
     const float G = blend_expf(power);
@@ -399,7 +398,7 @@ template <int NCH, bool kSafe>
 __device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, const float4* s_h,
                                           const float4* s_cull, float* s_rec, const int lo,
                                           const int cnt, const int l, const float pxf,
-                                          const float pyf0, const float ty0, const int (&nc)[4],
+                                          const float pyf0, const int (&nc)[4],
                                           const int (&nc_max)[4], float (&T)[4], float (&SdL)[4],
                                           const float (&dL)[4][3]) {
   for (int j = cnt - 1; j >= 0; --j) {
@@ -407,10 +406,13 @@ __device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, 
     const float4 b = s_b[j];
     const float4 hh = s_h[j];
     const float4 cu = s_cull[j];
+    // strips inside the splat's row extent, one bit each (the same for every
+    // lane: moved to a scalar register so the strip tests are scalar)
+    const uint32_t reach = __builtin_amdgcn_readfirstlane(__float_as_uint(cu.x));
     float v[kGradTerms];
 #pragma unroll
     for (int k = 0; k < kGradTerms; ++k) v[k] = -0.0f;
-    if (bwd_splat_terms<NCH, kSafe>(a, b, cu, hh, lo + j, pxf, pyf0, ty0, nc, nc_max, T, SdL, dL,
+    if (bwd_splat_terms<NCH, kSafe>(a, b, cu, hh, lo + j, pxf, pyf0, reach, nc, nc_max, T, SdL, dL,
                                     v))
       wave_reduce_terms(v, s_rec + j * kRec, l);
   }
@@ -424,7 +426,7 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
   __shared__ float4 s_a[kBwdBatch];
   __shared__ float4 s_b[kBwdBatch];
   __shared__ float4 s_h[kBwdBatch];     // conic scaled by (W/2, H/2)
-  __shared__ float4 s_cull[kBwdBatch];  // (row_lo, row_hi, -opacity/2, colour 3)
+  __shared__ float4 s_cull[kBwdBatch];  // (strips reached as bits, -, -opacity/2, colour 3)
   __shared__ uint32_t s_g[kBwdBatch];
   __shared__ float s_rec[kBwdBatch * kRec];
   const int tile = io.tile_order ? (int)io.tile_order[blockIdx.x] : (int)blockIdx.x;
@@ -499,7 +501,14 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
                        __builtin_isfinite(a.z) && __builtin_isfinite(a.w) &&
                        __builtin_isfinite(b.x) && __builtin_isfinite(b.y) &&
                        __builtin_isfinite(b.z) && __builtin_isfinite(b.w) && __builtin_isfinite(c);
-      s_cull[l] = make_float4(cu.x, cu.y, -0.5f * b.y, c);
+      // the strips k (rows ty0 + 4k .. + 3) the row extent reaches
+      uint32_t reach = 0u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float strip_lo = ty0 + (float)(4 * k);
+        if (cu.y >= strip_lo && cu.x <= strip_lo + 3.0f) reach |= 1u << k;
+      }
+      s_cull[l] = make_float4(__uint_as_float(reach), 0.0f, -0.5f * b.y, c);
     }
 #pragma unroll
     for (int i = 0; i < kRec; ++i) s_rec[i * kBwdBatch + l] = 0.0f;
@@ -512,10 +521,10 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
     const bool fast = tile_finite && __ballot(!ok) == 0ull;
     __syncthreads();
     if (fast)
-      bwd_batch<NCH, false>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, nc_max,
+      bwd_batch<NCH, false>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, nc, nc_max,
                             T, SdL, dL);
     else
-      bwd_batch<NCH, true>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, ty0, nc, nc_max,
+      bwd_batch<NCH, true>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, nc, nc_max,
                            T, SdL, dL);
     __syncthreads();
     // Flush: item q = (splat q/12, term q%12), so the lanes of one atomic
