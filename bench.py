@@ -529,14 +529,22 @@ def main():
     metric_map = torch.zeros(W * H, dtype=torch.int32, device=dev)
     win = gaussian_window(torch).to(dev)
 
+    # the viewspace placeholder (zeros whose gradient is the viewspace
+    # gradient) and the loss's unit seed are made once: a zero fill and a one
+    # fill per step would only repeat the same values
+    vsp_train = torch.zeros((P, 4), device=dev, requires_grad=True)
+    vsp_eval = torch.zeros((P, 4), device=dev)
+    seed = torch.ones((), device=dev)
+
     def render(i, train=True, count_iterations=False):
         c = cam_t[i % len(cam_t)]
-        vsp = torch.zeros((P, 4), device=dev, requires_grad=train)
-        # activations (sigmoid / exp / quaternion normalise): one fused kernel each way
-        scales, rots, opac = fastgs_core_amd.activate(raw["log_scales"], raw["quats"],
-                                                      raw["opacity_logits"])
-        inputs = {"means3d": raw["means3d"], "scales": scales, "rotations": rots,
-                  "opacities": opac, "dc": raw["dc"], "sh": raw["sh"], "background": background,
+        vsp = vsp_train if train else vsp_eval
+        vsp.grad = None
+        # the raw parameters: the activations (sigmoid / exp / quaternion
+        # normalise) run inside, their backward fused into the preprocess backward
+        inputs = {"means3d": raw["means3d"], "log_scales": raw["log_scales"],
+                  "raw_rotations": raw["quats"], "opacity_logits": raw["opacity_logits"],
+                  "dc": raw["dc"], "sh": raw["sh"], "background": background,
                   "metric_map": metric_map, "viewmatrix": c["viewmatrix"],
                   "projmatrix": c["projmatrix"], "campos": c["campos"], "viewspace_points": vsp}
         out = fastgs_core.rasterize_gaussians_forward(inputs, W, H, 16, 16, c["tan_fovx"],
@@ -551,7 +559,7 @@ def main():
         img = out["out_color"].view(3, H, W)
         tgt = targets[i % len(targets)]
         loss = fastgs_core_amd.l1_ssim_loss(img, tgt, 1.0, 0.2)
-        loss.backward()
+        loss.backward(seed)
         return out
 
     if args.calibrate:

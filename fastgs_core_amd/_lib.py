@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 class PreprocessParams(Structure):
@@ -45,7 +45,8 @@ class PreprocessBwdIO(Structure):
         "cov3d_precomp", "cov3d_fwd", "radii", "clamped", "dL_dxys", "dL_drgb",
         "dL_dconic_opacity", "dL_dcov3d", "dL_dviewspace_out", "dL_dmeans3d", "dL_ddc", "dL_dsh",
         "dL_dcolors_precomp", "dL_dopacities", "dL_dscales", "dL_drotations",
-        "dL_dviewspace_in")]
+        "dL_dviewspace_in", "quats_raw", "act_opacities", "dL_dlog_scales", "dL_dquats",
+        "dL_dlogits")]
 
 
 class BinningIO(Structure):

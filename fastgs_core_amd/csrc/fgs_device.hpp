@@ -82,6 +82,18 @@ __device__ __forceinline__ float splat_power(float A, float B, float C, float dx
   return splat_power_rows(B * dx, (A * dx) * dx, C, dy);
 }
 
+// Gradient through the training scripts' rotation activation
+// r = q / (|q| + 1e-8): dq = g/d - q (q.g) / (d^2 |q|), d = |q| + 1e-8 (the
+// second term is 0 at q = 0).  Shared by the activation backward and the
+// preprocess backward's fused form, so the two agree bit for bit.
+__device__ __forceinline__ float4 quat_normalize_grad(float4 q, float4 g) {
+  const float n = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+  const float d = n + 1e-8f;
+  const float qg = q.x * g.x + q.y * g.y + q.z * g.z + q.w * g.w;
+  const float c = n > 0.0f ? qg / (d * d * n) : 0.0f;
+  return make_float4(g.x / d - q.x * c, g.y / d - q.y * c, g.z / d - q.z * c, g.w / d - q.w * c);
+}
+
 // XCD-aware workgroup order.  The GPU hands the workgroups of a launch to its
 // 8 XCDs round robin in dispatch order (linear id L goes to XCD L % 8), and
 // each XCD has its own L2.  xcd_local_order(L, N) maps the N linear ids onto

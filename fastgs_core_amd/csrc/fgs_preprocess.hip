@@ -637,12 +637,26 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
   if (io.dL_dcolors_precomp)
 #pragma unroll
     for (int k = 0; k < 3; ++k) io.dL_dcolors_precomp[3 * I + k] = dcol[k];
-  io.dL_dopacities[I] = dop;
+  if (io.dL_dopacities) io.dL_dopacities[I] = dop;
   if (io.dL_dscales)
 #pragma unroll
     for (int k = 0; k < 3; ++k) io.dL_dscales[3 * I + k] = dsc[k];
   if (io.dL_drotations)
     *reinterpret_cast<float4*>(io.dL_drotations + 4 * I) = make_float4(dq[0], dq[1], dq[2], dq[3]);
+  // the activations' backward, with the operations of activations_bwd_kernel
+  // (fgs_train.hip), so the fused and the separate forms agree bit for bit
+  if (io.dL_dlogits) {
+    const float o = io.act_opacities[I];
+    io.dL_dlogits[I] = dop * (1.0f - o) * o;
+  }
+  if (io.dL_dlog_scales)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) io.dL_dlog_scales[3 * I + k] = dsc[k] * io.scales[3 * I + k];
+  if (io.dL_dquats) {
+    const float4 q = *reinterpret_cast<const float4*>(io.quats_raw + 4 * I);
+    *reinterpret_cast<float4*>(io.dL_dquats + 4 * I) =
+        quat_normalize_grad(q, make_float4(dq[0], dq[1], dq[2], dq[3]));
+  }
   *reinterpret_cast<float4*>(io.dL_dviewspace_in + 4 * I) = dvsp;
   if (!kStaged && ds) {
     for (int k = sh_written * 3; k < msh * 3; ++k) ds[k] = 0.0f;
@@ -724,13 +738,19 @@ extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
   if (p->P < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: P < 0");
   if (p->P == 0) return FGS_OK;
   if (!io->means3d || !io->viewmatrix || !io->projmatrix || !io->campos || !io->radii ||
-      !io->clamped || !io->dL_dmeans3d || !io->dL_dopacities || !io->dL_dviewspace_in)
+      !io->clamped || !io->dL_dmeans3d || !io->dL_dviewspace_in ||
+      !(io->dL_dopacities || (io->dL_dlogits && io->act_opacities)))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing tensor");
   if (p->use_cov3d_precomp ? !io->cov3d_precomp
                            : (!io->cov3d_fwd || !io->scales || !io->rotations))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing geometry tensors");
   if (!p->use_colors_precomp && p->degree > 0 && p->max_sh_coeffs >= 3 && (!io->sh || !io->dL_dsh))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing sh tensors");
+  if ((io->dL_dlogits && !io->act_opacities) || (io->dL_dquats && !io->quats_raw) ||
+      ((io->dL_dlog_scales || io->dL_dquats) && p->use_cov3d_precomp))
+    return set_error(FGS_ERR_INVALID_ARGUMENT,
+                     "fgs_preprocess_bwd: fused activation gradients need act_opacities, "
+                     "quats_raw and the scale/rotation path");
   const float fx = 0.5f * (float)p->image_width / fmaxf(p->tan_fovx, 1e-6f);
   const float fy = 0.5f * (float)p->image_height / fmaxf(p->tan_fovy, 1e-6f);
   const unsigned blocks = (unsigned)((p->P + 255) / 256);

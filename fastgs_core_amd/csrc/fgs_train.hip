@@ -64,12 +64,7 @@ activations_bwd_kernel(int32_t P, const float* __restrict__ quats,
     const float4 q = *reinterpret_cast<const float4*>(quats + 4 * (size_t)i);
     float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
     if (d_rotations) g = *reinterpret_cast<const float4*>(d_rotations + 4 * (size_t)i);
-    const float n = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
-    const float d = n + 1e-8f;
-    const float qg = q.x * g.x + q.y * g.y + q.z * g.z + q.w * g.w;
-    const float c = n > 0.0f ? qg / (d * d * n) : 0.0f;
-    *reinterpret_cast<float4*>(d_quats + 4 * (size_t)i) =
-        make_float4(g.x / d - q.x * c, g.y / d - q.y * c, g.z / d - q.z * c, g.w / d - q.w * c);
+    *reinterpret_cast<float4*>(d_quats + 4 * (size_t)i) = quat_normalize_grad(q, g);
   }
   if (d_logits) {
     const float o = opacities[i];

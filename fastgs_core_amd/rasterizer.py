@@ -165,11 +165,22 @@ class _Preprocess(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, cfg, means3d, dc, sh, colors_precomp, opacities, scales, rotations,
-                cov3d_precomp, viewmatrix, projmatrix, campos, viewspace_in):
+                cov3d_precomp, viewmatrix, projmatrix, campos, viewspace_in, log_scales=None,
+                raw_rotations=None, opacity_logits=None):
         lib = _lib.load()
         dev = means3d.device
         P = means3d.shape[0]
         f32 = dict(dtype=torch.float32, device=dev)
+        if cfg.get("raw"):
+            # the training scripts' activations applied here (fgs_activations_fwd);
+            # their backward is fused into the preprocess backward
+            scales = torch.empty((P, 3), **f32)
+            rotations = torch.empty((P, 4), **f32)
+            opacities = torch.empty(P, **f32)
+            if P > 0:
+                _lib.check(lib.fgs_activations_fwd(P, _p(log_scales), _p(raw_rotations),
+                                                   _p(opacity_logits), _p(scales), _p(rotations),
+                                                   _p(opacities), _stream(dev)))
         radii = torch.empty(P, dtype=torch.int32, device=dev)
         xys = torch.empty((P, 2), **f32)
         depths = torch.empty(P, **f32)
@@ -193,10 +204,11 @@ class _Preprocess(torch.autograd.Function):
                 _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io),
                                                   _stream(dev)))
         ctx.cfg = dict(cfg, st_base=None, st_masks=None)  # the records are forward-only
-        ctx.opacity_shape = opacities.shape
+        ctx.opacity_shape = (opacity_logits if cfg.get("raw") else opacities).shape
         ctx.sh_shape = None if sh is None else sh.shape
         ctx.save_for_backward(means3d, sh, scales, rotations, cov3d_precomp, viewmatrix,
-                              projmatrix, campos, cov3d, radii, clamped)
+                              projmatrix, campos, cov3d, radii, clamped, raw_rotations,
+                              opacities if cfg.get("raw") else None)
         ctx.mark_non_differentiable(radii, tiles, clamped)
         # outputs the loss does not reach arrive as None (no zero tensors)
         ctx.set_materialize_grads(False)
@@ -207,8 +219,9 @@ class _Preprocess(torch.autograd.Function):
                  g_vsp):
         lib = _lib.load()
         (means3d, sh, scales, rotations, cov3d_precomp, viewmatrix, projmatrix, campos, cov3d,
-         radii, clamped) = ctx.saved_tensors
+         radii, clamped, raw_rotations, act_opacities) = ctx.saved_tensors
         cfg = ctx.cfg
+        raw = bool(cfg.get("raw"))
         dev = means3d.device
         P = means3d.shape[0]
         f32 = dict(dtype=torch.float32, device=dev)
@@ -219,6 +232,8 @@ class _Preprocess(torch.autograd.Function):
         d_dc = torch.empty((P, 3), **f32) if sh_path else None
         d_sh = torch.empty(ctx.sh_shape, **f32) if (sh_path and sh is not None) else None
         d_col = torch.empty((P, 3), **f32) if not sh_path else None
+        # raw: the gradients of log-scales, raw rotations and opacity logits
+        # instead of those of the activated parameters
         d_opac = torch.empty(P, **f32)
         d_scales = torch.empty((P, 3), **f32) if not cfg["use_cov"] else None
         d_rot = torch.empty((P, 4), **f32) if not cfg["use_cov"] else None
@@ -231,7 +246,10 @@ class _Preprocess(torch.autograd.Function):
             _p(means3d), _p(scales), _p(rotations), _p(viewmatrix), _p(projmatrix), _p(campos),
             _p(sh), _p(cov3d_precomp), _p(cov3d), _p(radii), _p(clamped), _p(g_xys), _p(g_rgb),
             _p(g_conic), _p(g_cov3d), _p(g_vsp), _p(d_means3d), _p(d_dc), _p(d_sh), _p(d_col),
-            _p(d_opac), _p(d_scales), _p(d_rot), _p(d_vsp))
+            None if raw else _p(d_opac), None if raw else _p(d_scales),
+            None if raw else _p(d_rot), _p(d_vsp), _p(raw_rotations), _p(act_opacities),
+            _p(d_scales) if raw else None, _p(d_rot) if raw else None,
+            _p(d_opac) if raw else None)
         if P > 0:
             with _stage("preprocess_bwd"):
                 _lib.check(lib.fgs_preprocess_bwd(ctypes.byref(prm), ctypes.byref(io),
@@ -239,11 +257,13 @@ class _Preprocess(torch.autograd.Function):
         need = ctx.needs_input_grad
         d_cov_pre = torch.zeros_like(cov3d_precomp) if (cov3d_precomp is not None and need[8]) \
             else None
-        return (None, d_means3d, d_dc, d_sh, d_col, d_opac.view(ctx.opacity_shape), d_scales,
-                d_rot, d_cov_pre,
+        d_opac = d_opac.view(ctx.opacity_shape)
+        act = (None, None, None) if raw else (d_opac, d_scales, d_rot)
+        rawg = (d_scales, d_rot, d_opac) if raw else (None, None, None)
+        return (None, d_means3d, d_dc, d_sh, d_col, act[0], act[1], act[2], d_cov_pre,
                 torch.zeros_like(viewmatrix) if need[9] else None,
                 torch.zeros_like(projmatrix) if need[10] else None,
-                torch.zeros_like(campos) if need[11] else None, d_vsp)
+                torch.zeros_like(campos) if need[11] else None, d_vsp) + rawg
 
 
 class _Rasterize(torch.autograd.Function):
@@ -482,9 +502,20 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
             raise RuntimeError(f"{fn} missing required input tensor: {k}")
         return inputs[k]
 
+    # rasterize_gaussians also takes the raw parameters of a training step in
+    # place of the activated ones (no reference counterpart): the activations
+    # run inside and their backward is fused into the preprocess backward
+    raw = names is _RG_NAMES and all(_size(inputs.get(k)) != 0 for k in _RAW_KEYS)
+    if raw and any(_size(inputs.get(k)) != 0
+                   for k in ("opacities", "scales", "rotations", "cov3d_precomp")):
+        raise RuntimeError(f"{fn} takes either opacities/scales/rotations or the raw "
+                           f"{'/'.join(_RAW_KEYS)}, not both")
     for k in names["required"]:
-        req(k)
-    col, has_col, has_cov = _colour_and_geometry(inputs, fn, names["col_keys"], names["rot"])
+        if not (raw and k == "opacities"):
+            req(k)
+    geo = dict(inputs, scales=inputs["log_scales"], rotations=inputs["raw_rotations"]) if raw \
+        else inputs
+    col, has_col, has_cov = _colour_and_geometry(geo, fn, names["col_keys"], names["rot"])
     _check_blocks(block_x, block_y)
     sh_nd, sh_shape = _ndim_shape(inputs.get("sh"))
     max_sh = int(sh_shape[1]) if sh_nd >= 2 else 0
@@ -494,9 +525,14 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     f = lambda x: _to(x, dev, torch.float32)  # noqa: E731
     means3d = f(inputs[names["means3d"]])
     P = means3d.shape[0]
-    opac = f(inputs["opacities"])
+    opac = f(inputs["opacity_logits" if raw else "opacities"])
     if opac.numel() != P:
         raise ValueError(f"opacities has {opac.numel()} entries for {P} Gaussians")
+    if raw:
+        ls, rq = f(inputs["log_scales"]), f(inputs["raw_rotations"])
+        if ls.shape != (P, 3) or rq.shape != (P, 4):
+            raise ValueError(f"{fn} expects log_scales [P,3] and raw_rotations [P,4], got "
+                             f"{tuple(ls.shape)} and {tuple(rq.shape)}")
     vsp = inputs.get("viewspace_points")
     if vsp is None or _size(vsp) == 0:
         if not default_vsp:
@@ -507,7 +543,7 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     cfg = dict(degree=int(degree), max_sh=max_sh, W=int(image_width), H=int(image_height), gx=gx,
                gy=gy, use_cov=has_cov, use_col=has_col, scale_modifier=float(scale_modifier),
                mult=float(mult), tan_fovx=float(tan_fovx), tan_fovy=float(tan_fovy),
-               st_base=None, st_masks=None)
+               st_base=None, st_masks=None, raw=raw)
     if st_records and ((gx + 7) // 8) * ((gy + 7) // 8) <= 256:
         cfg["st_base"] = torch.empty(P, dtype=torch.int32, device=dev)
         cfg["st_masks"] = torch.empty((P, 4), dtype=torch.int64, device=dev)
@@ -515,6 +551,12 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     sh = f(inputs["sh"]) if sh_path else None
     if sh is not None and sh.numel() == 0:
         sh = sh.reshape(P, 0, 3) if sh.dim() < 3 else sh
+    if raw:
+        outs = _Preprocess.apply(
+            cfg, means3d, dc, sh, f(col) if has_col else None, None, None, None, None,
+            f(inputs[names["view"]]), f(inputs[names["proj"]]), f(inputs[names["campos"]]), vsp,
+            ls, rq, opac)
+        return outs, cfg, dev
     outs = _Preprocess.apply(
         cfg, means3d, dc, sh, f(col) if has_col else None, opac,
         None if has_cov else f(inputs["scales"]), None if has_cov else f(inputs[names["rot"]]),
@@ -523,6 +565,7 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     return outs, cfg, dev
 
 
+_RAW_KEYS = ("log_scales", "raw_rotations", "opacity_logits")
 _RG_NAMES = dict(required=("means3d", "background", "opacities", "metric_map", "viewmatrix",
                            "projmatrix", "campos"),
                  col_keys=("colors_precomp", "colors"), rot="rotations", means3d="means3d",
@@ -543,6 +586,15 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     """Full forward (binding.cpp:33-282): preprocess -> scan -> binning/sort ->
     tile ranges -> bucket offsets -> rasterize.  The two 4-byte reads of the
     reference (K and B) are waited for while the GPU has queued work.
+
+    ``inputs`` may carry, in place of ``opacities``, ``scales`` and
+    ``rotations``, the raw parameters of a training step (no reference
+    counterpart): ``log_scales`` [P,3], ``raw_rotations`` [P,4] and
+    ``opacity_logits`` [P].  The training scripts' activations
+    (train_scanner_fixed.py:523-536: exp, q/(|q|+1e-8), sigmoid) are then
+    applied inside, and the gradients reach the raw tensors directly: the
+    activations' backward is fused into the preprocess backward, with results
+    bit-identical to ``activate`` followed by the activated call.
 
     ``count_iterations`` (measurement, no reference counterpart) adds
     ``img_n_iter``: each pixel's iterations of the reference blend loop

@@ -152,6 +152,20 @@ typedef struct {
   float* dL_dscales;           /* [P,3] */
   float* dL_drotations;        /* [P,4] */
   float* dL_dviewspace_in;     /* [P,4] */
+  /* Training-step fusion (no reference counterpart; optional, NULL = off):
+   * the gradients of the raw parameters of the training scripts'
+   * activations scale = exp(log_scale), rotation = q / (|q| + 1e-8),
+   * opacity = sigmoid(logit) (train_scanner_fixed.py:523-536), written in
+   * place of dL_dscales / dL_drotations / dL_dopacities (which may then be
+   * NULL), bit-identical to fgs_activations_bwd applied to them.  quats_raw
+   * are the raw quaternions q, act_opacities the sigmoid outputs; the scales
+   * are `scales`.  dL_dlog_scales and dL_dquats need the scale / rotation
+   * path (use_cov3d_precomp = 0). */
+  const float* quats_raw;      /* [P,4] */
+  const float* act_opacities;  /* [P] */
+  float* dL_dlog_scales;       /* [P,3] */
+  float* dL_dquats;            /* [P,4] */
+  float* dL_dlogits;           /* [P] */
 } fgs_preprocess_bwd_io;
 
 /* Replaces FastGSPreprocess::vjp -> FastGSPreprocessBackward::eval_gpu

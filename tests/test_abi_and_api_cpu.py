@@ -77,6 +77,17 @@ def test_launch_events_argument_checks():
         assert lib.fgs_set_launch_events(name, None, None) == _lib.FGS_OK
 
 
+def test_api_raw_parameters_exclusive():
+    """The raw training parameters replace the activated ones; both at once is
+    an error raised before any GPU work."""
+    inp = _inputs()
+    P = inp["means3d"].shape[0]
+    inp.update(log_scales=np.zeros((P, 3), np.float32), raw_rotations=np.ones((P, 4), np.float32),
+               opacity_logits=np.zeros(P, np.float32))
+    with pytest.raises(RuntimeError, match="not both"):
+        fastgs_core.rasterize_gaussians(inp, 32, 32, 16, 16, 1.0, 1.0, 0)
+
+
 def _inputs():
     sc = syn.scene_config1(0, 64)
     cam = syn.config1_camera(32, 32)
