@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 class PreprocessParams(Structure):
@@ -36,7 +36,7 @@ class PreprocessFwdIO(Structure):
         "means3d", "dc", "sh", "colors_precomp", "opacities", "scales", "rotations",
         "cov3d_precomp", "viewmatrix", "projmatrix", "campos", "viewspace_in", "radii", "xys",
         "depths", "cov3d", "rgb", "conic_opacity", "tiles_touched", "clamped", "viewspace_out",
-        "st_base", "st_masks")]
+        "st_base", "st_masks", "log_scales", "raw_rotations", "opacity_logits")]
 
 
 class PreprocessBwdIO(Structure):
@@ -46,7 +46,7 @@ class PreprocessBwdIO(Structure):
         "dL_dconic_opacity", "dL_dcov3d", "dL_dviewspace_out", "dL_dmeans3d", "dL_ddc", "dL_dsh",
         "dL_dcolors_precomp", "dL_dopacities", "dL_dscales", "dL_drotations",
         "dL_dviewspace_in", "quats_raw", "act_opacities", "dL_dlog_scales", "dL_dquats",
-        "dL_dlogits")]
+        "dL_dlogits", "log_scales", "opacity_logits")]
 
 
 class BinningIO(Structure):

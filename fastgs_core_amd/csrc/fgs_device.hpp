@@ -82,6 +82,18 @@ __device__ __forceinline__ float splat_power(float A, float B, float C, float dx
   return splat_power_rows(B * dx, (A * dx) * dx, C, dy);
 }
 
+// The training scripts' parameter activations (train_scanner_fixed.py:523-536):
+// scale = exp(log_scale), rotation = q / (|q| + 1e-8), opacity =
+// sigmoid(logit).  Shared by the activation kernel and the preprocess kernels'
+// raw-parameter forms, so they agree bit for bit.
+__device__ __forceinline__ float act_scale(float log_scale) { return expf(log_scale); }
+__device__ __forceinline__ float4 act_rotation(float4 q) {
+  const float n = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+  const float d = n + 1e-8f;
+  return make_float4(q.x / d, q.y / d, q.z / d, q.w / d);
+}
+__device__ __forceinline__ float act_opacity(float logit) { return 1.0f / (1.0f + expf(-logit)); }
+
 // Gradient through the training scripts' rotation activation
 // r = q / (|q| + 1e-8): dq = g/d - q (q.g) / (d^2 |q|), d = |q| + 1e-8 (the
 // second term is 0 at q = 0).  Shared by the activation backward and the

@@ -163,6 +163,25 @@ __device__ __forceinline__ void store_sh_rows(const float* __restrict__ s_sh, in
   if (t < n) dst[t] = s_sh[t];
 }
 
+// Scale, rotation and opacity of Gaussian I: the activated inputs, or the
+// raw parameters activated here (the training-step form).
+__device__ __forceinline__ float3 load_scale(const float* scales, const float* log_scales,
+                                             size_t I) {
+  if (log_scales)
+    return make_float3(act_scale(log_scales[3 * I + 0]), act_scale(log_scales[3 * I + 1]),
+                       act_scale(log_scales[3 * I + 2]));
+  return make_float3(scales[3 * I + 0], scales[3 * I + 1], scales[3 * I + 2]);
+}
+__device__ __forceinline__ float4 load_rotation(const float* rotations, const float* raw, size_t I) {
+  if (raw) return act_rotation(*reinterpret_cast<const float4*>(raw + 4 * I));
+  return make_float4(rotations[4 * I + 0], rotations[4 * I + 1], rotations[4 * I + 2],
+                     rotations[4 * I + 3]);
+}
+__device__ __forceinline__ float load_opacity(const float* opacities, const float* logits,
+                                              size_t I) {
+  return logits ? act_opacity(logits[I]) : opacities[I];
+}
+
 // Tile walks longer than this many lines are taken by the whole wavefront
 // (tiles_walk_wave), so one wide Gaussian does not hold its 63 neighbours
 // for its full walk.
@@ -218,10 +237,9 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
 #pragma unroll
       for (int k = 0; k < 6; ++k) c3[k] = io.cov3d_precomp[6 * I + k];
     } else {
-      const float4 q = make_float4(io.rotations[4 * I + 0], io.rotations[4 * I + 1],
-                                   io.rotations[4 * I + 2], io.rotations[4 * I + 3]);
-      cov3d_from_sr(io.scales[3 * I + 0], io.scales[3 * I + 1], io.scales[3 * I + 2],
-                    prm.scale_modifier, q, c3);
+      const float4 q = load_rotation(io.rotations, io.raw_rotations, I);
+      const float3 sc = load_scale(io.scales, io.log_scales, I);
+      cov3d_from_sr(sc.x, sc.y, sc.z, prm.scale_modifier, q, c3);
     }
     Cov2D cv;
     cov2d_eval(V, mx, my, mz, focal_x, focal_y, prm.tan_fovx, prm.tan_fovy, c3, cv);
@@ -236,7 +254,8 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
       const float my_radius = ceilf(3.0f * __builtin_sqrtf(fmaxf(lambda1, lambda2)));
       const float px = ((pp0 + 1.0f) * (float)prm.image_width - 1.0f) * 0.5f;
       const float py = ((pp1 + 1.0f) * (float)prm.image_height - 1.0f) * 0.5f;
-      const float4 con_o = make_float4(conic0, conic1, conic2, io.opacities[I]);
+      const float4 con_o =
+          make_float4(conic0, conic1, conic2, load_opacity(io.opacities, io.opacity_logits, I));
       const WalkSetup ws = walk_setup(px, py, con_o, prm.grid_x, prm.grid_y, prm.mult, st);
       uint32_t n = 0u;
       if (!ws.empty) {
@@ -380,6 +399,7 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
   float dcol[3] = {0.f, 0.f, 0.f};
   float dop = 0.f;
   float dsc[3] = {0.f, 0.f, 0.f};
+  float3 sc_act = make_float3(0.f, 0.f, 0.f);  // the (activated) scales, once read
   float dq[4] = {0.f, 0.f, 0.f, 0.f};
   float4 dvsp = make_float4(0.f, 0.f, 0.f, 0.f);
   float* __restrict__ ds = kStaged ? dsv : (io.dL_dsh ? io.dL_dsh + I * (size_t)msh * 3 : nullptr);
@@ -568,8 +588,8 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
       }
     }
     if (!prm.use_cov3d_precomp) {
-      const float r = io.rotations[4 * I + 0], x = io.rotations[4 * I + 1],
-                  y = io.rotations[4 * I + 2], z = io.rotations[4 * I + 3];
+      const float4 rq = load_rotation(io.rotations, io.rotations ? nullptr : io.quats_raw, I);
+      const float r = rq.x, x = rq.y, y = rq.z, z = rq.w;
       float R[3][3];
       R[0][0] = 1.0f - 2.0f * (y * y + z * z);
       R[0][1] = 2.0f * (x * y - r * z);
@@ -580,9 +600,9 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
       R[2][0] = 2.0f * (x * z - r * y);
       R[2][1] = 2.0f * (y * z + r * x);
       R[2][2] = 1.0f - 2.0f * (x * x + y * y);
-      const float s[3] = {prm.scale_modifier * io.scales[3 * I + 0],
-                          prm.scale_modifier * io.scales[3 * I + 1],
-                          prm.scale_modifier * io.scales[3 * I + 2]};
+      sc_act = load_scale(io.scales, io.log_scales, I);
+      const float s[3] = {prm.scale_modifier * sc_act.x, prm.scale_modifier * sc_act.y,
+                          prm.scale_modifier * sc_act.z};
       float M[3][3];
 #pragma unroll
       for (int c = 0; c < 3; ++c)
@@ -646,12 +666,15 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
   // the activations' backward, with the operations of activations_bwd_kernel
   // (fgs_train.hip), so the fused and the separate forms agree bit for bit
   if (io.dL_dlogits) {
-    const float o = io.act_opacities[I];
+    const float o = load_opacity(io.act_opacities, io.act_opacities ? nullptr : io.opacity_logits, I);
     io.dL_dlogits[I] = dop * (1.0f - o) * o;
   }
-  if (io.dL_dlog_scales)
-#pragma unroll
-    for (int k = 0; k < 3; ++k) io.dL_dlog_scales[3 * I + k] = dsc[k] * io.scales[3 * I + k];
+  if (io.dL_dlog_scales) {
+    if (!(valid && io.radii[I] > 0)) sc_act = load_scale(io.scales, io.log_scales, I);
+    io.dL_dlog_scales[3 * I + 0] = dsc[0] * sc_act.x;
+    io.dL_dlog_scales[3 * I + 1] = dsc[1] * sc_act.y;
+    io.dL_dlog_scales[3 * I + 2] = dsc[2] * sc_act.z;
+  }
   if (io.dL_dquats) {
     const float4 q = *reinterpret_cast<const float4*>(io.quats_raw + 4 * I);
     *reinterpret_cast<float4*>(io.dL_dquats + 4 * I) =
@@ -684,11 +707,13 @@ extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
   if (!p || !io) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: null argument");
   if (p->P < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: P < 0");
   if (p->P == 0) return FGS_OK;
-  if (!io->means3d || !io->opacities || !io->viewmatrix || !io->projmatrix || !io->campos ||
+  if (!io->means3d || !(io->opacities || io->opacity_logits) || !io->viewmatrix ||
+      !io->projmatrix || !io->campos ||
       !io->viewspace_in || !io->radii || !io->xys || !io->depths || !io->cov3d || !io->rgb ||
       !io->conic_opacity || !io->tiles_touched || !io->clamped || !io->viewspace_out)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing tensor");
-  if (p->use_cov3d_precomp ? !io->cov3d_precomp : (!io->scales || !io->rotations))
+  if (p->use_cov3d_precomp ? !io->cov3d_precomp
+                           : (!(io->scales || io->log_scales) || !(io->rotations || io->raw_rotations)))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing geometry tensors");
   if (p->use_colors_precomp ? !io->colors_precomp : (!io->dc || (p->degree > 0 && !io->sh)))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing colour tensors");
@@ -739,14 +764,16 @@ extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
   if (p->P == 0) return FGS_OK;
   if (!io->means3d || !io->viewmatrix || !io->projmatrix || !io->campos || !io->radii ||
       !io->clamped || !io->dL_dmeans3d || !io->dL_dviewspace_in ||
-      !(io->dL_dopacities || (io->dL_dlogits && io->act_opacities)))
+      !(io->dL_dopacities || (io->dL_dlogits && (io->act_opacities || io->opacity_logits))))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing tensor");
   if (p->use_cov3d_precomp ? !io->cov3d_precomp
-                           : (!io->cov3d_fwd || !io->scales || !io->rotations))
+                           : (!io->cov3d_fwd || !(io->scales || io->log_scales) ||
+                              !(io->rotations || io->quats_raw)))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing geometry tensors");
   if (!p->use_colors_precomp && p->degree > 0 && p->max_sh_coeffs >= 3 && (!io->sh || !io->dL_dsh))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_bwd: missing sh tensors");
-  if ((io->dL_dlogits && !io->act_opacities) || (io->dL_dquats && !io->quats_raw) ||
+  if ((io->dL_dlogits && !(io->act_opacities || io->opacity_logits)) ||
+      (io->dL_dquats && !io->quats_raw) ||
       ((io->dL_dlog_scales || io->dL_dquats) && p->use_cov3d_precomp))
     return set_error(FGS_ERR_INVALID_ARGUMENT,
                      "fgs_preprocess_bwd: fused activation gradients need act_opacities, "

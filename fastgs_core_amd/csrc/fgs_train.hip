@@ -27,16 +27,12 @@ activations_fwd_kernel(int32_t P, const float* __restrict__ log_scales,
   if (i >= P) return;
   if (log_scales) {
 #pragma unroll
-    for (int k = 0; k < 3; ++k) scales[3 * (size_t)i + k] = expf(log_scales[3 * (size_t)i + k]);
+    for (int k = 0; k < 3; ++k) scales[3 * (size_t)i + k] = act_scale(log_scales[3 * (size_t)i + k]);
   }
-  if (quats) {
-    const float4 q = *reinterpret_cast<const float4*>(quats + 4 * (size_t)i);
-    const float n = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
-    const float d = n + 1e-8f;
+  if (quats)
     *reinterpret_cast<float4*>(rotations + 4 * (size_t)i) =
-        make_float4(q.x / d, q.y / d, q.z / d, q.w / d);
-  }
-  if (logits) opacities[i] = 1.0f / (1.0f + expf(-logits[i]));
+        act_rotation(*reinterpret_cast<const float4*>(quats + 4 * (size_t)i));
+  if (logits) opacities[i] = act_opacity(logits[i]);
 }
 
 // Gradients w.r.t. the raw parameters from the gradients of the activated

@@ -171,16 +171,8 @@ class _Preprocess(torch.autograd.Function):
         dev = means3d.device
         P = means3d.shape[0]
         f32 = dict(dtype=torch.float32, device=dev)
-        if cfg.get("raw"):
-            # the training scripts' activations applied here (fgs_activations_fwd);
-            # their backward is fused into the preprocess backward
-            scales = torch.empty((P, 3), **f32)
-            rotations = torch.empty((P, 4), **f32)
-            opacities = torch.empty(P, **f32)
-            if P > 0:
-                _lib.check(lib.fgs_activations_fwd(P, _p(log_scales), _p(raw_rotations),
-                                                   _p(opacity_logits), _p(scales), _p(rotations),
-                                                   _p(opacities), _stream(dev)))
+        # raw: the training scripts' activations are applied inside the
+        # preprocess kernels (forward and backward), from the raw parameters
         radii = torch.empty(P, dtype=torch.int32, device=dev)
         xys = torch.empty((P, 2), **f32)
         depths = torch.empty(P, **f32)
@@ -198,7 +190,8 @@ class _Preprocess(torch.autograd.Function):
             _p(means3d), _p(dc), _p(sh), _p(colors_precomp), _p(opacities), _p(scales),
             _p(rotations), _p(cov3d_precomp), _p(viewmatrix), _p(projmatrix), _p(campos),
             _p(viewspace_in), _p(radii), _p(xys), _p(depths), _p(cov3d), _p(rgb), _p(conic),
-            _p(tiles), _p(clamped), _p(vsp_out), _p(cfg["st_base"]), _p(cfg["st_masks"]))
+            _p(tiles), _p(clamped), _p(vsp_out), _p(cfg["st_base"]), _p(cfg["st_masks"]),
+            _p(log_scales), _p(raw_rotations), _p(opacity_logits))
         if P > 0:
             with _stage("preprocess_fwd"):
                 _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io),
@@ -207,8 +200,8 @@ class _Preprocess(torch.autograd.Function):
         ctx.opacity_shape = (opacity_logits if cfg.get("raw") else opacities).shape
         ctx.sh_shape = None if sh is None else sh.shape
         ctx.save_for_backward(means3d, sh, scales, rotations, cov3d_precomp, viewmatrix,
-                              projmatrix, campos, cov3d, radii, clamped, raw_rotations,
-                              opacities if cfg.get("raw") else None)
+                              projmatrix, campos, cov3d, radii, clamped, log_scales,
+                              raw_rotations, opacity_logits)
         ctx.mark_non_differentiable(radii, tiles, clamped)
         # outputs the loss does not reach arrive as None (no zero tensors)
         ctx.set_materialize_grads(False)
@@ -219,7 +212,7 @@ class _Preprocess(torch.autograd.Function):
                  g_vsp):
         lib = _lib.load()
         (means3d, sh, scales, rotations, cov3d_precomp, viewmatrix, projmatrix, campos, cov3d,
-         radii, clamped, raw_rotations, act_opacities) = ctx.saved_tensors
+         radii, clamped, log_scales, raw_rotations, opacity_logits) = ctx.saved_tensors
         cfg = ctx.cfg
         raw = bool(cfg.get("raw"))
         dev = means3d.device
@@ -247,9 +240,9 @@ class _Preprocess(torch.autograd.Function):
             _p(sh), _p(cov3d_precomp), _p(cov3d), _p(radii), _p(clamped), _p(g_xys), _p(g_rgb),
             _p(g_conic), _p(g_cov3d), _p(g_vsp), _p(d_means3d), _p(d_dc), _p(d_sh), _p(d_col),
             None if raw else _p(d_opac), None if raw else _p(d_scales),
-            None if raw else _p(d_rot), _p(d_vsp), _p(raw_rotations), _p(act_opacities),
+            None if raw else _p(d_rot), _p(d_vsp), _p(raw_rotations), None,
             _p(d_scales) if raw else None, _p(d_rot) if raw else None,
-            _p(d_opac) if raw else None)
+            _p(d_opac) if raw else None, _p(log_scales), _p(opacity_logits))
         if P > 0:
             with _stage("preprocess_bwd"):
                 _lib.check(lib.fgs_preprocess_bwd(ctypes.byref(prm), ctypes.byref(io),

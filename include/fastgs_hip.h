@@ -116,6 +116,15 @@ typedef struct {
    * Both set or both NULL. */
   uint32_t* st_base;           /* [P] */
   uint64_t* st_masks;          /* [P,4], 16-byte aligned */
+  /* Training-step fusion (no reference counterpart; optional, NULL = off):
+   * the raw parameters, activated here as the training scripts do
+   * (train_scanner_fixed.py:523-536): scale = exp(log_scale), rotation =
+   * q / (|q| + 1e-8), opacity = sigmoid(logit), bit-identical to
+   * fgs_activations_fwd.  Each one set replaces its activated input, which
+   * may then be NULL. */
+  const float* log_scales;     /* [P,3] */
+  const float* raw_rotations;  /* [P,4] */
+  const float* opacity_logits; /* [P] */
 } fgs_preprocess_fwd_io;
 
 /* Replaces FastGSPreprocess::eval_gpu (fastgs_preprocess.cpp:81-169) /
@@ -160,12 +169,18 @@ typedef struct {
    * NULL), bit-identical to fgs_activations_bwd applied to them.  quats_raw
    * are the raw quaternions q, act_opacities the sigmoid outputs; the scales
    * are `scales`.  dL_dlog_scales and dL_dquats need the scale / rotation
-   * path (use_cov3d_precomp = 0). */
+   * path (use_cov3d_precomp = 0).  With log_scales set the scales are
+   * computed from it (scales may be NULL), with quats_raw set and rotations
+   * NULL the rotations from quats_raw, and with opacity_logits set and
+   * act_opacities NULL the opacities from the logits, as fgs_preprocess_fwd
+   * does. */
   const float* quats_raw;      /* [P,4] */
   const float* act_opacities;  /* [P] */
   float* dL_dlog_scales;       /* [P,3] */
   float* dL_dquats;            /* [P,4] */
   float* dL_dlogits;           /* [P] */
+  const float* log_scales;     /* [P,3] */
+  const float* opacity_logits; /* [P] */
 } fgs_preprocess_bwd_io;
 
 /* Replaces FastGSPreprocess::vjp -> FastGSPreprocessBackward::eval_gpu
