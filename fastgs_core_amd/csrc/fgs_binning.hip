@@ -1384,6 +1384,7 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
 // consecutive positions, so each store is one contiguous run.
 constexpr int kL2Stage = 4608;
 constexpr int kL2PerLane = kL2Chunk / kWave;  // 8 entries per lane on the tile-by-tile path
+static_assert(kL2Stage >= 2 * kL2Chunk, "the tile-by-tile path stages a chunk in the stage arrays");
 __global__ void __launch_bounds__(kL1Group)
 l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
                const uint32_t* __restrict__ st_start, const uint32_t* __restrict__ chunk_first,
@@ -1392,8 +1393,8 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
                const uint32_t* __restrict__ base2, const uint32_t* __restrict__ tile_start,
                int32_t P, const float* __restrict__ depths, int64_t K,
                uint64_t* __restrict__ keys, uint32_t* __restrict__ point_list) {
-  __shared__ uint32_t s_g[kL2Stage];
-  __shared__ uint32_t s_db[kL2Stage];
+  __shared__ __align__(16) uint32_t s_g[kL2Stage];
+  __shared__ __align__(16) uint32_t s_db[kL2Stage];
   __shared__ uint32_t s_wc[kWavesPerBlock][kWave];
   const uint32_t c = blockIdx.x;
   if (c >= nchunks[0]) return;
@@ -1412,18 +1413,29 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
     if (x < sg.gx && y < sg.gy) gbase = tile_start[y * sg.gx + x] + base2[(size_t)c * kWave + l];
   }
   if (total > (uint32_t)kL2Stage) {  // uniform: the tile-by-tile path
+    // the chunk's entries are loaded once per workgroup into the (here
+    // unused) staging arrays: masks in s_g, indices and depth bits in s_db
+    uint64_t* s_m = reinterpret_cast<uint64_t*>(s_g);
+    for (int q = t; q < kL2Chunk; q += kL1Group) {
+      const uint32_t e = e0 + (uint32_t)q;
+      const bool valid = e < e1;
+      const uint64_t m = valid ? masks[e] : 0ull;
+      const uint32_t g = valid ? list[e] : 0u;
+      s_m[q] = m;
+      s_db[q] = g;
+      s_db[kL2Chunk + q] =
+          (m != 0ull && g < (uint32_t)P) ? __float_as_uint(depths[g]) : 0xFFFFFFFFu;
+    }
+    __syncthreads();
     uint64_t em[kL2PerLane];
     uint32_t eg[kL2PerLane], edb[kL2PerLane];
 #pragma unroll
     for (int r = 0; r < kL2PerLane; ++r) {
-      const uint32_t e = e0 + (uint32_t)(r * kWave + l);
-      const bool valid = e < e1;
-      em[r] = valid ? masks[e] : 0ull;
-      eg[r] = valid ? list[e] : 0u;
+      const int q = r * kWave + l;
+      em[r] = s_m[q];
+      eg[r] = s_db[q];
+      edb[r] = s_db[kL2Chunk + q];
     }
-#pragma unroll
-    for (int r = 0; r < kL2PerLane; ++r)
-      edb[r] = (em[r] != 0ull && eg[r] < (uint32_t)P) ? __float_as_uint(depths[eg[r]]) : 0xFFFFFFFFu;
     for (int j = w; j < kWave; j += kWavesPerBlock) {
       const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
       if (nj == 0u) continue;
