@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 
 class PreprocessParams(Structure):
@@ -118,6 +118,10 @@ SIGNATURES = {
     "fgs_abi_version": (c_int32, []),
     "fgs_preprocess_fwd": (c_int32, [POINTER(PreprocessParams), POINTER(PreprocessFwdIO), c_void_p]),
     "fgs_preprocess_bwd": (c_int32, [POINTER(PreprocessParams), POINTER(PreprocessBwdIO), c_void_p]),
+    "fgs_preprocess_geometry_fwd": (c_int32, [POINTER(PreprocessParams), POINTER(PreprocessFwdIO),
+                                              c_void_p]),
+    "fgs_preprocess_colour_fwd": (c_int32, [POINTER(PreprocessParams), POINTER(PreprocessFwdIO),
+                                            c_void_p]),
     "fgs_scan_workspace_bytes": (c_size_t, [c_int64]),
     "fgs_set_wait_spin_limit": (c_uint32, [c_uint32]),
     "fgs_set_launch_events": (c_int32, [c_char_p, c_void_p, c_void_p]),

@@ -13,7 +13,8 @@ thread_local char g_last_error[512] = "";
 // Caller events per launch kind: [kind][0] before, [kind][1] after.
 std::atomic<void*> g_launch_events[fgs::kLaunchKinds][2];
 constexpr const char* kLaunchNames[fgs::kLaunchKinds] = {
-    "preprocess_fwd", "rasterize_fwd", "rasterize_bwd", "preprocess_bwd", "loss_fwd", "loss_bwd"};
+    "preprocess_fwd", "rasterize_fwd", "rasterize_bwd", "preprocess_bwd", "loss_fwd", "loss_bwd",
+    "preprocess_colour"};
 }  // namespace
 
 namespace fgs {
@@ -48,7 +49,7 @@ int32_t launch_mark(LaunchKind k, hipStream_t st, int after) {
 
 extern "C" const char* fgs_last_error(void) { return g_last_error; }
 
-extern "C" int32_t fgs_abi_version(void) { return 12; }
+extern "C" int32_t fgs_abi_version(void) { return 13; }
 
 extern "C" int32_t fgs_set_launch_events(const char* kernel, void* start, void* stop) {
   if (!kernel) return fgs::set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_set_launch_events: null name");

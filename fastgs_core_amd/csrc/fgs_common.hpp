@@ -27,6 +27,7 @@ enum LaunchKind {
   kLaunchPreprocessBwd,
   kLaunchLossFwd,
   kLaunchLossBwd,
+  kLaunchPreprocessColour,
   kLaunchKinds
 };
 int32_t launch_mark(LaunchKind k, hipStream_t st, int after);

@@ -8,6 +8,8 @@
 // fastgs_preprocess_backward.metal:60-430.  Matrices arrive as 16 floats,
 // column-major; the Metal float3x3 constructor fills columns, so X[c][r]
 // below is column c, row r of the Metal matrix.
+#include <cstdio>
+
 #include "fgs_common.hpp"
 
 namespace fgs {
@@ -182,6 +184,54 @@ __device__ __forceinline__ float load_opacity(const float* opacities, const floa
   return logits ? act_opacity(logits[I]) : opacities[I];
 }
 
+// Colour of Gaussian I (fastgs_preprocess.metal:117-169 through computeColorFromSH):
+// colors_precomp, or the SH colour toward the camera centre clamped at 0
+// (clamp[c] = the unclamped value was negative).  s: its SH rest
+// coefficients (3 floats each), in LDS or global memory.
+__device__ __forceinline__ void gaussian_colour(const fgs_preprocess_params& prm,
+                                                const float* __restrict__ colors_precomp,
+                                                const float* __restrict__ campos,
+                                                const float* __restrict__ dc,
+                                                const float* __restrict__ s, size_t I, float mx,
+                                                float my, float mz, float col[3],
+                                                uint8_t clamp[3]) {
+  if (prm.use_colors_precomp) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) col[c] = colors_precomp[3 * I + c];
+    return;
+  }
+  const float v0 = mx - campos[0], v1 = my - campos[1], v2 = mz - campos[2];
+  const float len = __builtin_sqrtf(v0 * v0 + v1 * v1 + v2 * v2);
+  const float x = v0 / len, y = v1 / len, z = v2 / len;
+  const float* __restrict__ d = dc + 3 * I;
+  const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float res = kSH_C0 * d[c];
+    if (prm.degree > 0) {
+      res = res - kSH_C1 * y * s[0 * 3 + c] + kSH_C1 * z * s[1 * 3 + c] -
+            kSH_C1 * x * s[2 * 3 + c];
+      if (prm.degree > 1) {
+        res += kSH_C2[0] * xy * s[3 * 3 + c] + kSH_C2[1] * yz * s[4 * 3 + c] +
+               kSH_C2[2] * (2.0f * zz - xx - yy) * s[5 * 3 + c] +
+               kSH_C2[3] * xz * s[6 * 3 + c] + kSH_C2[4] * (xx - yy) * s[7 * 3 + c];
+        if (prm.degree > 2) {
+          res += kSH_C3[0] * y * (3.0f * xx - yy) * s[8 * 3 + c] +
+                 kSH_C3[1] * xy * z * s[9 * 3 + c] +
+                 kSH_C3[2] * y * (4.0f * zz - xx - yy) * s[10 * 3 + c] +
+                 kSH_C3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy) * s[11 * 3 + c] +
+                 kSH_C3[4] * x * (4.0f * zz - xx - yy) * s[12 * 3 + c] +
+                 kSH_C3[5] * z * (xx - yy) * s[13 * 3 + c] +
+                 kSH_C3[6] * x * (xx - 3.0f * yy) * s[14 * 3 + c];
+        }
+      }
+    }
+    res += 0.5f;
+    clamp[c] = res < 0.0f;
+    col[c] = fmaxf(res, 0.0f);
+  }
+}
+
 // Tile walks longer than this many lines are taken by the whole wavefront
 // (tiles_walk_wave), so one wide Gaussian does not hold its 63 neighbours
 // for its full walk.
@@ -189,7 +239,9 @@ constexpr int kWaveWalkLines = 16;
 
 // kRow = 0: SH rows are read from global memory where needed; kRow > 0: the
 // rows (kRow = 3 * max_sh_coeffs floats) of the block are staged through LDS.
-template <int kRow>
+// kColour = false: the geometry only (rgb and clamped are not written;
+// preprocess_colour_kernel writes them, possibly on another stream).
+template <int kRow, bool kColour = true>
 __global__ void __launch_bounds__(256)
 preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_io io,
                       float focal_x, float focal_y) {
@@ -270,43 +322,11 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
         }
       }
       if (n != 0u) {
-        if (prm.use_colors_precomp) {
-#pragma unroll
-          for (int c = 0; c < 3; ++c) col[c] = io.colors_precomp[3 * I + c];
-        } else {
-          const float v0 = mx - io.campos[0], v1 = my - io.campos[1], v2 = mz - io.campos[2];
-          const float len = __builtin_sqrtf(v0 * v0 + v1 * v1 + v2 * v2);
-          const float x = v0 / len, y = v1 / len, z = v2 / len;
-          const float* __restrict__ s =
-              kRow > 0 ? s_sh + threadIdx.x * kRow : io.sh + I * (size_t)row;
-          const float* __restrict__ d = io.dc + 3 * I;
-          const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
-#pragma unroll
-          for (int c = 0; c < 3; ++c) {
-            float res = kSH_C0 * d[c];
-            if (prm.degree > 0) {
-              res = res - kSH_C1 * y * s[0 * 3 + c] + kSH_C1 * z * s[1 * 3 + c] -
-                    kSH_C1 * x * s[2 * 3 + c];
-              if (prm.degree > 1) {
-                res += kSH_C2[0] * xy * s[3 * 3 + c] + kSH_C2[1] * yz * s[4 * 3 + c] +
-                       kSH_C2[2] * (2.0f * zz - xx - yy) * s[5 * 3 + c] +
-                       kSH_C2[3] * xz * s[6 * 3 + c] + kSH_C2[4] * (xx - yy) * s[7 * 3 + c];
-                if (prm.degree > 2) {
-                  res += kSH_C3[0] * y * (3.0f * xx - yy) * s[8 * 3 + c] +
-                         kSH_C3[1] * xy * z * s[9 * 3 + c] +
-                         kSH_C3[2] * y * (4.0f * zz - xx - yy) * s[10 * 3 + c] +
-                         kSH_C3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy) * s[11 * 3 + c] +
-                         kSH_C3[4] * x * (4.0f * zz - xx - yy) * s[12 * 3 + c] +
-                         kSH_C3[5] * z * (xx - yy) * s[13 * 3 + c] +
-                         kSH_C3[6] * x * (xx - 3.0f * yy) * s[14 * 3 + c];
-                }
-              }
-            }
-            res += 0.5f;
-            clamp[c] = res < 0.0f;
-            col[c] = fmaxf(res, 0.0f);
-          }
-        }
+        if constexpr (kColour)
+          gaussian_colour(prm, io.colors_precomp, io.campos, io.dc,
+                          kRow > 0 ? s_sh + threadIdx.x * kRow
+                                   : (io.sh ? io.sh + I * (size_t)row : nullptr),
+                          I, mx, my, mz, col, clamp);
         depth = pv2;
         radius = f2i(my_radius);
         xy0 = px;
@@ -354,10 +374,12 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
   c3o[0] = make_float2(c3[0], c3[1]);
   c3o[1] = make_float2(c3[2], c3[3]);
   c3o[2] = make_float2(c3[4], c3[5]);
+  if constexpr (kColour) {
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
-    io.rgb[3 * I + c] = col[c];
-    io.clamped[3 * I + c] = clamp[c];
+    for (int c = 0; c < 3; ++c) {
+      io.rgb[3 * I + c] = col[c];
+      io.clamped[3 * I + c] = clamp[c];
+    }
   }
   if (io.st_base) {
     const uint32_t w = cnt != 0u ? st.word() : 0u;
@@ -369,6 +391,34 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
       dst[1] = make_uint4((uint32_t)st.m2, (uint32_t)(st.m2 >> 32), (uint32_t)st.m3,
                           (uint32_t)(st.m3 >> 32));
     }
+  }
+}
+
+// The colour half of preprocess_fwd_kernel (the rgb and clamped rows), after
+// the geometry half: Gaussians with radius > 0 (those that touch a tile) get
+// gaussian_colour, the others zeros.  kRow as in preprocess_fwd_kernel.
+template <int kRow>
+__global__ void __launch_bounds__(256)
+preprocess_colour_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_io io) {
+  extern __shared__ float4 s_sh4[];
+  float* __restrict__ s_sh = reinterpret_cast<float*>(s_sh4);
+  const int row = kRow > 0 ? kRow : prm.max_sh_coeffs * 3;
+  if constexpr (kRow > 0) stage_sh_rows<kRow>(io.sh, prm.P, s_sh);
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= prm.P) return;
+  const size_t I = (size_t)i;
+  float col[3] = {0.f, 0.f, 0.f};
+  uint8_t clamp[3] = {0, 0, 0};
+  if (io.radii[I] > 0)
+    gaussian_colour(prm, io.colors_precomp, io.campos, io.dc,
+                    kRow > 0 ? s_sh + threadIdx.x * kRow
+                             : (io.sh ? io.sh + I * (size_t)row : nullptr),
+                    I, io.means3d[3 * I + 0], io.means3d[3 * I + 1], io.means3d[3 * I + 2], col,
+                    clamp);
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    io.rgb[3 * I + c] = col[c];
+    io.clamped[3 * I + c] = clamp[c];
   }
 }
 
@@ -702,33 +752,46 @@ static int staged_sh_row(const fgs_preprocess_params* p, const float* sh, const 
   return (m == 3 || m == 8 || m == 15) ? 3 * m : 0;
 }
 
-extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
-                                      const fgs_preprocess_fwd_io* io, void* stream) {
-  if (!p || !io) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: null argument");
-  if (p->P < 0) return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: P < 0");
+// Arguments of the preprocess forward, checked once for the fused call and
+// for each of its two halves.
+static int32_t preprocess_fwd_check(const fgs_preprocess_params* p, const fgs_preprocess_fwd_io* io,
+                                    const char* who) {
+  char msg[160];
+  auto fail = [&](const char* what) {
+    std::snprintf(msg, sizeof(msg), "%s: %s", who, what);
+    return set_error(FGS_ERR_INVALID_ARGUMENT, msg);
+  };
+  if (!p || !io) return fail("null argument");
+  if (p->P < 0) return fail("P < 0");
   if (p->P == 0) return FGS_OK;
   if (!io->means3d || !(io->opacities || io->opacity_logits) || !io->viewmatrix ||
       !io->projmatrix || !io->campos ||
       !io->viewspace_in || !io->radii || !io->xys || !io->depths || !io->cov3d || !io->rgb ||
       !io->conic_opacity || !io->tiles_touched || !io->clamped || !io->viewspace_out)
-    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing tensor");
+    return fail("missing tensor");
   if (p->use_cov3d_precomp ? !io->cov3d_precomp
                            : (!(io->scales || io->log_scales) || !(io->rotations || io->raw_rotations)))
-    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing geometry tensors");
+    return fail("missing geometry tensors");
   if (p->use_colors_precomp ? !io->colors_precomp : (!io->dc || (p->degree > 0 && !io->sh)))
-    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: missing colour tensors");
+    return fail("missing colour tensors");
   if (!p->use_colors_precomp && p->degree > 0) {
     const int d = p->degree > 3 ? 3 : p->degree;
     if (p->max_sh_coeffs < (d + 1) * (d + 1) - 1)
-      return set_error(FGS_ERR_INVALID_ARGUMENT,
-                       "fgs_preprocess_fwd: sh has fewer coefficients than the degree needs");
+      return fail("sh has fewer coefficients than the degree needs");
   }
   if (p->image_width <= 0 || p->image_height <= 0 || p->grid_x <= 0 || p->grid_y <= 0)
-    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_preprocess_fwd: bad image size");
+    return fail("bad image size");
   if (!io->st_base != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u))
-    return set_error(FGS_ERR_INVALID_ARGUMENT,
-                     "fgs_preprocess_fwd: st_base and st_masks must both be set (st_masks "
-                     "16-byte aligned) or both NULL");
+    return fail("st_base and st_masks must both be set (st_masks 16-byte aligned) or both NULL");
+  return FGS_OK;
+}
+
+// part: 0 the fused kernel, 1 the geometry half, 2 the colour half.
+static int32_t preprocess_fwd_launch(const fgs_preprocess_params* p,
+                                     const fgs_preprocess_fwd_io* io, void* stream, int part,
+                                     const char* who) {
+  if (const int32_t e = preprocess_fwd_check(p, io, who)) return e;
+  if (p->P == 0) return FGS_OK;
   const float fx = (float)p->image_width / (2.0f * p->tan_fovx);
   const float fy = (float)p->image_height / (2.0f * p->tan_fovy);
   const unsigned blocks = (unsigned)((p->P + 255) / 256);
@@ -736,25 +799,65 @@ extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
   // 16-byte loads; the direct path reads 4-byte elements 180 bytes apart.
   const hipStream_t st = (hipStream_t)stream;
   const dim3 grid(blocks), block(256);
+  if (part == 2) {
+    if (const int32_t e = launch_mark(kLaunchPreprocessColour, st, 0)) return e;
+    switch (staged_sh_row(p, io->sh, io->sh)) {
+      case 9:
+        hipLaunchKernelGGL(preprocess_colour_kernel<9>, grid, block, 256 * 9 * sizeof(float), st,
+                           *p, *io);
+        break;
+      case 24:
+        hipLaunchKernelGGL(preprocess_colour_kernel<24>, grid, block, 256 * 24 * sizeof(float),
+                           st, *p, *io);
+        break;
+      case 45:
+        hipLaunchKernelGGL(preprocess_colour_kernel<45>, grid, block, 256 * 45 * sizeof(float),
+                           st, *p, *io);
+        break;
+      default:
+        hipLaunchKernelGGL(preprocess_colour_kernel<0>, grid, block, 0, st, *p, *io);
+    }
+    if (check_launch("preprocess_colour_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
+    return launch_mark(kLaunchPreprocessColour, st, 1);
+  }
   if (const int32_t e = launch_mark(kLaunchPreprocessFwd, st, 0)) return e;
-  switch (staged_sh_row(p, io->sh, io->sh)) {
-    case 9:
-      hipLaunchKernelGGL(preprocess_fwd_kernel<9>, grid, block, 256 * 9 * sizeof(float), st, *p,
-                         *io, fx, fy);
-      break;
-    case 24:
-      hipLaunchKernelGGL(preprocess_fwd_kernel<24>, grid, block, 256 * 24 * sizeof(float), st,
-                         *p, *io, fx, fy);
-      break;
-    case 45:
-      hipLaunchKernelGGL(preprocess_fwd_kernel<45>, grid, block, 256 * 45 * sizeof(float), st,
-                         *p, *io, fx, fy);
-      break;
-    default:
-      hipLaunchKernelGGL(preprocess_fwd_kernel<0>, grid, block, 0, st, *p, *io, fx, fy);
+  if (part == 1) {
+    hipLaunchKernelGGL((preprocess_fwd_kernel<0, false>), grid, block, 0, st, *p, *io, fx, fy);
+  } else {
+    switch (staged_sh_row(p, io->sh, io->sh)) {
+      case 9:
+        hipLaunchKernelGGL(preprocess_fwd_kernel<9>, grid, block, 256 * 9 * sizeof(float), st, *p,
+                           *io, fx, fy);
+        break;
+      case 24:
+        hipLaunchKernelGGL(preprocess_fwd_kernel<24>, grid, block, 256 * 24 * sizeof(float), st,
+                           *p, *io, fx, fy);
+        break;
+      case 45:
+        hipLaunchKernelGGL(preprocess_fwd_kernel<45>, grid, block, 256 * 45 * sizeof(float), st,
+                           *p, *io, fx, fy);
+        break;
+      default:
+        hipLaunchKernelGGL(preprocess_fwd_kernel<0>, grid, block, 0, st, *p, *io, fx, fy);
+    }
   }
   if (check_launch("preprocess_fwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
   return launch_mark(kLaunchPreprocessFwd, st, 1);
+}
+
+extern "C" int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p,
+                                      const fgs_preprocess_fwd_io* io, void* stream) {
+  return preprocess_fwd_launch(p, io, stream, 0, "fgs_preprocess_fwd");
+}
+
+extern "C" int32_t fgs_preprocess_geometry_fwd(const fgs_preprocess_params* p,
+                                               const fgs_preprocess_fwd_io* io, void* stream) {
+  return preprocess_fwd_launch(p, io, stream, 1, "fgs_preprocess_geometry_fwd");
+}
+
+extern "C" int32_t fgs_preprocess_colour_fwd(const fgs_preprocess_params* p,
+                                             const fgs_preprocess_fwd_io* io, void* stream) {
+  return preprocess_fwd_launch(p, io, stream, 2, "fgs_preprocess_colour_fwd");
 }
 
 extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,

@@ -117,6 +117,35 @@ def _stream(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
+class _SideStreams(threading.local):
+    """Per thread and device: the side stream of the colour half of the
+    preprocess and its two events (reused from call to call: every call joins
+    its colour half before the next one is queued)."""
+
+    def __init__(self):
+        self.by_device = {}
+
+
+_SIDE = _SideStreams()
+
+
+def _side_stream(dev: torch.device):
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    entry = _SIDE.by_device.get(key)
+    if entry is None:
+        entry = (torch.cuda.Stream(device=dev), torch.cuda.Event(), torch.cuda.Event())
+        _SIDE.by_device[key] = entry
+    return entry
+
+
+def _join_colour(cfg, dev) -> None:
+    """Orders the current stream after the colour half of the preprocess."""
+    ev = cfg.get("colour_done")
+    if ev is not None:
+        torch.cuda.current_stream(dev).wait_event(ev)
+        cfg["colour_done"] = None
+
+
 def _size(x) -> int:
     if x is None:
         return 0
@@ -192,11 +221,27 @@ class _Preprocess(torch.autograd.Function):
             _p(viewspace_in), _p(radii), _p(xys), _p(depths), _p(cov3d), _p(rgb), _p(conic),
             _p(tiles), _p(clamped), _p(vsp_out), _p(cfg["st_base"]), _p(cfg["st_masks"]),
             _p(log_scales), _p(raw_rotations), _p(opacity_logits))
-        if P > 0:
+        if P > 0 and cfg.get("split_colour"):
+            # geometry on this stream; the colour half on the side stream after
+            # it, overlapping the binning (joined before the rasterize)
+            with _stage("preprocess_fwd"):
+                _lib.check(lib.fgs_preprocess_geometry_fwd(ctypes.byref(prm), ctypes.byref(io),
+                                                           _stream(dev)))
+            side, geo_done, colour_done = _side_stream(dev)
+            geo_done.record(torch.cuda.current_stream(dev))
+            side.wait_event(geo_done)
+            _lib.check(lib.fgs_preprocess_colour_fwd(ctypes.byref(prm), ctypes.byref(io),
+                                                     ctypes.c_void_p(side.cuda_stream)))
+            colour_done.record(side)
+            for t in (means3d, campos, dc, sh, colors_precomp, radii, rgb, clamped):
+                if t is not None:
+                    t.record_stream(side)
+            cfg["colour_done"] = colour_done
+        elif P > 0:
             with _stage("preprocess_fwd"):
                 _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io),
                                                   _stream(dev)))
-        ctx.cfg = dict(cfg, st_base=None, st_masks=None)  # the records are forward-only
+        ctx.cfg = dict(cfg, st_base=None, st_masks=None, colour_done=None)  # forward-only
         ctx.opacity_shape = (opacity_logits if cfg.get("raw") else opacities).shape
         ctx.sh_shape = None if sh is None else sh.shape
         ctx.save_for_backward(means3d, sh, scales, rotations, cov3d_precomp, viewmatrix,
@@ -536,7 +581,8 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     cfg = dict(degree=int(degree), max_sh=max_sh, W=int(image_width), H=int(image_height), gx=gx,
                gy=gy, use_cov=has_cov, use_col=has_col, scale_modifier=float(scale_modifier),
                mult=float(mult), tan_fovx=float(tan_fovx), tan_fovy=float(tan_fovy),
-               st_base=None, st_masks=None, raw=raw)
+               st_base=None, st_masks=None, raw=raw, split_colour=bool(st_records and SPLIT_COLOUR),
+               colour_done=None)
     if st_records and ((gx + 7) // 8) * ((gy + 7) // 8) <= 256:
         cfg["st_base"] = torch.empty(P, dtype=torch.int32, device=dev)
         cfg["st_masks"] = torch.empty((P, 4), dtype=torch.int64, device=dev)
@@ -559,6 +605,10 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
 
 
 _RAW_KEYS = ("log_scales", "raw_rotations", "opacity_logits")
+
+# rasterize_gaussians runs the preprocess's colour half (the SH colours) on a
+# side stream, where it overlaps the binning; False runs the fused kernel.
+SPLIT_COLOUR = True
 _RG_NAMES = dict(required=("means3d", "background", "opacities", "metric_map", "viewmatrix",
                            "projmatrix", "campos"),
                  col_keys=("colors_precomp", "colors"), rot="rotations", means3d="means3d",
@@ -633,6 +683,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
         if B > 0:
             rcfg = dict(W=cfg["W"], H=cfg["H"], C=3, T=T, B=B, get_flag=bool(get_flag),
                         write_sampled=ws, count_iter=bool(count_iterations))
+            _join_colour(cfg, dev)  # the rasterize reads rgb
             (bucket_to_tile, sampled_t, sampled_ar, final_t, n_contrib, max_contrib,
              pixel_colors, out_color, metric_count) = _Rasterize.apply(
                 rcfg, ranges, point_list, bucket_offsets, xys, rgb, conic, background, radii,
@@ -659,6 +710,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
         max_contrib = torch.zeros(0, **i32)
         pixel_colors = torch.zeros(0, **f32)
         out_color = torch.zeros(0, **f32)
+    _join_colour(cfg, dev)  # before rgb / clamped reach the caller
     result = {
         "rendered": K, "num_buckets": B, "out_color": out_color, "radii": radii,
         "point_offsets": point_offsets, "ranges": ranges, "bucket_count": bucket_count,

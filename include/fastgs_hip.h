@@ -50,7 +50,9 @@ int32_t fgs_abi_version(void);
  * without the small kernels an entry point launches around it.  `kernel`
  * names the main kernel of one stage: "preprocess_fwd", "rasterize_fwd",
  * "rasterize_bwd", "preprocess_bwd", "loss_fwd" or "loss_bwd" (the SSIM map
- * kernels of fgs_l1_ssim_fwd / fgs_l1_ssim_bwd).  Both events NULL clears the
+ * kernels of fgs_l1_ssim_fwd / fgs_l1_ssim_bwd), or "preprocess_colour" (the
+ * kernel of fgs_preprocess_colour_fwd; "preprocess_fwd" also names the kernel
+ * of fgs_preprocess_geometry_fwd).  Both events NULL clears the
  * entry; one of them NULL, or an unknown name, is FGS_ERR_INVALID_ARGUMENT.
  * A process-wide setting read at each launch; the events must stay valid
  * until it is cleared. */
@@ -131,6 +133,17 @@ typedef struct {
  * fastgs_preprocess_forward_kernel (fastgs_preprocess.metal:384-484). */
 int32_t fgs_preprocess_fwd(const fgs_preprocess_params* p, const fgs_preprocess_fwd_io* io,
                            void* stream);
+
+/* fgs_preprocess_fwd in two halves (the same arguments, the same results):
+ * the geometry half writes every output except rgb and clamped; the colour
+ * half, queued after it (it reads radii), writes rgb and clamped.  The colour
+ * half may run on another stream, ordered after the geometry half by an
+ * event, so that it overlaps the binning that follows on the first stream.
+ * No reference counterpart (the split of fastgs_preprocess.metal:384-484). */
+int32_t fgs_preprocess_geometry_fwd(const fgs_preprocess_params* p,
+                                    const fgs_preprocess_fwd_io* io, void* stream);
+int32_t fgs_preprocess_colour_fwd(const fgs_preprocess_params* p, const fgs_preprocess_fwd_io* io,
+                                  void* stream);
 
 typedef struct {
   /* primals */

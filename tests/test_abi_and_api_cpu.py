@@ -73,7 +73,7 @@ def test_launch_events_argument_checks():
         _lib.FGS_ERR_INVALID_ARGUMENT
     assert b"both" in lib.fgs_last_error()
     for name in (b"preprocess_fwd", b"rasterize_fwd", b"rasterize_bwd", b"preprocess_bwd",
-                 b"loss_fwd", b"loss_bwd"):
+                 b"loss_fwd", b"loss_bwd", b"preprocess_colour"):
         assert lib.fgs_set_launch_events(name, None, None) == _lib.FGS_OK
 
 

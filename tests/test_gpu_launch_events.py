@@ -13,7 +13,7 @@ from tests.helpers import to_torch
 pytestmark = pytest.mark.gpu
 
 NAMES = ("preprocess_fwd", "rasterize_fwd", "rasterize_bwd", "preprocess_bwd", "loss_fwd",
-         "loss_bwd")
+         "loss_bwd", "preprocess_colour")
 
 
 def test_launch_events_bracket_the_main_kernels():
@@ -21,6 +21,9 @@ def test_launch_events_bracket_the_main_kernels():
 
     import fastgs_core
     import fastgs_core_amd
+    from fastgs_core_amd import rasterizer
+
+    assert rasterizer.SPLIT_COLOUR  # the colour kernel runs (on the side stream)
 
     lib = _lib.load()
     W, H = 256, 192
@@ -65,6 +68,10 @@ def test_launch_events_bracket_the_main_kernels():
         assert 0.0 < v < total, (n, v, total)
     # the rasterize forward's kernel runs after the preprocess kernel ends
     assert ev["preprocess_fwd"][1].elapsed_time(ev["rasterize_fwd"][0]) >= 0.0
+    # the colour half starts after the geometry half and ends before the
+    # rasterize forward reads its colours
+    assert ev["preprocess_fwd"][1].elapsed_time(ev["preprocess_colour"][0]) >= 0.0
+    assert ev["preprocess_colour"][1].elapsed_time(ev["rasterize_fwd"][0]) >= 0.0
     # cleared: a further frame leaves the events where they were
     before = ev["rasterize_bwd"][0].elapsed_time(ev["rasterize_bwd"][1])
     run()
