@@ -6,18 +6,17 @@
 // (scripts/train_scanner_fastgs.py:911-966), which the rasterizer's
 // backward consumes as dL/dout_color.
 //
-// Both passes use one wavefront per strip of 64 columns x 32 output rows of
-// one plane, lane l owning column l.  The wavefront walks the strip's 42
+// Both passes use one wavefront per strip of 64 columns x 34 output rows of
+// one plane, lane l owning column l.  The wavefront walks the strip's 44
 // input rows (5-row halo above and below) top to bottom: each row's 74
-// values (5-column halo each side) are staged in LDS (two row buffers, so one
-// barrier per row), the lane blurs its column horizontally and keeps the
-// result for the last 11 rows in a register ring (the row loop is unrolled by
-// 11, so the ring is indexed statically); once 11 rows are in, the vertical
-// blur of the ring gives one output row.  Input rows are loaded 11 rows
-// before they are staged (a second register ring), so a row's global load
-// latency overlaps the work of the rows before it; the one barrier per row
-// orders LDS only, so those loads stay in flight across it.
-//
+// values (5-column halo each side) are staged in LDS (two row buffers; a
+// one-wave workgroup needs no barrier between them, only its LDS ordering),
+// the lane blurs its column horizontally and keeps the result for the last
+// 11 rows in a register ring (rows are taken 11 at a time, so the ring is
+// indexed statically); once 11 rows are in, the vertical blur of the ring
+// gives one output row.  Input rows are loaded 11 rows before they are
+// staged (a second register ring), so a row's load latency overlaps the work
+// of the rows before it.
 // Forward: the five moments x, y, x^2, y^2, xy are blurred; the SSIM value
 // and its partial derivatives with respect to the three blurred moments of x
 // (E[x], E[x^2], E[xy]) are written per pixel, and per-strip partial sums of
@@ -34,10 +33,11 @@
 namespace fgs {
 
 constexpr int kSW = 64;                // strip width: one column per lane
-constexpr int kSH = 32;                // output rows per strip
+constexpr int kSH = 34;                // output rows per strip (kRows = 4 x 11)
 constexpr int kLR = 5;                 // window radius (11 taps)
-constexpr int kRowIn = kSW + 2 * kLR;  // 74 staged values per row
-constexpr int kRows = kSH + 2 * kLR;   // 42 input rows per strip
+constexpr int kRowIn = 2 * kSW;        // staged values per row: 74 used, all lanes write two
+constexpr int kRows = kSH + 2 * kLR;   // 44 input rows per strip
+static_assert(kRows % 11 == 0, "the row loop takes the rows 11 at a time");
 
 struct LossArgs {
   int C, H, W;
@@ -46,14 +46,35 @@ struct LossArgs {
   float win[11];
 };
 
+// Image planes are read and written through raw buffer resources: an
+// offset at or past the resource's size reads 0 and drops a store.  The zero
+// padding of the window and the pixels past the image edge are therefore
+// offsets, not branches, and the rows' loads and stores stay in one
+// straight-line stream whose outstanding counts the compiler can track (a
+// load behind a lane-masked branch made it wait for every load in flight).
+// Plane sizes are checked on the host: H * W * 4 < 2^31.
+constexpr uint32_t kOob = 0x80000000u;
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+__device__ __forceinline__ Rsrc plane_rsrc(const float* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buf_load(Rsrc r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ void buf_store(Rsrc r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)off, 0, 0);
+}
+
 // The lane's staged values of one input row: column c0 - 5 + l and, for
 // l < 10, column c0 + 59 + l; zero outside the image.
-__device__ __forceinline__ void load_row(const float* __restrict__ p, const LossArgs& a, int gr,
-                                         int c0, int l, float& v0, float& v1) {
+__device__ __forceinline__ void load_row(Rsrc p, const LossArgs& a, int gr, int c0, int l,
+                                         float& v0, float& v1) {
   const bool rin = gr >= 0 && gr < a.H;
   const int ca = c0 - kLR + l, cb = c0 - kLR + kSW + l;
-  v0 = (rin && ca >= 0 && ca < a.W) ? p[(size_t)gr * a.W + ca] : 0.0f;
-  v1 = (rin && l < 2 * kLR && cb < a.W) ? p[(size_t)gr * a.W + cb] : 0.0f;
+  const int rowo = gr * a.W;
+  v0 = buf_load(p, (rin && ca >= 0 && ca < a.W) ? (uint32_t)(rowo + ca) * 4u : kOob);
+  v1 = buf_load(p, (rin && l < 2 * kLR && cb < a.W) ? (uint32_t)(rowo + cb) * 4u : kOob);
 }
 
 // Input rows of NM planes loaded 11 rows ahead: row i lives in slot i % 11,
@@ -63,8 +84,8 @@ __device__ __forceinline__ void load_row(const float* __restrict__ p, const Loss
 template <int NM>
 struct RowRing {
   float v0[NM][11], v1[NM][11];
-  __device__ __forceinline__ void fill(const float* const (&p)[NM], const LossArgs& a, int gr0,
-                                       int c0, int l) {
+  __device__ __forceinline__ void fill(const Rsrc (&p)[NM], const LossArgs& a, int gr0, int c0,
+                                       int l) {
 #pragma unroll
     for (int q = 0; q < 11; ++q)
 #pragma unroll
@@ -72,6 +93,7 @@ struct RowRing {
   }
 };
 
+template <bool kMaps>
 __global__ void __launch_bounds__(kSW)
 l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float* __restrict__ tgt,
                    float* __restrict__ dmaps, float* __restrict__ partials) {
@@ -87,81 +109,99 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
   const int c0 = strip * kSW, r0 = chunk * kSH;
   const int gc = c0 + l;
   const size_t HW = (size_t)a.H * a.W;
-  const float* const src[2] = {img + plane * HW, tgt + plane * HW};
+  const uint32_t pb = (uint32_t)HW * 4u;
+  const Rsrc src[2] = {plane_rsrc(img + plane * HW, pb), plane_rsrc(tgt + plane * HW, pb)};
+  const size_t CHW = (size_t)a.C * HW;
+  float* const dbase = kMaps ? dmaps : (float*)img;  // no stores without maps
+  const uint32_t db = kMaps ? pb : 0u;
+  const Rsrc dst[3] = {plane_rsrc(dbase + plane * HW, db), plane_rsrc(dbase + CHW + plane * HW, db),
+                       plane_rsrc(dbase + 2 * CHW + plane * HW, db)};
   const float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
+  const bool col_in = gc < a.W;
   float ring[11][5];
   float ssim_sum = 0.f, l1_sum = 0.f;
   RowRing<2> rq;
   rq.fill(src, a, r0 - kLR, c0, l);
-  for (int base = 0; base < kRows; base += 11) {
+  // input row i, staged from ring slot sl = i % 11; `first` marks the first
+  // 11 rows (i == sl), whose first ten only fill the window
+  auto row = [&](const int i, const int sl, const bool first) __attribute__((always_inline)) {
+    float* sx = s_x[i & 1];
+    float* sy = s_y[i & 1];
+    // every lane writes both values (the second is zero past lane 9), so
+    // the row has no lane-masked branch for the compiler to sink work into
+    sx[l] = rq.v0[0][sl];
+    sy[l] = rq.v0[1][sl];
+    sx[kSW + l] = rq.v1[0][sl];
+    sy[kSW + l] = rq.v1[1][sl];
+    // row i + 11 into the freed slot; past the strip's rows, a row index
+    // outside the image makes the loads read nothing
+    const int pf = i + 11 < kRows ? r0 - kLR + i + 11 : -1;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) load_row(src[m], a, pf, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
+    lds_barrier();
+    float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 11; ++k) {
+      const float x = sx[l + k], y = sy[l + k], w = a.win[k];
+      m0 = __builtin_fmaf(w, x, m0);
+      m1 = __builtin_fmaf(w, y, m1);
+      m2 = __builtin_fmaf(w, x * x, m2);
+      m3 = __builtin_fmaf(w, y * y, m3);
+      m4 = __builtin_fmaf(w, x * y, m4);
+    }
+    ring[sl][0] = m0;
+    ring[sl][1] = m1;
+    ring[sl][2] = m2;
+    ring[sl][3] = m3;
+    ring[sl][4] = m4;
+    // |x - y| of the strip's own pixels, from the staged centre column (zero
+    // outside the image, where both values read zero)
+    const float xc = sx[l + kLR], yc = sy[l + kLR];
+    l1_sum += (i >= kLR && i < kLR + kSH) ? fabsf(xc - yc) : 0.f;
+    if (first && i < 2 * kLR) return;  // compile-time
+    const int orow = r0 + i - 2 * kLR;
+    float mx = 0.f, my = 0.f, exx = 0.f, eyy = 0.f, exy = 0.f;
+#pragma unroll
+    for (int k = 0; k < 11; ++k) {
+      const int q = (sl + 1 + k) % 11;  // ring slot of input row orow - 5 + k
+      const float w = a.win[k];
+      mx = __builtin_fmaf(w, ring[q][0], mx);
+      my = __builtin_fmaf(w, ring[q][1], my);
+      exx = __builtin_fmaf(w, ring[q][2], exx);
+      eyy = __builtin_fmaf(w, ring[q][3], eyy);
+      exy = __builtin_fmaf(w, ring[q][4], exy);
+    }
+    const bool out = orow < a.H && col_in;
+    const float sxx = exx - mx * mx, syy = eyy - my * my, sxy = exy - mx * my;
+    const float A = 2.f * mx * my + C1, Bv = 2.f * sxy + C2;
+    const float Cv = mx * mx + my * my + C1, D = sxx + syy + C2;
+    const float inv = 1.0f / (Cv * D);  // 1/Cv = D inv, 1/D = Cv inv
+    const float S = A * Bv * inv;
+    ssim_sum += out ? S : 0.f;
+    if (kMaps) {
+      // partials w.r.t. mu_x, sigma_xx, sigma_xy, then to the raw moments
+      const float dS_dmu = 2.f * my * Bv * inv - S * 2.f * mx * (D * inv);
+      const float dS_dsxx = -S * (Cv * inv);
+      const float dS_dsxy = 2.f * A * inv;
+      const float d1 = dS_dmu + dS_dsxx * (-2.f * mx) + dS_dsxy * (-my);
+      const uint32_t po = out ? (uint32_t)(orow * a.W + gc) * 4u : kOob;
+      buf_store(dst[0], po, d1);
+      buf_store(dst[1], po, dS_dsxx);
+      buf_store(dst[2], po, dS_dsxy);
+    }
+  };
+  // rows are kept apart in the schedule: interleaving them lengthens
+  // register live ranges past three waves per SIMD
+#pragma unroll
+  for (int sl = 0; sl < 11; ++sl) {
+    row(sl, sl, true);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int base = 11; base < kRows; base += 11) {
 #pragma unroll
     for (int sl = 0; sl < 11; ++sl) {
-      const int i = base + sl;
-      if (i >= kRows) break;  // uniform
-      float* sx = s_x[i & 1];
-      float* sy = s_y[i & 1];
-      sx[l] = rq.v0[0][sl];
-      sy[l] = rq.v0[1][sl];
-      if (l < 2 * kLR) {
-        sx[kSW + l] = rq.v1[0][sl];
-        sy[kSW + l] = rq.v1[1][sl];
-      }
-      if (i + 11 < kRows) {
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-          load_row(src[m], a, r0 - kLR + i + 11, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
-      }
-      lds_barrier();
-      float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
-#pragma unroll
-      for (int k = 0; k < 11; ++k) {
-        const float x = sx[l + k], y = sy[l + k], w = a.win[k];
-        m0 = __builtin_fmaf(w, x, m0);
-        m1 = __builtin_fmaf(w, y, m1);
-        m2 = __builtin_fmaf(w, x * x, m2);
-        m3 = __builtin_fmaf(w, y * y, m3);
-        m4 = __builtin_fmaf(w, x * y, m4);
-      }
-      ring[sl][0] = m0;
-      ring[sl][1] = m1;
-      ring[sl][2] = m2;
-      ring[sl][3] = m3;
-      ring[sl][4] = m4;
-      const float xc = sx[l + kLR], yc = sy[l + kLR];
-      // |x - y| of the strip's own pixels, from the staged centre column
-      const int irow = r0 - kLR + i;
-      if (i >= kLR && i < kLR + kSH && irow < a.H && gc < a.W) l1_sum += fabsf(xc - yc);
-      if (i < 2 * kLR) continue;
-      const int orow = r0 + i - 2 * kLR;
-      float mx = 0.f, my = 0.f, exx = 0.f, eyy = 0.f, exy = 0.f;
-#pragma unroll
-      for (int k = 0; k < 11; ++k) {
-        const int q = (sl + 1 + k) % 11;  // ring slot of input row orow - 5 + k
-        const float w = a.win[k];
-        mx = __builtin_fmaf(w, ring[q][0], mx);
-        my = __builtin_fmaf(w, ring[q][1], my);
-        exx = __builtin_fmaf(w, ring[q][2], exx);
-        eyy = __builtin_fmaf(w, ring[q][3], eyy);
-        exy = __builtin_fmaf(w, ring[q][4], exy);
-      }
-      if (orow >= a.H || gc >= a.W) continue;
-      const float sxx = exx - mx * mx, syy = eyy - my * my, sxy = exy - mx * my;
-      const float A = 2.f * mx * my + C1, Bv = 2.f * sxy + C2;
-      const float Cv = mx * mx + my * my + C1, D = sxx + syy + C2;
-      const float inv = 1.0f / (Cv * D);  // 1/Cv = D inv, 1/D = Cv inv
-      const float S = A * Bv * inv;
-      ssim_sum += S;
-      if (dmaps) {
-        // partials w.r.t. mu_x, sigma_xx, sigma_xy, then to the raw moments
-        const float dS_dmu = 2.f * my * Bv * inv - S * 2.f * mx * (D * inv);
-        const float dS_dsxx = -S * (Cv * inv);
-        const float dS_dsxy = 2.f * A * inv;
-        const float d1 = dS_dmu + dS_dsxx * (-2.f * mx) + dS_dsxy * (-my);
-        const size_t po = (size_t)plane * HW + (size_t)orow * a.W + gc;
-        dmaps[po] = d1;
-        dmaps[(size_t)a.C * HW + po] = dS_dsxx;
-        dmaps[(size_t)2 * a.C * HW + po] = dS_dsxy;
-      }
+      row(base + sl, sl, false);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // strip partial sums (fixed order)
@@ -219,65 +259,73 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
   const int gc = c0 + l;
   const size_t HW = (size_t)a.H * a.W;
   const size_t CHW = (size_t)a.C * HW;
-  const float* const dp[3] = {dmaps + plane * HW, dmaps + CHW + plane * HW,
-                              dmaps + 2 * CHW + plane * HW};
-  const float* __restrict__ xp = img + plane * HW;
-  const float* __restrict__ yp = tgt + plane * HW;
+  const uint32_t pb = (uint32_t)HW * 4u;
+  const Rsrc dp[3] = {plane_rsrc(dmaps + plane * HW, pb), plane_rsrc(dmaps + CHW + plane * HW, pb),
+                      plane_rsrc(dmaps + 2 * CHW + plane * HW, pb)};
+  const Rsrc xp = plane_rsrc(img + plane * HW, pb), yp = plane_rsrc(tgt + plane * HW, pb);
+  const Rsrc gp = plane_rsrc(dimg + plane * HW, pb);
   const float g = grad_out ? grad_out[0] : 1.0f;
   const float inv_n = (float)(1.0 / (double)CHW);
+  const bool col_in = gc < a.W;
   float ring[11][3];
   RowRing<3> rq;
   rq.fill(dp, a, r0 - kLR, c0, l);
   // x, y of the lane's pixel in image row r0 - 5 + i, loaded with input row i
   // into slot i % 11 and used five rows later, when that row is the output
   float qx[11], qy[11];
-  const bool col_in = gc < a.W;
-  for (int base = 0; base < kRows; base += 11) {
+  auto row = [&](const int i, const int sl, const bool first) __attribute__((always_inline)) {
+    float (*sd)[kRowIn] = s_d[i & 1];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      sd[m][l] = rq.v0[m][sl];
+      sd[m][kSW + l] = rq.v1[m][sl];  // zero past lane 9
+    }
+    const int pf = i + 11 < kRows ? r0 - kLR + i + 11 : -1;  // -1: reads nothing
+#pragma unroll
+    for (int m = 0; m < 3; ++m) load_row(dp[m], a, pf, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
+    {
+      const int irow = r0 - kLR + i;
+      const bool in = col_in && i >= kLR && i < kLR + kSH && irow < a.H;
+      const uint32_t o = in ? (uint32_t)(irow * a.W + gc) * 4u : kOob;
+      qx[sl] = buf_load(xp, o);
+      qy[sl] = buf_load(yp, o);
+    }
+    lds_barrier();
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      float h = 0.f;
+#pragma unroll
+      for (int k = 0; k < 11; ++k) h = __builtin_fmaf(a.win[k], sd[m][l + k], h);
+      ring[sl][m] = h;
+    }
+    if (first && i < 2 * kLR) return;  // compile-time
+    const int orow = r0 + i - 2 * kLR;
+    float B[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 11; ++k) {
+      const int q = (sl + 1 + k) % 11;
+#pragma unroll
+      for (int m = 0; m < 3; ++m) B[m] = __builtin_fmaf(a.win[k], ring[q][m], B[m]);
+    }
+    const float x = qx[(sl + 6) % 11], y = qy[(sl + 6) % 11];  // loaded at row i - 5
+    const float d = x - y;
+    const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
+    const float dssim = B[0] + 2.f * x * B[1] + y * B[2];
+    const uint32_t o = (orow < a.H && col_in) ? (uint32_t)(orow * a.W + gc) * 4u : kOob;
+    buf_store(gp, o, g * inv_n * (a.w_l1 * sgn - a.w_ssim * dssim));
+  };
+  // rows are kept apart in the schedule: interleaving them lengthens
+  // register live ranges past three waves per SIMD
+#pragma unroll
+  for (int sl = 0; sl < 11; ++sl) {
+    row(sl, sl, true);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int base = 11; base < kRows; base += 11) {
 #pragma unroll
     for (int sl = 0; sl < 11; ++sl) {
-      const int i = base + sl;
-      if (i >= kRows) break;  // uniform
-      float (*sd)[kRowIn] = s_d[i & 1];
-#pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        sd[m][l] = rq.v0[m][sl];
-        if (l < 2 * kLR) sd[m][kSW + l] = rq.v1[m][sl];
-      }
-      if (i + 11 < kRows) {
-#pragma unroll
-        for (int m = 0; m < 3; ++m)
-          load_row(dp[m], a, r0 - kLR + i + 11, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
-      }
-      {
-        const int irow = r0 - kLR + i;
-        const bool in = col_in && i >= kLR && i < kLR + kSH && irow < a.H;
-        qx[sl] = in ? xp[(size_t)irow * a.W + gc] : 0.0f;
-        qy[sl] = in ? yp[(size_t)irow * a.W + gc] : 0.0f;
-      }
-      lds_barrier();
-#pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        float h = 0.f;
-#pragma unroll
-        for (int k = 0; k < 11; ++k) h = __builtin_fmaf(a.win[k], sd[m][l + k], h);
-        ring[sl][m] = h;
-      }
-      if (i < 2 * kLR) continue;
-      const int orow = r0 + i - 2 * kLR;
-      float B[3] = {0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k = 0; k < 11; ++k) {
-        const int q = (sl + 1 + k) % 11;
-#pragma unroll
-        for (int m = 0; m < 3; ++m) B[m] = __builtin_fmaf(a.win[k], ring[q][m], B[m]);
-      }
-      const float x = qx[(sl + 6) % 11], y = qy[(sl + 6) % 11];  // loaded at row i - 5
-      if (orow >= a.H || !col_in) continue;
-      const size_t o = plane * HW + (size_t)orow * a.W + gc;
-      const float d = x - y;
-      const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
-      const float dssim = B[0] + 2.f * x * B[1] + y * B[2];
-      dimg[o] = g * inv_n * (a.w_l1 * sgn - a.w_ssim * dssim);
+      row(base + sl, sl, false);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -379,14 +427,20 @@ extern "C" int32_t fgs_l1_ssim_fwd(const float* img, const float* tgt, int32_t C
                                    void* workspace, void* stream) {
   if (C <= 0 || H <= 0 || W <= 0)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_l1_ssim_fwd: bad image shape");
+  if ((size_t)H * (size_t)W >= ((size_t)1 << 29))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_l1_ssim_fwd: image plane of 2^29 pixels or more");
   if (!img || !tgt || !loss || !workspace)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_l1_ssim_fwd: null pointer");
   const LossArgs a = make_args(C, H, W, w_l1, w_ssim);
   const int nt = a.strips_x * a.chunks_y;
   hipStream_t st = (hipStream_t)stream;
   if (const int32_t e = launch_mark(kLaunchLossFwd, st, 0)) return e;
-  hipLaunchKernelGGL(l1_ssim_fwd_kernel, dim3(nt, C), dim3(kSW), 0, st, a, img, tgt, dmaps,
-                     (float*)workspace);
+  if (dmaps)
+    hipLaunchKernelGGL(l1_ssim_fwd_kernel<true>, dim3(nt, C), dim3(kSW), 0, st, a, img, tgt, dmaps,
+                       (float*)workspace);
+  else
+    hipLaunchKernelGGL(l1_ssim_fwd_kernel<false>, dim3(nt, C), dim3(kSW), 0, st, a, img, tgt,
+                       dmaps, (float*)workspace);
   if (check_launch("l1_ssim_fwd") != FGS_OK) return FGS_ERR_LAUNCH;
   if (const int32_t e = launch_mark(kLaunchLossFwd, st, 1)) return e;
   hipLaunchKernelGGL(l1_ssim_reduce_kernel, dim3(1), dim3(256), 0, st, (const float*)workspace,
@@ -399,6 +453,8 @@ extern "C" int32_t fgs_l1_ssim_bwd(const float* img, const float* tgt, const flo
                                    float w_l1, float w_ssim, float* dimg, void* stream) {
   if (C <= 0 || H <= 0 || W <= 0)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_l1_ssim_bwd: bad image shape");
+  if ((size_t)H * (size_t)W >= ((size_t)1 << 29))
+    return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_l1_ssim_bwd: image plane of 2^29 pixels or more");
   if (!img || !tgt || !dmaps || !dimg)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_l1_ssim_bwd: null pointer");
   const LossArgs a = make_args(C, H, W, w_l1, w_ssim);

@@ -138,8 +138,17 @@ def _side_stream(dev: torch.device):
     return entry
 
 
+def _start_colour(cfg) -> None:
+    """Queues the colour half of the preprocess on the side stream, after
+    the work queued so far on the current stream."""
+    fn = cfg.pop("colour_launch", None)
+    if fn is not None:
+        fn()
+
+
 def _join_colour(cfg, dev) -> None:
     """Orders the current stream after the colour half of the preprocess."""
+    _start_colour(cfg)
     ev = cfg.get("colour_done")
     if ev is not None:
         torch.cuda.current_stream(dev).wait_event(ev)
@@ -227,21 +236,28 @@ class _Preprocess(torch.autograd.Function):
             with _stage("preprocess_fwd"):
                 _lib.check(lib.fgs_preprocess_geometry_fwd(ctypes.byref(prm), ctypes.byref(io),
                                                            _stream(dev)))
-            side, geo_done, colour_done = _side_stream(dev)
-            geo_done.record(torch.cuda.current_stream(dev))
-            side.wait_event(geo_done)
-            _lib.check(lib.fgs_preprocess_colour_fwd(ctypes.byref(prm), ctypes.byref(io),
-                                                     ctypes.c_void_p(side.cuda_stream)))
-            colour_done.record(side)
-            for t in (means3d, campos, dc, sh, colors_precomp, radii, rgb, clamped):
-                if t is not None:
-                    t.record_stream(side)
-            cfg["colour_done"] = colour_done
+            def launch_colour(prm=prm, io=io, keep=(means3d, campos, dc, sh, colors_precomp,
+                                                    radii, rgb, clamped)):
+                side, start, colour_done = _side_stream(dev)
+                start.record(torch.cuda.current_stream(dev))
+                side.wait_event(start)
+                _lib.check(lib.fgs_preprocess_colour_fwd(ctypes.byref(prm), ctypes.byref(io),
+                                                         ctypes.c_void_p(side.cuda_stream)))
+                colour_done.record(side)
+                for t in keep:
+                    if t is not None:
+                        t.record_stream(side)
+                cfg["colour_done"] = colour_done
+
+            cfg["colour_launch"] = launch_colour
+            if COLOUR_START == "geometry":
+                _start_colour(cfg)
         elif P > 0:
             with _stage("preprocess_fwd"):
                 _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io),
                                                   _stream(dev)))
-        ctx.cfg = dict(cfg, st_base=None, st_masks=None, colour_done=None)  # forward-only
+        ctx.cfg = dict(cfg, st_base=None, st_masks=None, colour_done=None,
+                       colour_launch=None)  # forward-only
         ctx.opacity_shape = (opacity_logits if cfg.get("raw") else opacities).shape
         ctx.sh_shape = None if sh is None else sh.shape
         ctx.save_for_backward(means3d, sh, scales, rotations, cov3d_precomp, viewmatrix,
@@ -609,6 +625,10 @@ _RAW_KEYS = ("log_scales", "raw_rotations", "opacity_logits")
 # rasterize_gaussians runs the preprocess's colour half (the SH colours) on a
 # side stream, where it overlaps the binning; False runs the fused kernel.
 SPLIT_COLOUR = True
+# where the colour half starts on the GPU: right after the geometry half
+# ("geometry"), after the scan of tiles_touched ("scan"), or after the depth
+# sort, once K is known ("depth")
+COLOUR_START = "scan"
 _RG_NAMES = dict(required=("means3d", "background", "opacities", "metric_map", "viewmatrix",
                            "projmatrix", "campos"),
                  col_keys=("colors_precomp", "colors"), rot="rotations", means3d="means3d",
@@ -651,6 +671,8 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     gx, gy = cfg["gx"], cfg["gy"]
     T = gx * gy
     scan_buf = _inclusive_scan_i32(tiles)  # point_offsets, then the scan's wait status
+    if COLOUR_START == "scan":
+        _start_colour(cfg)
     point_offsets = scan_buf[:P]
     # the zero-count metric array is made before the wait for K: the host work
     # between K's arrival and the binning launch is on the GPU's critical path
@@ -658,6 +680,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     background = _to(inputs["background"], dev, torch.float32)
     metric_map = _to(inputs["metric_map"], dev, torch.int32)
     K, depth_ws = _count_and_depth_order(scan_buf, depths.detach(), tiles)
+    _start_colour(cfg)
     point_list_keys = point_list = ranges = bucket_count = bucket_offsets = None
     bucket_to_tile = sampled_t = sampled_ar = final_t = n_contrib = max_contrib = None
     pixel_colors = out_color = None
