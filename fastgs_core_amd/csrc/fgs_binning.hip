@@ -1052,14 +1052,17 @@ l1_top_scan_kernel(int S, uint32_t* __restrict__ segsum, uint32_t* __restrict__ 
 // super-tile set gets mask 0, filled in by l1_wide_masks_kernel (every real
 // pair has at least one tile, so 0 marks exactly those).
 constexpr int kL1Pairs = 2048;  // LDS pair capacity per round
+template <bool kCarry>
 __global__ void __launch_bounds__(kL1Group)
 l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
-                const uint32_t* __restrict__ recw, const uint64_t* __restrict__ sets,
-                const uint32_t* __restrict__ cnt1, const uint32_t* __restrict__ segsum,
-                const uint32_t* __restrict__ st_start, int64_t cap, uint32_t* __restrict__ list,
-                uint64_t* __restrict__ masks) {
+                const uint32_t* __restrict__ skeys, const uint32_t* __restrict__ recw,
+                const uint64_t* __restrict__ sets, const uint32_t* __restrict__ cnt1,
+                const uint32_t* __restrict__ segsum, const uint32_t* __restrict__ st_start,
+                int64_t cap, uint32_t* __restrict__ list, uint64_t* __restrict__ masks,
+                uint32_t* __restrict__ ldb) {
   __shared__ uint64_t s_pm[kL1Pairs];  // mask of each pair (0: walk it)
   __shared__ uint32_t s_pg[kL1Pairs];  // Gaussian of each pair
+  __shared__ uint32_t s_pd[kCarry ? kL1Pairs : 1];  // kCarry: its depth bits (sorted key)
   __shared__ uint8_t s_ps[kL1Pairs];   // super-tile of each pair
   __shared__ uint32_t s_wh[kWavesPerBlock][kMaxSt];
   __shared__ uint32_t s_base[kMaxSt];
@@ -1069,7 +1072,7 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
   const int w = t / kWave;
   const int i = (int)blockIdx.x * kL1Group + t;
   uint64_t m[4] = {0ull, 0ull, 0ull, 0ull};
-  uint32_t g = 0, rw = 0;
+  uint32_t g = 0, rw = 0, db = 0;
   if (i < P) {
     const uint4* src = reinterpret_cast<const uint4*>(sets + 4 * (size_t)i);
     const uint4 a = src[0], b = src[1];
@@ -1079,6 +1082,7 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
     m[3] = (uint64_t)b.z | ((uint64_t)b.w << 32);
     g = order[i];
     rw = recw[i];
+    if (kCarry) db = skeys[i];
   }
   const int rows = (int)((gridDim.x + kL1Segs - 1) / kL1Segs);
   const int seg = (int)blockIdx.x / rows;
@@ -1109,6 +1113,7 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
         if (p >= r0 && p < r0 + kL1Pairs) {
           s_ps[p - r0] = (uint8_t)sid;
           s_pg[p - r0] = g;
+          if (kCarry) s_pd[p - r0] = db;
           s_pm[p - r0] = m[k];
         }
         ++p;
@@ -1123,6 +1128,7 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
           if (p >= r0 && p < r0 + kL1Pairs) {
             s_ps[p - r0] = (uint8_t)(64 * wd + k);
             s_pg[p - r0] = g;
+            if (kCarry) s_pd[p - r0] = db;
             s_pm[p - r0] = 0ull;
           }
           ++p;
@@ -1154,6 +1160,7 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
         if ((int64_t)pos < cap) {
           list[pos] = s_pg[q];
           masks[pos] = s_pm[q];
+          if (kCarry) ldb[pos] = s_pd[q];
         }
       }
       __syncthreads();
@@ -1385,14 +1392,15 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
 constexpr int kL2Stage = 4608;
 constexpr int kL2PerLane = kL2Chunk / kWave;  // 8 entries per lane on the tile-by-tile path
 static_assert(kL2Stage >= 2 * kL2Chunk, "the tile-by-tile path stages a chunk in the stage arrays");
+template <bool kCarry>
 __global__ void __launch_bounds__(kL1Group)
 l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
                const uint32_t* __restrict__ st_start, const uint32_t* __restrict__ chunk_first,
                const uint32_t* __restrict__ chunk_st, const uint32_t* __restrict__ nchunks,
                const uint64_t* __restrict__ masks, const uint32_t* __restrict__ cnt2,
                const uint32_t* __restrict__ base2, const uint32_t* __restrict__ tile_start,
-               int32_t P, const float* __restrict__ depths, int64_t K,
-               uint64_t* __restrict__ keys, uint32_t* __restrict__ point_list) {
+               int32_t P, const float* __restrict__ depths, const uint32_t* __restrict__ ldb,
+               int64_t K, uint64_t* __restrict__ keys, uint32_t* __restrict__ point_list) {
   __shared__ __align__(16) uint32_t s_g[kL2Stage];
   __shared__ __align__(16) uint32_t s_db[kL2Stage];
   __shared__ uint32_t s_wc[kWavesPerBlock][kWave];
@@ -1424,7 +1432,8 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
       s_m[q] = m;
       s_db[q] = g;
       s_db[kL2Chunk + q] =
-          (m != 0ull && g < (uint32_t)P) ? __float_as_uint(depths[g]) : 0xFFFFFFFFu;
+          kCarry ? (valid ? ldb[e] : 0xFFFFFFFFu)
+                 : ((m != 0ull && g < (uint32_t)P) ? __float_as_uint(depths[g]) : 0xFFFFFFFFu);
     }
     __syncthreads();
     uint64_t em[kL2PerLane];
@@ -1479,7 +1488,7 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
     if (e < q1) {
       m = masks[e];
       g = list[e];
-      db = g < (uint32_t)P ? __float_as_uint(depths[g]) : 0xFFFFFFFFu;
+      db = kCarry ? ldb[e] : (g < (uint32_t)P ? __float_as_uint(depths[g]) : 0xFFFFFFFFu);
     }
     // lane j: the round's entries having tile j (bit i = entry i).  Lane j
     // walks them in entry (depth) order and fetches each entry's index and
@@ -1587,9 +1596,17 @@ static BinningLayout binning_layout(int32_t P, int64_t K, int32_t T) {
 }
 
 // Workspace of the two-level path (sized for kMaxSt super-tiles).
+// The list entries' depth bits: above this many Gaussians, l1_place writes
+// each entry's depth bits (its sorted key) beside it and l2_emit reads them
+// in list order; below, l2_emit gathers depths[g], whose array then stays in
+// the L2 cache (at 1M Gaussians carrying them measured slower, at 3M the
+// gather fetched about 1.1 GB per frame).
+constexpr int32_t kCarryDepthMinP = 1 << 21;
+static inline bool carry_depth_bits(int32_t P) { return P > kCarryDepthMinP; }
+
 struct TwoLevelLayout {
-  size_t recw, sets, cnt1, segsum, st_start, chunk_first, nchunks, chunk_st, list, masks, cnt2,
-      base2, tile_total, tile_start, total;
+  size_t recw, sets, cnt1, segsum, st_start, chunk_first, nchunks, chunk_st, list, masks, ldb,
+      cnt2, base2, tile_total, tile_start, total;
   int64_t max_chunks;
 };
 
@@ -1608,6 +1625,7 @@ static TwoLevelLayout two_level_layout(int32_t P, int64_t K, int32_t T) {
   L.chunk_st = o; o += al((size_t)L.max_chunks * 4);
   L.list = o; o += al((size_t)K * 4);
   L.masks = o; o += al((size_t)K * 8);
+  L.ldb = o; o += carry_depth_bits(P) ? al((size_t)K * 4) : 0;
   L.cnt2 = o; o += al((size_t)L.max_chunks * kWave * 4);
   L.base2 = o; o += al((size_t)L.max_chunks * kWave * 4);
   L.tile_total = o; o += al((size_t)T * 4);
@@ -1853,8 +1871,15 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
                        cnt1, segsum);
     hipLaunchKernelGGL(l1_top_scan_kernel, dim3(1), dim3(kMaxSt), 0, st, sg.S, segsum, st_start,
                        chunk_first, chunk_st, nchunks, L.max_chunks);
-    hipLaunchKernelGGL(l1_place_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order, recw,
-                       sets, cnt1, segsum, st_start, K, list, masks);
+    const bool carry = carry_depth_bits(P);
+    const uint32_t* skeys = (const uint32_t*)(dws + depth_layout(P).dkeys_s);
+    uint32_t* ldb = carry ? (uint32_t*)(ws + L.ldb) : nullptr;
+    if (carry)
+      hipLaunchKernelGGL(l1_place_kernel<true>, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order,
+                         skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
+    else
+      hipLaunchKernelGGL(l1_place_kernel<false>, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order,
+                         skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
     hipLaunchKernelGGL(l1_wide_masks_kernel, dim3(kWideGroups), dim3(256), 0, st, sg, io->mult,
                        st_start, P, io->xys, io->conic_opacity, list, K, masks);
     const unsigned nch = (unsigned)L.max_chunks;
@@ -1864,9 +1889,14 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
                        base2, tile_total, L.max_chunks);
     hipLaunchKernelGGL(l2_tile_scan_kernel, dim3(1), dim3(1024), 0, st, T, tile_total, tile_start,
                        io->ranges, io->bucket_count, io->bucket_offsets, ww);
-    hipLaunchKernelGGL(l2_emit_kernel, dim3(nch), dim3(kL1Group), 0, st, sg, list, st_start,
-                       chunk_first, chunk_st, nchunks, masks, cnt2, base2, tile_start, P,
-                       io->depths, K, io->point_list_keys, io->point_list);
+    if (carry)
+      hipLaunchKernelGGL(l2_emit_kernel<true>, dim3(nch), dim3(kL1Group), 0, st, sg, list,
+                         st_start, chunk_first, chunk_st, nchunks, masks, cnt2, base2, tile_start,
+                         P, io->depths, ldb, K, io->point_list_keys, io->point_list);
+    else
+      hipLaunchKernelGGL(l2_emit_kernel<false>, dim3(nch), dim3(kL1Group), 0, st, sg, list,
+                         st_start, chunk_first, chunk_st, nchunks, masks, cnt2, base2, tile_start,
+                         P, io->depths, ldb, K, io->point_list_keys, io->point_list);
     return check_launch("binning_sorted (two-level)");
   }
   const BinningLayout L = binning_layout(P < 1 ? 1 : P, K < 1 ? 1 : K, T);
