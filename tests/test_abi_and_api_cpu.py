@@ -77,6 +77,19 @@ def test_launch_events_argument_checks():
         assert lib.fgs_set_launch_events(name, None, None) == _lib.FGS_OK
 
 
+def test_loss_rejects_oversized_planes():
+    """The SSIM kernels address a plane through a buffer resource whose byte
+    offsets must stay below 2^31: planes of 2^29 pixels or more are rejected
+    before any pointer is read or any kernel launched."""
+    lib = _lib.load()
+    for fn, args in (("fgs_l1_ssim_fwd", (None, None, 3, 1 << 15, 1 << 14, 1.0, 0.2, None, None,
+                                         None, None)),
+                     ("fgs_l1_ssim_bwd", (None, None, None, None, 3, 1 << 14, 1 << 15, 1.0, 0.2,
+                                         None, None))):
+        assert getattr(lib, fn)(*args) == _lib.FGS_ERR_INVALID_ARGUMENT, fn
+        assert b"2^29" in lib.fgs_last_error(), fn
+
+
 def test_api_raw_parameters_exclusive():
     """The raw training parameters replace the activated ones; both at once is
     an error raised before any GPU work."""
