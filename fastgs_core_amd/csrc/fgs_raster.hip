@@ -698,7 +698,10 @@ extern "C" int32_t fgs_rasterize_fwd(const fgs_raster_params* p, const fgs_raste
     span(io->pixel_colors + 3 * HW, (C - 3) * HW);
     span(io->out_color + 3 * HW, (C - 3) * HW);
   }
-  if (p->bucket_sum > 0) span(io->bucket_to_tile, p->bucket_sum);
+  // Every tile the kernel renders writes its own buckets (bucket_offsets
+  // partitions [0, B)), so bucket_to_tile needs clearing only when some tiles
+  // are not rendered; entries past B (a caller's upper bound) are its to cut.
+  if (p->bucket_sum > 0 && tiles < p->num_tiles) span(io->bucket_to_tile, p->bucket_sum);
   if (tiles < gx * gy) {
     // Pixels of tiles beyond num_tiles are never rendered: clear them.
     span(io->final_t, HW);

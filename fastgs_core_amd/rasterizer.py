@@ -401,18 +401,24 @@ class _Rasterize(torch.autograd.Function):
 # ---------------------------------------------------------------------------
 # stage helpers shared by the public functions
 # ---------------------------------------------------------------------------
-def _inclusive_scan_i32(x: torch.Tensor) -> torch.Tensor:
+def _inclusive_scan_i32(x: torch.Tensor, side=None) -> torch.Tensor:
     """Inclusive scan of x into the first n words of an (n + 1)-word buffer; the
     last word receives the scan's wait status, so one copy of the final two
-    words reads the total and the status together."""
+    words reads the total and the status together.  side: a stream that has
+    waited for x, to run the scan on (the buffers are allocated on the current
+    stream and marked as used by side)."""
     lib = _lib.load()
     n = x.numel()
     buf = torch.empty(n + 1, dtype=torch.int32, device=x.device)
     ws = torch.empty(int(lib.fgs_scan_workspace_bytes(max(n, 1))), dtype=torch.uint8,
                      device=x.device)
+    if side is not None:
+        for t in (x, buf, ws):
+            t.record_stream(side)
+    stream = ctypes.c_void_p(side.cuda_stream) if side is not None else _stream(x.device)
     with _stage("scan"):
         _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(buf[:n]) if n else None, n, _p(ws),
-                                              _p(buf[n:]), _stream(x.device)))
+                                              _p(buf[n:]), stream))
     return buf
 
 
@@ -493,7 +499,7 @@ def _wait_read(pending):
     return v, st
 
 
-def _count_and_depth_order(scan_buf, depths, tiles):
+def _count_and_depth_order(scan_buf, depths, tiles, pending=None):
     """K = point_offsets[P-1] (binding.cpp:153-154), read with the scan's wait
     status, and the depth order of the Gaussians, the first stage of the
     binning.  The depth sort needs only P, so it is queued between the copy of
@@ -503,7 +509,8 @@ def _count_and_depth_order(scan_buf, depths, tiles):
         return 0, None
     lib = _lib.load()
     dev = tiles.device
-    pending = _read_async(scan_buf, P - 1)
+    if pending is None:  # else the copy is already queued (on the side stream)
+        pending = _read_async(scan_buf, P - 1)
     dws = torch.empty(int(lib.fgs_depth_order_workspace_bytes(P)), dtype=torch.uint8, device=dev)
     with _stage("binning"):
         _lib.check(lib.fgs_depth_order(P, _p(depths), _p(tiles), _p(dws), _stream(dev)))
@@ -629,6 +636,9 @@ SPLIT_COLOUR = True
 # ("geometry"), after the scan of tiles_touched ("scan"), or after the depth
 # sort, once K is known ("depth")
 COLOUR_START = "scan"
+# with the colour half split off, the scan of tiles_touched and the copy of K
+# also run on the side stream, before the colour half
+SCAN_ON_SIDE = True
 _RG_NAMES = dict(required=("means3d", "background", "opacities", "metric_map", "viewmatrix",
                            "projmatrix", "campos"),
                  col_keys=("colors_precomp", "colors"), rot="rotations", means3d="means3d",
@@ -670,16 +680,29 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     P = xys.shape[0]
     gx, gy = cfg["gx"], cfg["gy"]
     T = gx * gy
-    scan_buf = _inclusive_scan_i32(tiles)  # point_offsets, then the scan's wait status
-    if COLOUR_START == "scan":
-        _start_colour(cfg)
+    pending_k = None
+    if cfg.get("colour_launch") is not None and SCAN_ON_SIDE and P > 0:
+        # the scan and the copy of K on the side stream, then the colour half:
+        # the launch stream goes straight on to the depth sort, which needs
+        # only the geometry
+        side, start, _ = _side_stream(dev)
+        start.record(torch.cuda.current_stream(dev))
+        side.wait_event(start)
+        scan_buf = _inclusive_scan_i32(tiles, side)  # point_offsets, then the wait status
+        with torch.cuda.stream(side):
+            pending_k = _read_async(scan_buf, P - 1)
+            _start_colour(cfg)
+    else:
+        scan_buf = _inclusive_scan_i32(tiles)  # point_offsets, then the scan's wait status
+        if COLOUR_START == "scan":
+            _start_colour(cfg)
     point_offsets = scan_buf[:P]
     # the zero-count metric array is made before the wait for K: the host work
     # between K's arrival and the binning launch is on the GPU's critical path
     metric_count = torch.zeros(P if get_flag else 0, dtype=torch.int32, device=dev)
     background = _to(inputs["background"], dev, torch.float32)
     metric_map = _to(inputs["metric_map"], dev, torch.int32)
-    K, depth_ws = _count_and_depth_order(scan_buf, depths.detach(), tiles)
+    K, depth_ws = _count_and_depth_order(scan_buf, depths.detach(), tiles, pending_k)
     _start_colour(cfg)
     point_list_keys = point_list = ranges = bucket_count = bucket_offsets = None
     bucket_to_tile = sampled_t = sampled_ar = final_t = n_contrib = max_contrib = None
