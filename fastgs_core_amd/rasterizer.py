@@ -691,7 +691,8 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
         scan_buf = _inclusive_scan_i32(tiles, side)  # point_offsets, then the wait status
         with torch.cuda.stream(side):
             pending_k = _read_async(scan_buf, P - 1)
-            _start_colour(cfg)
+            if COLOUR_START == "scan":
+                _start_colour(cfg)
     else:
         scan_buf = _inclusive_scan_i32(tiles)  # point_offsets, then the scan's wait status
         if COLOUR_START == "scan":
