@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 
 class PreprocessParams(Structure):
@@ -56,7 +56,7 @@ class BinningIO(Structure):
     ] + [(n, c_void_p) for n in (
         "xys", "depths", "conic_opacity", "tiles_touched", "point_list_keys", "point_list",
         "ranges", "bucket_count", "bucket_offsets", "workspace", "depth_order", "st_base",
-        "st_masks", "wait_status")]
+        "st_masks", "wait_status", "host_result")]
 
 
 class RasterParams(Structure):

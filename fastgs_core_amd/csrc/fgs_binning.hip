@@ -791,15 +791,26 @@ __global__ void bucket_count_kernel(int32_t T, const uint32_t* __restrict__ rang
 struct WaitWords {
   const uint32_t* w[3];
   uint32_t* out;
+  uint64_t* host;  // NULL, or host memory for (status << 32) | B
 };
-__device__ __forceinline__ void report_waits(const WaitWords& ww) {
-  if (threadIdx.x == 0 && ww.out) {
-    uint32_t v = 0u;
+// The OR of the waits' words (thread 0; 0 elsewhere), written to ww.out.
+__device__ __forceinline__ uint32_t report_waits(const WaitWords& ww) {
+  uint32_t v = 0u;
+  if (threadIdx.x == 0) {
 #pragma unroll
     for (int k = 0; k < 3; ++k)
       if (ww.w[k]) v |= __hip_atomic_load(ww.w[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *ww.out = v;
+    if (ww.out) *ww.out = v;
   }
+  return v;
+}
+// Thread 0: the wait status and B to the caller's host word, as one 64-bit
+// store at system scope (it reaches host memory as one write, so the host,
+// polling the word, sees both halves together).
+__device__ __forceinline__ void report_host(const WaitWords& ww, uint32_t status, uint32_t B) {
+  if (threadIdx.x == 0 && ww.host)
+    __hip_atomic_store(ww.host, ((uint64_t)status << 32) | (uint64_t)B, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Bucket counts (ceil(n / 32) per tile) and their inclusive scan, by one
@@ -809,7 +820,7 @@ bucket_scan_kernel(int32_t T, const uint32_t* __restrict__ ranges,
                    uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets,
                    WaitWords ww) {
   __shared__ uint32_t s_tmp[1024 / kWave + 1];
-  report_waits(ww);
+  const uint32_t status = report_waits(ww);
   uint32_t carry = 0;
   for (int base = 0; base < T; base += 1024) {
     const int t = base + (int)threadIdx.x;
@@ -824,6 +835,7 @@ bucket_scan_kernel(int32_t T, const uint32_t* __restrict__ ranges,
     if (t < T) bucket_offsets[t] = carry + ex + c;
     carry += total;
   }
+  report_host(ww, status, carry);
 }
 
 // ---------------------------------------------------------------------------
@@ -1319,7 +1331,7 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
                     uint32_t* __restrict__ bucket_count, uint32_t* __restrict__ bucket_offsets,
                     WaitWords ww) {
   __shared__ uint32_t s_tmp[1024 / kWave + 1];
-  report_waits(ww);
+  const uint32_t status = report_waits(ww);
   __shared__ uint32_t s_v[kTileLds];
   const int t = (int)threadIdx.x;
   const int t0 = t * kTilesPer;
@@ -1371,6 +1383,7 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
     const int idx = i * 1024 + t;
     if (idx < T) bucket_offsets[idx] = s_v[tpad(idx)];
   }
+  if (T > 0) report_host(ww, status, s_v[tpad(T - 1)]);
 }
 
 // Level 2e: every entry's tiles written at tile start + entries of the tile
@@ -1832,6 +1845,7 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
   char* ws = (char*)io->workspace;
   WaitWords ww{};
   ww.out = io->wait_status;
+  ww.host = io->host_result;
   if (io->depth_order) ww.w[0] = depth_err_word((const char*)io->depth_order, P);
   else if (K > 0 && P > 0) ww.w[0] = depth_err_word(ws, P);
   // Gaussians by depth bits: from the caller's depth workspace, or sorted here

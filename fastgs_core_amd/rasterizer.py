@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import time
 from typing import Any, Dict, Optional
 
 import numpy as np
@@ -425,7 +426,7 @@ def _inclusive_scan_i32(x: torch.Tensor, side=None) -> torch.Tensor:
 def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: float,
                     depth_ws: Optional[torch.Tensor] = None,
                     st_base: Optional[torch.Tensor] = None,
-                    st_masks: Optional[torch.Tensor] = None):
+                    st_masks: Optional[torch.Tensor] = None, host_word=None):
     lib = _lib.load()
     dev = xys.device
     P = xys.shape[0]
@@ -440,7 +441,8 @@ def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: f
     ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
     io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
                         _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws),
-                        _p(depth_ws), _p(st_base), _p(st_masks), _p(tbuf[4 * T:]))
+                        _p(depth_ws), _p(st_base), _p(st_masks), _p(tbuf[4 * T:]),
+                        _p(host_word[0]) if host_word is not None else None)
     with _stage("binning"):
         _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
     return keys, plist, ranges, bucket_count, bucket_offsets, tbuf
@@ -489,6 +491,49 @@ def _read_async(buf: torch.Tensor, i: int):
     host.copy_(buf[i:i + 2], non_blocking=True)
     ev.record(torch.cuda.current_stream(buf.device))
     return host, view, ev
+
+
+class _HostWords:
+    """Pinned 64-bit words the binning writes (status << 32) | B into."""
+
+    def __init__(self):
+        self.free = []
+
+
+_HOST_WORDS = _HostWords()
+_HOST_SENTINEL = -1  # low half 0xFFFFFFFF: not written yet
+
+
+def _host_word():
+    """A pinned word set to the sentinel, for fgs_binning_io.host_result."""
+    if _HOST_WORDS.free:
+        word = _HOST_WORDS.free.pop()
+    else:
+        t = torch.empty(1, dtype=torch.int64, pin_memory=True)
+        word = (t, t.numpy())
+    word[1][0] = _HOST_SENTINEL
+    return word
+
+
+def _poll_host_word(word, dev, timeout_s: float = 5.0):
+    """(B, status) once the device has written the word.  The value lands
+    before the binning's last kernel runs, so the host rarely spins; a word
+    still unwritten after timeout_s is read again after the stream has
+    drained, then reported as an error."""
+    view = word[1]
+    v = int(view[0])
+    if (v & 0xFFFFFFFF) == 0xFFFFFFFF:
+        t0 = time.perf_counter()
+        while (v & 0xFFFFFFFF) == 0xFFFFFFFF:
+            if time.perf_counter() - t0 > timeout_s:
+                torch.cuda.current_stream(dev).synchronize()
+                v = int(view[0])
+                if (v & 0xFFFFFFFF) == 0xFFFFFFFF:
+                    raise RuntimeError("fgs_binning_sorted did not write its host result")
+                break
+            v = int(view[0])
+    _HOST_WORDS.free.append(word)
+    return v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF
 
 
 def _wait_read(pending):
@@ -639,6 +684,8 @@ COLOUR_START = "scan"
 # with the colour half split off, the scan of tiles_touched and the copy of K
 # also run on the side stream, before the colour half
 SCAN_ON_SIDE = True
+# B read from a pinned word the binning writes (no copy on the launch stream)
+HOST_B = True
 _RG_NAMES = dict(required=("means3d", "background", "opacities", "metric_map", "viewmatrix",
                            "projmatrix", "campos"),
                  col_keys=("colors_precomp", "colors"), rot="rotations", means3d="means3d",
@@ -710,11 +757,15 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
     pixel_colors = out_color = None
     B = 0
     if K > 0:
+        ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
+        # B without a copy: the binning writes it (with its wait status) into
+        # a pinned host word, read after the rasterize launch
+        host_word = _host_word() if (HOST_B and not ws and T > 0) else None
         with torch.no_grad():
             (point_list_keys, point_list, ranges, bucket_count, bucket_offsets,
              tbuf) = _binning_sorted(xys.detach(), depths.detach(), conic.detach(), tiles, K, gx,
-                                     gy, float(mult), depth_ws, cfg["st_base"], cfg["st_masks"])
-        ws = WRITE_SAMPLED_STATE if write_sampled is None else bool(write_sampled)
+                                     gy, float(mult), depth_ws, cfg["st_base"], cfg["st_masks"],
+                                     host_word)
         if ws:
             # the sampled state is B * 256 entries: B is needed before the launch
             B, status = _value_and_status(tbuf, 4 * T - 1)
@@ -725,7 +776,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
             # is sized by that bound and cut to B once the value arrives, which
             # is waited for after the rasterize launch (with the binning's wait
             # status, the word after it)
-            pending_b = _read_async(tbuf, 4 * T - 1)
+            pending_b = host_word if host_word is not None else _read_async(tbuf, 4 * T - 1)
             B = (K + 31 * T) // 32
         if B > 0:
             rcfg = dict(W=cfg["W"], H=cfg["H"], C=3, T=T, B=B, get_flag=bool(get_flag),
@@ -736,7 +787,8 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
                 rcfg, ranges, point_list, bucket_offsets, xys, rgb, conic, background, radii,
                 metric_map, metric_count, vsp_out)
         if pending_b is not None:
-            B, status = _wait_read(pending_b)
+            B, status = (_poll_host_word(pending_b, dev) if host_word is not None
+                         else _wait_read(pending_b))
             check_wait(status, "rasterize_gaussians_forward (binning)")
             if bucket_to_tile is not None:
                 bucket_to_tile = bucket_to_tile[:B]

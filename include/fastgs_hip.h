@@ -307,6 +307,14 @@ typedef struct {
    * of its own waits and of the depth order it consumes (depth_order, or the
    * one it runs itself), after them in stream order. */
   uint32_t* wait_status;
+  /* NULL, or host memory the device can write (pinned) for one 64-bit word
+   * (no reference counterpart: the read of B at binding.cpp:209-212 without
+   * a copy).  When num_tiles > 0 the call's bucket scan writes
+   * (wait status << 32) | B there, B = bucket_offsets[T-1], as one store at
+   * system scope, once both are known (before the call's last kernel).  The
+   * caller sets the word to a value whose low half is 0xFFFFFFFF first and
+   * reads it once it has changed. */
+  uint64_t* host_result;
 } fgs_binning_io;
 
 size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, int32_t num_tiles);
