@@ -46,35 +46,48 @@ __device__ __forceinline__ float det_expf(float x) {
   return __builtin_ldexpf(p, (int)n);
 }
 
-// exp of a blend exponent (the rasterizer's G = exp(power), power <= 0 where
-// it is used): 2^t with t = x*log2(e) rounded to float, n = floor(t) and
-// f = t - n (exact) in [0, 1); 2^f = 1 + f*q(f), q of degree 4 fitted to the
-// relative error at 400 Chebyshev nodes on [0, 1] (iteratively reweighted
-// least squares), Horner with fused multiply-adds; scaled by ldexp.  x is
-// clamped at -87.  Relative error at most 2e-7 (the polynomial) + 0.35 ulp(t)
-// + 1.34e-8 |x| (t's rounding and log2(e)'s): below 4.3e-7 on [-5.5, 0],
-// where alpha >= 1/255 can hold for opacity <= 1.  Eleven instructions
-// against det_expf's fourteen; used by the rasterizer's forward and backward,
-// which decide from the same value.
-__device__ __forceinline__ float blend_expf(float x) {
-  x = fmaxf(x, -87.0f);
-  const float t = x * 1.44269504088896341f;
-  const float n = floorf(t);
-  const float f = t - n;
+// log2(e) rounded to float.
+constexpr float kLog2e = 1.44269504088896341f;
+
+// The rasterizer's blend exponent is kept in base 2: G = exp(power) =
+// 2^t with t = log2(e) power.  log2(e) enters the splat's conic coefficients
+// once per splat (splat_log2_coeffs), so no pixel multiplies by it.
+//
+// 2^t for t <= 0 where it is used: t is clamped at -126, n = floor(t) and
+// f = min(t - floor(t), 0x1.fffffep-1) in [0, 1), which are what
+// v_cvt_flr_i32_f32 and v_fract_f32 return (checked against floorf and the
+// IEEE subtraction for every float in [-126, 8]); 2^f = 1 + f*q(f), q of
+// degree 4 fitted to the relative error at 400 Chebyshev nodes on [0, 1]
+// (iteratively reweighted least squares), Horner with fused multiply-adds;
+// scaled by ldexp.  Relative error at most 2e-7 against 2^t.  Nine
+// instructions; used by the rasterizer's forward and backward, which decide
+// from the same value.
+__device__ __forceinline__ float blend_exp2f(float t) {
+  t = fmaxf(t, -126.0f);
+  const float f = __builtin_amdgcn_fractf(t);
+  int n;
+  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(n) : "v"(t));
   float q = 0x1.e86492p-10f;
   q = __builtin_fmaf(q, f, 0x1.279248p-7f);
   q = __builtin_fmaf(q, f, 0x1.c925b2p-5f);
   q = __builtin_fmaf(q, f, 0x1.ebd92ep-3f);
   q = __builtin_fmaf(q, f, 0x1.62e4d4p-1f);
-  return __builtin_ldexpf(__builtin_fmaf(f, q, 1.0f), (int)n);
+  return __builtin_ldexpf(__builtin_fmaf(f, q, 1.0f), n);
 }
 
-// Exponent of a splat at offset (dx, dy) from its centre, from the conic
-// (a, b, c) as A = -a/2, B = -b, C = -c/2 (each exact): power =
-// A dx^2 + B dx dy + C dy^2, evaluated as fma(dy, fma(C, dy, B dx), (A dx) dx)
-// so that per splat B dx and (A dx) dx can be kept and every pixel row costs
-// two fused multiply-adds.  Absolute error at most 3 * 2^-24 (|A| dx^2 +
-// |B dx dy| + |C| dy^2).
+// Base-2 exponent coefficients of a splat with conic (a, b, c):
+// A = (-a/2) log2(e), B = -b log2(e), C = (-c/2) log2(e), one rounding each,
+// so that t = A dx^2 + B dx dy + C dy^2 = log2(e) power.
+__device__ __forceinline__ float3 splat_log2_coeffs(float a, float b, float c) {
+  return make_float3((-0.5f * a) * kLog2e, -b * kLog2e, (-0.5f * c) * kLog2e);
+}
+
+// Exponent of a splat at offset (dx, dy) from its centre, from the
+// coefficients (A, B, C) of splat_log2_coeffs: t = A dx^2 + B dx dy + C dy^2,
+// evaluated as fma(dy, fma(C, dy, B dx), (A dx) dx) so that per splat B dx
+// and (A dx) dx can be kept and every pixel row costs two fused
+// multiply-adds.  Absolute error at most 3 * 2^-24 (|A| dx^2 + |B dx dy| +
+// |C| dy^2), plus the coefficients' roundings (2^-24 relative each).
 __device__ __forceinline__ float splat_power_rows(float Bdx, float Adxdx, float C, float dy) {
   return __builtin_fmaf(dy, __builtin_fmaf(C, dy, Bdx), Adxdx);
 }

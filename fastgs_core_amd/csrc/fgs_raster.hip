@@ -59,13 +59,14 @@ __device__ __forceinline__ void stage_splat(uint32_t g, uint32_t P, const float*
 // Rows [lo, hi] outside which no pixel of a splat can reach alpha >= 1/255.
 // alpha >= 1/255 needs o*exp(power) >= 1/255, i.e. q(d) = d^T Conic d <= tau =
 // 2 ln(255 o).  The row extent of {q <= tau} is sqrt(tau * a / det).  Margins:
-// the float power of a pixel (splat_power) differs from -q/2 by at most
-// 3 * 2^-24 (a dx^2 + c dy^2) <= 1.8e-7 q (1 + |rho|) / (1 - |rho|) < 8e-4 q
-// for the conics culled here (det > 1e-3 a c, rho = b / sqrt(a c)); the exp
-// (blend_expf, relative error < 4.3e-7 on [-5.5, 0]), the hardware log and
-// the product o*G move the threshold by ~1e-6; det loses at most ~6e-5 to
-// cancellation.  tau' = 1.01 tau + 0.05 and hy * 1.001 + 0.25 px cover all of
-// these several times over.  Ill-conditioned or non-positive conics, NaN
+// the float base-2 exponent of a pixel (splat_power on splat_log2_coeffs)
+// differs from t = -log2(e) q/2 by at most (4 * 2^-24 + 1.4e-8) log2(e)
+// (a dx^2/2 + |b dx dy| + c dy^2/2) <= 2.6e-7 |t| (1 + |rho|) / (1 - |rho|),
+// under 1.1e-3 |t| for the conics culled here (det > 1e-3 a c, rho =
+// b / sqrt(a c)); the exp (blend_exp2f, relative error < 2e-7), the hardware
+// log and the product o*G move the threshold by ~1e-6; det loses at most
+// ~6e-5 to cancellation.  tau' = 1.01 tau + 0.05 and hy * 1.001 + 0.25 px
+// cover all of these.  Ill-conditioned or non-positive conics, NaN
 // opacities and non-finite centres are not culled; o < 0.999/255 never
 // blends.
 __device__ __forceinline__ float2 splat_rows(float y, float a, float b, float c, float o) {
@@ -142,11 +143,12 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
       float4 a, b;
       float c;
       stage_splat<NCH>(g, (uint32_t)prm.num_points, io.means2d, io.colors, prm.num_channels, io.conic_opacity, a, b, c);
-      // staged as (x, y, A, B) and (C, o, ...) with A = -a/2, B = -b,
-      // C = -c/2, the operands of splat_power
-      a.z = -0.5f * a.z;
-      a.w = -a.w;
-      b.x = -0.5f * b.x;
+      // staged as (x, y, A, B) and (C, o, ...) with the base-2 exponent
+      // coefficients of splat_log2_coeffs, the operands of splat_power
+      const float3 k2 = splat_log2_coeffs(a.z, a.w, b.x);
+      a.z = k2.x;
+      a.w = k2.y;
+      b.x = k2.z;
       s_a[t] = a;
       s_b[t] = b;
       s_c[t] = c;
@@ -168,6 +170,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
     auto walk = [&](auto finite_tag) {
       constexpr bool kFinite = decltype(finite_tag)::value;
       for (int j0 = 0; j0 < cnt8; j0 += 8) {
+        int lg = 0;  // u + 1 of the group's last splat the pixel takes (0: none)
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int j = j0 + u;
@@ -185,18 +188,24 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           const float4 b = s_b[j];
           const float dx = a.x - pxf;
           const float dy = a.y - pyf;
-          const float power = splat_power(a.z, a.w, b.x, dx, dy);
-          const float alpha = fminf(0.99f, b.y * blend_expf(power));
+          const float t2 = splat_power(a.z, a.w, b.x, dx, dy);  // log2(e) power
+          const float alpha = fminf(0.99f, b.y * blend_exp2f(t2));
           const float test_t = T * (1.0f - alpha);
-          const bool blend = live && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
+          const bool blend = live && !(t2 > 0.0f) && !(alpha < 1.0f / 255.0f);
           const bool stop = blend && test_t < 0.0001f;
           const bool take = blend && !stop;
           live = live && !stop;
-          // colour by fused multiply-adds (no decision depends on it).  aT is 0
-          // where the pixel does not take the splat; with a non-finite colour
-          // in the batch the colour is selected to 0 there as well (0 * inf
-          // would be NaN), otherwise c * 0 adds an exact zero.
-          const float aT = take ? alpha * T : 0.0f;
+          // colour by fused multiply-adds (no decision depends on it), with
+          // the weight alpha T taken as T - T (1 - alpha): the transmittance
+          // the splat removes, one subtraction instead of a product and a
+          // select (it differs from the product by the rounding of T (1 -
+          // alpha), below 2^-24 T, and the weights of a pixel sum to at most
+          // 1 - T_final).  aT is exactly 0 where the pixel does not take the
+          // splat; with a non-finite colour in the batch the colour is
+          // selected to 0 there as well (0 * inf would be NaN), otherwise
+          // c * 0 adds an exact zero.
+          const float Tn = take ? test_t : T;
+          const float aT = T - Tn;
           const float c2 = NCH > 2 ? s_c[j] : 0.0f;
           if (kFinite) {
             acc[0] = __builtin_fmaf(b.z, aT, acc[0]);
@@ -209,10 +218,11 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           }
           if (kMetric && take && count_metric && s_g[j] < (uint32_t)prm.num_points)
             atomicAdd(&io.metric_count[s_g[j]], 1);
-          T = take ? test_t : T;
-          last = take ? (uint32_t)(jj + 1) : last;
+          T = Tn;
+          lg = take ? u + 1 : lg;
           if (kIters) iters = stop ? (uint32_t)(jj + 1) : iters;
         }
+        last = lg ? (uint32_t)(base + j0 + lg) : last;
         if (__ballot(live) == 0ull) break;  // uniform
       }
     };
@@ -334,20 +344,21 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
   bool any = false;
   const float dx = a.x - pxf;
   const float dxdx = dx * dx;
-  // the forward's power, with its per-splat parts kept for the four strips
-  const float Bdx = -a.w * dx;
-  const float Adxdx = (-0.5f * a.z * dx) * dx;
-  const float Cc = -0.5f * b.x;
+  // the forward's base-2 exponent (a.z, a.w, b.x hold the coefficients of
+  // splat_log2_coeffs), with its per-splat parts kept for the four strips
+  const float Bdx = a.w * dx;
+  const float Adxdx = (a.z * dx) * dx;
+  const float Cc = b.x;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     if (jj >= nc_max[k]) continue;  // every pixel of the strip ends before this splat
     if (!((reach >> k) & 1u)) continue;  // outside the splat's rows (scalar test)
     const float dy = a.y - (pyf0 + (float)(4 * k));
-    const float power = splat_power_rows(Bdx, Adxdx, Cc, dy);
-    const float G = blend_expf(power);
+    const float t2 = splat_power_rows(Bdx, Adxdx, Cc, dy);
+    const float G = blend_exp2f(t2);
     const float oG = b.y * G;
     const float alpha = fminf(0.99f, oG);
-    const bool act = jj < nc[k] && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
+    const bool act = jj < nc[k] && !(t2 > 0.0f) && !(alpha < 1.0f / 255.0f);
     if (__ballot(act) == 0ull) continue;  // wave-uniform
     any = true;
     // 1/(1-alpha) by the hardware reciprocal (1 ulp): the backward takes no
@@ -490,16 +501,18 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
       stage_splat<NCH>(g, (uint32_t)P, io.means2d, io.colors, prm.num_channels, io.conic_opacity,
                        a, b, c);
       const float4 hh = make_float4(a.z * hx, a.w * hx, b.x * hy, a.w * hy);
-      s_a[l] = a;
-      s_b[l] = b;
+      // the exponent's base-2 coefficients, as the forward stages them
+      const float3 k2 = splat_log2_coeffs(a.z, a.w, b.x);
+      s_a[l] = make_float4(a.x, a.y, k2.x, k2.y);
+      s_b[l] = make_float4(k2.z, b.y, b.z, b.w);
       s_h[l] = hh;
       s_g[l] = g;
       const float2 cu = splat_rows(a.y, a.z, a.w, b.x, b.y);
       fin = __builtin_isfinite(a.x) && __builtin_isfinite(a.y) &&
                        __builtin_isfinite(hh.x) && __builtin_isfinite(hh.y) &&
                        __builtin_isfinite(hh.z) && __builtin_isfinite(hh.w) &&
-                       __builtin_isfinite(a.z) && __builtin_isfinite(a.w) &&
-                       __builtin_isfinite(b.x) && __builtin_isfinite(b.y) &&
+                       __builtin_isfinite(k2.x) && __builtin_isfinite(k2.y) &&
+                       __builtin_isfinite(k2.z) && __builtin_isfinite(b.y) &&
                        __builtin_isfinite(b.z) && __builtin_isfinite(b.w) && __builtin_isfinite(c);
       // the strips k (rows ty0 + 4k .. + 3) the row extent reaches
       uint32_t reach = 0u;

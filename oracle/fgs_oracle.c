@@ -38,7 +38,8 @@ typedef double real;
 #define RMIN(a, b) fmin(a, b)
 #define RMAX(a, b) fmax(a, b)
 #define REXP(x) exp(x)
-#define RBEXP(x) exp(x)
+#define RBEXP2(x) exp2(x)
+#define ORC_LOG2E 1.4426950408889634
 #define RFMA(a, b, c) fma(a, b, c)
 #define RLOG(x) log(x)
 #else
@@ -50,7 +51,8 @@ typedef float real;
 #define RMIN(a, b) fminf(a, b)
 #define RMAX(a, b) fmaxf(a, b)
 #define REXP(x) orc_expf(x)
-#define RBEXP(x) orc_blend_expf(x)
+#define RBEXP2(x) orc_blend_exp2f(x)
+#define ORC_LOG2E 1.44269504088896341f
 #define RFMA(a, b, c) fmaf(a, b, c)
 #define RLOG(x) orc_logf(x)
 #endif
@@ -83,19 +85,20 @@ float orc_expf(float x) {
   return ldexpf(p, (int)n);
 }
 
-/* exp of a blend exponent (the rasterizer's G = exp(power)): 2^t with
- * t = x*log2(e) rounded to float, n = floor(t), f = t - n (exact) in [0, 1);
- * 2^f = 1 + f*q(f), q of degree 4 fitted to the relative error at 400
- * Chebyshev nodes on [0, 1] by iteratively reweighted least squares, Horner
- * with correctly rounded fused multiply-adds; scaled by ldexp (exact).  x is
- * clamped at -87.  Relative error at most 2e-7 plus 0.35 ulp of t and
- * 1.34e-8 |x| (the roundings of t and of log2(e)); tests/test_oracle_math.py
- * pins it against float64 exp. */
-float orc_blend_expf(float x) {
-  x = fmaxf(x, -87.0f);
-  const float t = x * 1.44269504088896341f;
+/* 2^t for the rasterizer's base-2 blend exponent t = log2(e) power (its
+ * G = exp(power); the coefficients of splat_power carry log2(e)): t clamped
+ * at -126, n = floor(t), f = min(t - n, 0x1.fffffep-1) in [0, 1) (t - n
+ * rounds to 1 for t just below 0; the HIP kernels' v_fract_f32 returns this
+ * clamped value and their v_cvt_flr_i32_f32 floor(t), checked for every float
+ * in [-126, 8]); 2^f = 1 + f*q(f), q of degree 4 fitted to the relative error
+ * at 400 Chebyshev nodes on [0, 1] by iteratively reweighted least squares,
+ * Horner with correctly rounded fused multiply-adds; scaled by ldexp (exact).
+ * Relative error at most 2e-7 against 2^t; tests/test_oracle_math.py pins it
+ * against float64 exp2. */
+float orc_blend_exp2f(float t) {
+  t = fmaxf(t, -126.0f);
   const float n = floorf(t);
-  const float f = t - n;
+  const float f = fminf(t - n, 0x1.fffffep-1f);
   float q = 0x1.e86492p-10f;
   q = fmaf(q, f, 0x1.279248p-7f);
   q = fmaf(q, f, 0x1.c925b2p-5f);
@@ -145,14 +148,17 @@ static inline int32_t orc_f2i(real v) {
   return (int32_t)v;
 }
 
-/* Exponent of a splat at offset (dx, dy) from its centre (the blend loops of
- * fastgs_rasterize.metal:105-106 and fastgs_rasterize_backward.metal:189-190:
- * power = -1/2 (a dx^2 + c dy^2) - b dx dy for the conic (a, b, c)), written
- * as A dx^2 + B dx dy + C dy^2 with A = -a/2, B = -b, C = -c/2 (each exact)
- * and evaluated as fma(dy, fma(C, dy, B dx), (A dx) dx), the HIP kernels'
- * operation order. */
+/* Base-2 exponent of a splat at offset (dx, dy) from its centre: t =
+ * log2(e) power, power = -1/2 (a dx^2 + c dy^2) - b dx dy for the conic
+ * (a, b, c) (the blend loops of fastgs_rasterize.metal:105-106 and
+ * fastgs_rasterize_backward.metal:189-190, whose exp(power) is 2^t), written
+ * as A dx^2 + B dx dy + C dy^2 with A = (-a/2) log2(e), B = -b log2(e),
+ * C = (-c/2) log2(e) (one rounding each) and evaluated as
+ * fma(dy, fma(C, dy, B dx), (A dx) dx), the HIP kernels' operation order.
+ * t > 0 exactly where the reference's power > 0 up to these roundings. */
 static inline real splat_power(const real* co, real dx, real dy) {
-  const real A = (real)-0.5 * co[0], B = -co[1], C = (real)-0.5 * co[2];
+  const real A = ((real)-0.5 * co[0]) * ORC_LOG2E, B = -co[1] * ORC_LOG2E;
+  const real C = ((real)-0.5 * co[2]) * ORC_LOG2E;
   return RFMA(dy, RFMA(C, dy, B * dx), (A * dx) * dx);
 }
 
@@ -709,9 +715,9 @@ void orc_rasterize_fwd(const orc_rparams* rp, const uint32_t* ranges, const uint
           real dx = means2d[2 * (size_t)g] - pxf;
           real dy = means2d[2 * (size_t)g + 1] - pyf;
           const real* co = conic_opacity + 4 * (size_t)g;
-          real power = splat_power(co, dx, dy);
-          if (power > (real)0) continue;
-          real alpha = RMIN((real)0.99, co[3] * RBEXP(power));
+          real t2 = splat_power(co, dx, dy); /* log2(e) power */
+          if (t2 > (real)0) continue;
+          real alpha = RMIN((real)0.99, co[3] * RBEXP2(t2));
           if (alpha < (real)1 / (real)255) continue;
           real test_t = T * ((real)1 - alpha);
           if (test_t < (real)0.0001) break;
@@ -822,9 +828,9 @@ void orc_rasterize_bwd_mag(const orc_rparams* rp, const uint32_t* ranges,
             real dx = means2d[2 * (size_t)g] - pxf;
             real dy = means2d[2 * (size_t)g + 1] - pyf;
             const real* co = conic_opacity + 4 * (size_t)g;
-            real power = splat_power(co, dx, dy);
-            if (power > (real)0) continue;
-            real G = RBEXP(power);
+            real t2 = splat_power(co, dx, dy); /* log2(e) power */
+            if (t2 > (real)0) continue;
+            real G = RBEXP2(t2);
             real alpha = RMIN((real)0.99, co[3] * G);
             if (alpha < (real)1 / (real)255) continue;
             rec_g[m] = g;

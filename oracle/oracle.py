@@ -11,9 +11,10 @@ of ``rasterize_gaussians_forward`` (reference binding.cpp:33-282) and
 then fastgs_preprocess.cpp:191-206).
 
 Parity status of each C function (how it is pinned; see tests/test_oracle_*):
-  orc_expf / orc_logf /    : error bounds against numpy float64 exp/log.
-  orc_blend_expf
-  splat_power              : error bound against the float64 quadratic form.
+  orc_expf / orc_logf /    : error bounds against numpy float64 exp/log/exp2.
+  orc_blend_exp2f
+  splat_power              : error bound against log2(e) times the float64
+                             quadratic form.
   orc_preprocess_fwd       : closed forms (identity camera cov2D = J J^T + 0.3),
                              reference KAT (preprocess_smoke: all zero), and the
                              double build's finite differences through it.
@@ -103,8 +104,8 @@ class Oracle:
         L = self.lib
         L.orc_expf.restype = c_float
         L.orc_expf.argtypes = [c_float]
-        L.orc_blend_expf.restype = c_float
-        L.orc_blend_expf.argtypes = [c_float]
+        L.orc_blend_exp2f.restype = c_float
+        L.orc_blend_exp2f.argtypes = [c_float]
         L.orc_splat_power.restype = c_double
         L.orc_splat_power.argtypes = [c_double] * 5
         L.orc_logf.restype = c_float
@@ -124,8 +125,8 @@ class Oracle:
     def expf(self, x: float) -> float:
         return self.lib.orc_expf(float(x))
 
-    def blend_expf(self, x: float) -> float:
-        return self.lib.orc_blend_expf(float(x))
+    def blend_exp2f(self, t: float) -> float:
+        return self.lib.orc_blend_exp2f(float(t))
 
     def splat_power(self, a, b, c, dx, dy) -> float:
         return self.lib.orc_splat_power(float(a), float(b), float(c), float(dx), float(dy))

@@ -3,9 +3,10 @@ row extent (splat_rows in fastgs_core_amd/csrc/fgs_raster.hip).  Skipping a
 strip that holds a pixel with alpha >= 1/255 would corrupt that pixel's
 transmittance recovery, so the extent must contain every such pixel.
 
-This CPU test restates the kernel's float32 arithmetic with numpy (power
-as splat_power computes it, fused multiply-adds emulated in float64; the exp
-and the hardware log perturbed by at least their error) on splats from
+This CPU test restates the kernel's float32 arithmetic with numpy (the
+base-2 exponent as splat_power computes it from splat_log2_coeffs, fused
+multiply-adds emulated in float64; the exp and the hardware log perturbed by
+at least their error) on splats from
 isotropic to the most
 elongated the extent is used for (det just above 1e-3 a c), and checks that
 every pixel that blends lies inside the extent, and that the extent is not
@@ -16,7 +17,8 @@ import numpy as np
 f32 = np.float32
 
 
-EXP_ERR = 4.5e-7  # blend_expf's relative error on [-5.5, 0] is below 4.3e-7
+EXP_ERR = 2.5e-7  # blend_exp2f's relative error against 2^t is below 2e-7
+LOG2E = f32(1.44269504088896341)
 
 
 def _fma32(x, y, z):
@@ -24,9 +26,10 @@ def _fma32(x, y, z):
 
 
 def _power32(a, b, c, dx, dy):
-    """splat_power: fma(dy, fma(C, dy, B dx), (A dx) dx), A = -a/2, B = -b,
-    C = -c/2, in float32 (works elementwise on arrays)."""
-    A, B, C = f32(-0.5) * a, -b, f32(-0.5) * c
+    """splat_power on splat_log2_coeffs: fma(dy, fma(C, dy, B dx), (A dx) dx),
+    A = (-a/2) log2(e), B = -b log2(e), C = (-c/2) log2(e), in float32 (works
+    elementwise on arrays): the base-2 exponent t, G = 2^t."""
+    A, B, C = f32(f32(-0.5) * a) * LOG2E, f32(-b) * LOG2E, f32(f32(-0.5) * c) * LOG2E
     return _fma32(dy, _fma32(C, dy, f32(B * dx)), f32(f32(A * dx) * dx))
 
 
@@ -81,7 +84,7 @@ def _active_rows(x, y, a, b, c, o, rng):
     dx = f32(x) - X
     dy = f32(y) - Y
     power = _power32(a, b, c, dx, dy).astype(np.float32)
-    G = np.exp(power.astype(np.float64)) * (1.0 + EXP_ERR)
+    G = np.exp2(power.astype(np.float64)) * (1.0 + EXP_ERR)
     alpha = np.minimum(0.99, np.float64(o) * G)
     act = (alpha >= 1.0 / 255.0) & ~(power > 0)
     return Y[act]
@@ -122,7 +125,7 @@ def test_row_extent_at_the_ellipse_tip():
                 y = f32(-sgn * dy * (1 - eps))
                 fx, fy = f32(x - f32(0.0)), f32(y - f32(0.0))
                 power = _power32(a, b, c, fx, fy)
-                alpha = min(0.99, np.float64(o) * np.exp(np.float64(power)) * (1 + EXP_ERR))
+                alpha = min(0.99, np.float64(o) * np.exp2(np.float64(power)) * (1 + EXP_ERR))
                 if not (alpha >= 1.0 / 255.0) or power > 0:
                     continue
                 for log_err in (-3e-6, 3e-6):

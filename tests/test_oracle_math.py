@@ -1,9 +1,10 @@
 """Pins the oracle's deterministic exp/log and its SH basis against mathematics.
 
-orc_expf / orc_logf / orc_blend_expf are the transcendental functions both the
-oracle and the HIP kernels implement with the same IEEE operations; here they
-are checked against float64 numpy within their stated bounds, and the blend
-exponent splat_power against the float64 quadratic form.  The SH basis of orc_color_from_sh
+orc_expf / orc_logf / orc_blend_exp2f are the transcendental functions both
+the oracle and the HIP kernels implement with the same IEEE operations; here
+they are checked against float64 numpy within their stated bounds, and the
+base-2 blend exponent splat_power against log2(e) times the float64 quadratic
+form.  The SH basis of orc_color_from_sh
 (fastgs_preprocess.metal:117-169) is checked function by function against
 scipy's spherical harmonics (which carry the Condon-Shortley phase), at the
 six axis directions, the eight cube diagonals and random directions: a
@@ -28,34 +29,37 @@ def test_expf_error_bound(oracle):
     assert np.all(np.diff(got[order]) >= 0)
 
 
-def test_blend_expf_error_bound(oracle):
-    """orc_blend_expf (the rasterizer's exp of power): relative error at most
-    2e-7 (the polynomial, float evaluation included) plus the error of
-    t = x log2(e) in float: 0.35 ulp of t (the product's rounding) and
-    1.34e-8 |x| (log2(e) rounded to float), checked point by point over
-    [-87, 0] and densely over [-5.5, 0], where alpha >= 1/255 can hold; exact
-    at 0."""
+def test_blend_exp2f_error_bound(oracle):
+    """orc_blend_exp2f (2^t for the rasterizer's base-2 blend exponent):
+    relative error at most 2e-7 against float64 exp2, point by point over
+    [-126, 0] and densely over [-8, 0], where alpha >= 1/255 can hold; exact
+    at 0 and at the integers.  Just below 0, t - floor(t) rounds to 1 and is
+    clamped to 0x1.fffffep-1 as v_fract_f32 does; the result stays within the
+    bound there."""
     rng = np.random.default_rng(1)
-    xs = np.concatenate([np.linspace(-87.0, 0.0, 20001), rng.uniform(-5.5, 0.0, 40000),
-                         -np.logspace(-8, 1.9, 2000),
-                         np.array([0.0, -1e-30, -0.5, -1.0, -5.54, -86.99])]).astype(np.float32)
-    got = np.array([oracle.blend_expf(float(x)) for x in xs], np.float64)
-    ref = np.exp(xs.astype(np.float64))
+    ts = np.concatenate([np.linspace(-126.0, 0.0, 20001), rng.uniform(-8.0, 0.0, 40000),
+                         -np.logspace(-12, 2.1, 3000),
+                         np.array([0.0, -1e-30, -2.0 ** -26, -2.0 ** -25, -0.5, -1.0, -8.0,
+                                   -125.99])]).astype(np.float32)
+    got = np.array([oracle.blend_exp2f(float(t)) for t in ts], np.float64)
+    ref = np.exp2(ts.astype(np.float64))
     rel = np.abs(got - ref) / ref
-    t = (xs * np.float32(1.44269504088896341)).astype(np.float32)
-    bound = (2.0e-7 + 0.3466 * np.spacing(np.abs(t)).astype(np.float64)
-             + 1.34e-8 * np.abs(xs.astype(np.float64)) + 1e-12)
-    assert np.all(rel <= bound), (rel / bound).max()
-    small = xs >= -5.5
-    assert rel[small].max() < 4.3e-7, rel[small].max()
-    assert oracle.blend_expf(0.0) == 1.0
+    assert rel.max() < 2.0e-7, rel.max()
+    for k in range(-126, 1):
+        assert oracle.blend_exp2f(float(k)) == 2.0 ** k
+    # below the clamp the value is that of -126
+    assert oracle.blend_exp2f(-1000.0) == 2.0 ** -126
+    assert oracle.blend_exp2f(float("-inf")) == 2.0 ** -126
 
 
 def test_splat_power_error_bound(oracle):
     """splat_power (oracle and kernels): fma(dy, fma(C, dy, B dx), (A dx) dx)
-    with A = -a/2, B = -b, C = -c/2 equals the quadratic form
-    -1/2 (a dx^2 + c dy^2) - b dx dy within 3 * 2^-24 (a dx^2 / 2 + |b dx dy|
-    + c dy^2 / 2); a sign slip or a dropped term is far outside it."""
+    with A = (-a/2) log2(e), B = -b log2(e), C = (-c/2) log2(e) equals
+    log2(e) (-1/2 (a dx^2 + c dy^2) - b dx dy) within
+    (4 * 2^-24 + 1.4e-8) log2(e) (a dx^2 / 2 + |b dx dy| + c dy^2 / 2): three
+    roundings of the evaluation, one of each coefficient, and log2(e) rounded
+    to float (1.34e-8 relative); a sign slip or a dropped term is far outside
+    it."""
     rng = np.random.default_rng(2)
     n = 20000
     a = np.exp(rng.uniform(-8, 2, n)).astype(np.float32)
@@ -65,13 +69,18 @@ def test_splat_power_error_bound(oracle):
     dx = rng.uniform(-40, 40, n).astype(np.float32)
     dy = rng.uniform(-40, 40, n).astype(np.float32)
     A, B, C, X, Y = (v.astype(np.float64) for v in (a, b, c, dx, dy))
-    exact = -0.5 * (A * X * X + C * Y * Y) - B * X * Y
-    scale = 0.5 * A * X * X + np.abs(B * X * Y) + 0.5 * C * Y * Y
+    L = np.log2(np.e)
+    exact = L * (-0.5 * (A * X * X + C * Y * Y) - B * X * Y)
+    scale = L * (0.5 * A * X * X + np.abs(B * X * Y) + 0.5 * C * Y * Y)
     got = np.array([oracle.splat_power(*v) for v in zip(a, b, c, dx, dy)])
     err = np.abs(got - exact)
-    assert np.all(err <= 3 * 2.0 ** -24 * scale + 1e-30), (err / scale).max()
-    # the same values through the double build are the exact form to 1e-15
-    assert oracle.splat_power(2.0, 0.5, 1.0, 3.0, -2.0) == np.float32(-0.5 * (18 + 4) + 3.0)
+    assert np.all(err <= (4 * 2.0 ** -24 + 1.4e-8) * scale + 1e-30), (err / scale).max()
+    # known answers: each term alone, with the sign of the reference's power
+    Lf = float(np.float32(L))
+    assert oracle.splat_power(2.0, 0.0, 0.0, 1.0, 0.0) == -Lf
+    assert oracle.splat_power(0.0, 0.0, 2.0, 0.0, 1.0) == -Lf
+    assert oracle.splat_power(0.0, 1.0, 0.0, 1.0, 1.0) == -Lf
+    assert oracle.splat_power(0.0, 1.0, 0.0, 1.0, -1.0) == Lf
 
 
 def test_logf_error_bound(oracle):
