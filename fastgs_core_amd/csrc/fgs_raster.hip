@@ -323,7 +323,9 @@ __device__ __forceinline__ void wave_reduce_terms(float (&v)[kGradTerms], float*
 //   dL/dalpha = T_j (col . dL) - SdL / (1 - alpha),  SdL += alpha T_j (col . dL).
 // With w = G o dL/dalpha and h = (a W/2, b W/2, c H/2, b H/2) from the conic
 // (a, b, c):  d/dmean2d = -w (h.x dx + h.y dy, h.z dy + h.w dx),
-// d/dconic = -w/2 (dx^2, dx dy, dy^2), d/dopacity = G dL/dalpha.
+// d/dconic = -w/2 (dx^2, dx dy, dy^2), d/dopacity = G dL/dalpha.  The
+// pixels' sums are taken without the splat's factor o (-o, -o/2), which
+// multiplies each sum once when the record is flushed.
 //
 // kSafe = false is the fast form: the terms of pixels that do not blend the
 // splat are driven to exact zeros by three selects, which needs every operand
@@ -364,11 +366,15 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
     // 1/(1-alpha) by the hardware reciprocal (1 ulp): the backward takes no
     // decision from T, so IEEE division is not needed here.
     const float rci = __builtin_amdgcn_rcpf(1.0f - alpha);
-    const float Tj = act ? T[k] * rci : T[k];
+    const float Tp = T[k];
+    const float Tj = act ? Tp * rci : Tp;
     T[k] = Tj;
     {
 #pragma clang fp contract(fast)
-      const float aT = act ? alpha * Tj : 0.0f;
+      // alpha T_j; in the fast form as T_j - T_j (1 - alpha), the
+      // transmittance the splat removes (exactly 0 where the pixel does not
+      // blend it, one subtraction instead of a product and a select)
+      const float aT = kSafe ? (act ? alpha * Tj : 0.0f) : Tj - Tp;
       const float col[3] = {b.z, b.w, cu.w};
       float cdl = col[0] * dL[k][0];
 #pragma unroll
@@ -385,16 +391,29 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
       }
       const bool geo = act && !(oG > 0.99f);
       const float gm = geo ? G : 0.0f;
-      // w2 = -w/2 (cu.z = -o/2): the conic terms are w2 (dx^2, dx dy, dy^2)
-      // and the means2d terms -w (..) = 2 w2 (..), doubled when flushed.
-      const float w2 = gm * (cu.z * dL_dalpha);
-      const float tx = w2 * (h.x * dx + h.y * dy);
-      const float ty = w2 * (h.z * dy + h.w * dx);
-      const float w2dy = w2 * dy;
-      const float t[8] = {tx,          ty,          fabsf(tx), fabsf(ty),
-                          w2 * dxdx,   w2dy * dx,   w2dy * dy, gm * dL_dalpha};
+      // q = G dL/dalpha is the opacity term.  w = o q; the splat's factor
+      // -o/2 (cu.z) is applied when its record is flushed, so here the conic
+      // terms are q (dx^2, dx dy, dy^2) and the means2d terms
+      // q (h.x dx + h.y dy, h.z dy + h.w dx) and their magnitudes.
+      const float qg = gm * dL_dalpha;
+      const float mx = h.x * dx + h.y * dy;
+      const float my = h.z * dy + h.w * dx;
+      const float qdy = qg * dy;
+      if (kSafe) {
+        const float t[8] = {qg * mx,   qg * my,   fabsf(qg) * fabsf(mx), fabsf(qg) * fabsf(my),
+                            qg * dxdx, qdy * dx,  qdy * dy,              qg};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] += kSafe ? (geo ? t[i] : 0.0f) : t[i];
+        for (int i = 0; i < 8; ++i) v[i] += geo ? t[i] : 0.0f;
+      } else {
+        v[0] = __builtin_fmaf(qg, mx, v[0]);
+        v[1] = __builtin_fmaf(qg, my, v[1]);
+        v[2] = __builtin_fmaf(fabsf(qg), fabsf(mx), v[2]);
+        v[3] = __builtin_fmaf(fabsf(qg), fabsf(my), v[3]);
+        v[4] = __builtin_fmaf(qg, dxdx, v[4]);
+        v[5] = __builtin_fmaf(qdy, dx, v[5]);
+        v[6] = __builtin_fmaf(qdy, dy, v[6]);
+        v[7] += qg;
+      }
     }
   }
   return any;
@@ -548,7 +567,11 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
       const int q = i * kBwdBatch + l;
       const int s = q / kRec, t = q - (q / kRec) * kRec;
       if (s < cnt && t < 8 + NCH) {
-        const float w = t < 4 ? 2.0f * s_rec[q] : s_rec[q];  // means2d terms were halved
+        // the splat's factor on its geometry terms: -o for the means2d
+        // terms, |o| for their magnitudes, -o/2 for the conic's
+        const float hz = s_cull[s].z;  // -o/2
+        const float f = t < 2 ? 2.0f * hz : (t < 4 ? fabsf(2.0f * hz) : (t < 7 ? hz : 1.0f));
+        const float w = s_rec[q] * f;
         const uint32_t g = s_g[s];
         if (w != 0.0f && g < (uint32_t)P) {
           float* dst = t < 4 ? io.dL_dviewspace + 4 * (size_t)g + t
