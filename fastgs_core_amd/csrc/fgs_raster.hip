@@ -190,7 +190,7 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           const float dy = a.y - pyf;
           const float t2 = splat_power(a.z, a.w, b.x, dx, dy);  // log2(e) power
           const float alpha = fminf(0.99f, b.y * blend_exp2f(t2));
-          const float test_t = T * (1.0f - alpha);
+          const float test_t = __builtin_fmaf(-alpha, T, T);  // T (1 - alpha), one rounding
           const bool blend = live && !(t2 > 0.0f) && !(alpha < 1.0f / 255.0f);
           const bool stop = blend && test_t < 0.0001f;
           const bool take = blend && !stop;
@@ -198,8 +198,8 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           // colour by fused multiply-adds (no decision depends on it), with
           // the weight alpha T taken as T - T (1 - alpha): the transmittance
           // the splat removes, one subtraction instead of a product and a
-          // select (it differs from the product by the rounding of T (1 -
-          // alpha), below 2^-24 T, and the weights of a pixel sum to at most
+          // select (it differs from the product by the rounding of test_t,
+          // below 2^-24 T, and the weights of a pixel sum to at most
           // 1 - T_final).  aT is exactly 0 where the pixel does not take the
           // splat; with a non-finite colour in the batch the colour is
           // selected to 0 there as well (0 * inf would be NaN), otherwise

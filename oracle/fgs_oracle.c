@@ -719,7 +719,8 @@ void orc_rasterize_fwd(const orc_rparams* rp, const uint32_t* ranges, const uint
           if (t2 > (real)0) continue;
           real alpha = RMIN((real)0.99, co[3] * RBEXP2(t2));
           if (alpha < (real)1 / (real)255) continue;
-          real test_t = T * ((real)1 - alpha);
+          /* T (1 - alpha) as one fused multiply-add, the HIP kernel's form */
+          real test_t = RFMA(-alpha, T, T);
           if (test_t < (real)0.0001) break;
           for (int c = 0; c < C; ++c) acc[c] += colors[(size_t)g * NC + c] * alpha * T;
           if (rp->get_flag && metric_map[pix] == 1) {
@@ -841,7 +842,7 @@ void orc_rasterize_bwd_mag(const orc_rparams* rp, const uint32_t* ranges,
             rec[5 * m + 3] = dx;
             rec[5 * m + 4] = dy;
             m++;
-            T = T * ((real)1 - alpha);
+            T = RFMA(-alpha, T, T); /* the forward's transmittance */
           }
           real Tf = final_t[pix];
           real dL[3] = {0, 0, 0};
