@@ -14,6 +14,10 @@
  *                   '/' and sqrt, and the deterministic orc_expf / orc_logf
  *                   below, which the HIP kernels implement with the same
  *                   operations.  Integer outputs are therefore bit-identical.
+ *                   Two rasterizer steps are written in another order, each
+ *                   stated where it is used: the blend exponent in base 2
+ *                   (splat_power, orc_blend_exp2f: exp(power) = 2^t) and the
+ *                   transmittance update T (1 - alpha) as fma(-alpha, T, T).
  *   liborc_f64.so : real = double, libm exp/log.  Used by the finite-difference
  *                   tests that pin the analytic backward.
  *
