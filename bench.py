@@ -282,7 +282,8 @@ def run_densify_loop(args):
 
 
 class StageTimer:
-    """Event pairs recorded on the launch stream around each C-ABI stage.
+    """Event pairs recorded around each C-ABI stage on the stream it is launched on (the
+    launch stream; the scan of tiles_touched runs on a side stream beside the depth sort).
     A stage entered more than once in one step (binning: the depth order, then
     the rest) is reported as the sum of its intervals in that step."""
 

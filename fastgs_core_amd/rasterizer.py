@@ -417,9 +417,11 @@ def _inclusive_scan_i32(x: torch.Tensor, side=None) -> torch.Tensor:
         for t in (x, buf, ws):
             t.record_stream(side)
     stream = ctypes.c_void_p(side.cuda_stream) if side is not None else _stream(x.device)
-    with _stage("scan"):
-        _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(buf[:n]) if n else None, n, _p(ws),
-                                              _p(buf[n:]), stream))
+    # the stage timer records on the stream the scan runs on
+    with torch.cuda.stream(side if side is not None else torch.cuda.current_stream(x.device)):
+        with _stage("scan"):
+            _lib.check(lib.fgs_inclusive_scan_u32(_p(x), _p(buf[:n]) if n else None, n, _p(ws),
+                                                  _p(buf[n:]), stream))
     return buf
 
 
