@@ -367,14 +367,15 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
     // decision from T, so IEEE division is not needed here.
     const float rci = __builtin_amdgcn_rcpf(1.0f - alpha);
     const float Tp = T[k];
-    const float Tj = act ? Tp * rci : Tp;
+    // alpha T_j; in the fast form as T_j - T_{j+1} = T_{j+1} / (1 - alpha) -
+    // T_{j+1}, the transmittance the splat removes (exactly 0 where the pixel
+    // does not blend it), and T_j = T_{j+1} + that, so T is updated in place
+    const float aTf = act ? __builtin_fmaf(Tp, rci, -Tp) : 0.0f;
+    const float Tj = kSafe ? (act ? Tp * rci : Tp) : Tp + aTf;
     T[k] = Tj;
     {
 #pragma clang fp contract(fast)
-      // alpha T_j; in the fast form as T_j - T_j (1 - alpha), the
-      // transmittance the splat removes (exactly 0 where the pixel does not
-      // blend it, one subtraction instead of a product and a select)
-      const float aT = kSafe ? (act ? alpha * Tj : 0.0f) : Tj - Tp;
+      const float aT = kSafe ? (act ? alpha * Tj : 0.0f) : aTf;
       const float col[3] = {b.z, b.w, cu.w};
       float cdl = col[0] * dL[k][0];
 #pragma unroll
