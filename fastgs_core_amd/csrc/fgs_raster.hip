@@ -233,7 +233,8 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
         walk(FiniteTag<false>{});
     }
     done = live ? 0 : 1;
-    __syncthreads();
+    // the next round's __syncthreads_count is the barrier before its staging
+    // overwrites the batch; after the last round the batch is not read again
   }
   if (inside) {
     io.final_t[pix] = T;
