@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 
 class PreprocessParams(Structure):
@@ -46,7 +46,7 @@ class PreprocessBwdIO(Structure):
         "dL_dconic_opacity", "dL_dcov3d", "dL_dviewspace_out", "dL_dmeans3d", "dL_ddc", "dL_dsh",
         "dL_dcolors_precomp", "dL_dopacities", "dL_dscales", "dL_drotations",
         "dL_dviewspace_in", "quats_raw", "act_opacities", "dL_dlog_scales", "dL_dquats",
-        "dL_dlogits", "log_scales", "opacity_logits")]
+        "dL_dlogits", "log_scales", "opacity_logits")] + [("dL_dxys_stride", c_int64)]
 
 
 class BinningIO(Structure):

@@ -481,8 +481,9 @@ preprocess_bwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_bwd_
     const Mat16 V = load_mat(io.viewmatrix);
     const Mat16 Pm = load_mat(io.projmatrix);
     const float ph3 = Pm.m[3] * px + Pm.m[7] * py + Pm.m[11] * pz + Pm.m[15];
-    const float gx = io.dL_dxys ? io.dL_dxys[2 * I + 0] : 0.f;
-    const float gy = io.dL_dxys ? io.dL_dxys[2 * I + 1] : 0.f;
+    const size_t xs = io.dL_dxys_stride > 0 ? (size_t)io.dL_dxys_stride : 2u;
+    const float gx = io.dL_dxys ? io.dL_dxys[xs * I + 0] : 0.f;
+    const float gy = io.dL_dxys ? io.dL_dxys[xs * I + 1] : 0.f;
     float cg0 = 0.f, cg1 = 0.f, cg2 = 0.f, cg3 = 0.f;
     if (io.dL_dconic_opacity) {
       const float4 g = *reinterpret_cast<const float4*>(io.dL_dconic_opacity + 4 * I);
@@ -906,6 +907,9 @@ extern "C" int32_t fgs_preprocess_bwd(const fgs_preprocess_params* p,
     return set_error(FGS_ERR_INVALID_ARGUMENT,
                      "fgs_preprocess_bwd: fused activation gradients need act_opacities, "
                      "quats_raw and the scale/rotation path");
+  if (io->dL_dxys_stride < 0 || io->dL_dxys_stride == 1)
+    return set_error(FGS_ERR_INVALID_ARGUMENT,
+                     "fgs_preprocess_bwd: dL_dxys_stride must be 0 or at least 2");
   const float fx = 0.5f * (float)p->image_width / fmaxf(p->tan_fovx, 1e-6f);
   const float fy = 0.5f * (float)p->image_height / fmaxf(p->tan_fovy, 1e-6f);
   const unsigned blocks = (unsigned)((p->P + kShBlock - 1) / kShBlock);

@@ -669,6 +669,15 @@ copy_means2d_grad_kernel(const float* __restrict__ vsp, float* __restrict__ dmea
   *reinterpret_cast<float2*>(dmeans2d + 2 * (size_t)g) = make_float2(v.x, v.y);
 }
 
+// The copy, when the caller asks for dL_dmeans2d (a NULL one is read in place
+// from dL_dviewspace).
+static int32_t copy_means2d_grad(const fgs_raster_bwd_io* io, int P, hipStream_t st) {
+  if (!io->dL_dmeans2d || P <= 0) return check_launch("rasterize_bwd");
+  hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
+                     io->dL_dviewspace, io->dL_dmeans2d, P);
+  return check_launch("copy_means2d_grad_kernel");
+}
+
 }  // namespace fgs
 
 using namespace fgs;
@@ -777,7 +786,7 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   if (p->num_tiles < tiles) tiles = p->num_tiles;
   const int P = p->num_points;
   const int C = p->num_channels;
-  if (P > 0 && (!io->dL_dmeans2d || !io->dL_dcolors || !io->dL_dconic_opacity || !io->dL_dviewspace))
+  if (P > 0 && (!io->dL_dcolors || !io->dL_dconic_opacity || !io->dL_dviewspace))
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_rasterize_bwd: missing gradient tensor");
   hipStream_t st = (hipStream_t)stream;
   // the atomically accumulated gradients start at zero
@@ -798,9 +807,7 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
   if (tiles == 0) {
     hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)fill_blocks), dim3(kOrderThreads), 0, st, f,
                        nullptr, 0, nullptr);
-    hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
-                       io->dL_dviewspace, io->dL_dmeans2d, P);
-    return check_launch("copy_means2d_grad_kernel");
+    return copy_means2d_grad(io, P, st);
   }
   if (!io->ranges || !io->point_list || !io->means2d || !io->colors || !io->conic_opacity ||
       !io->background || !io->final_t || !io->n_contrib || !io->max_contrib || !io->dL_dout_color)
@@ -820,7 +827,5 @@ extern "C" int32_t fgs_rasterize_bwd(const fgs_raster_params* p, const fgs_raste
     hipLaunchKernelGGL(raster_bwd_kernel<1>, dim3(tiles), dim3(64), 0, st, *p, kio, sh);
   if (check_launch("raster_bwd_kernel") != FGS_OK) return FGS_ERR_LAUNCH;
   if (const int32_t e = launch_mark(kLaunchRasterBwd, st, 1)) return e;
-  hipLaunchKernelGGL(copy_means2d_grad_kernel, dim3(ceil_div_u(P, 256)), dim3(256), 0, st,
-                     io->dL_dviewspace, io->dL_dmeans2d, P);
-  return check_launch("copy_means2d_grad_kernel");
+  return copy_means2d_grad(io, P, st);
 }

@@ -40,6 +40,10 @@ TILE = 16
 # unless requested (zero-size tensors are returned otherwise).
 WRITE_SAMPLED_STATE = False
 
+# The rasterize backward returns dL/dmeans2d as a view of dL/dviewspace (its
+# first two components) instead of a copy; False restores the copy.
+MEANS2D_GRAD_VIEW = True
+
 # Optional stage timer (used by bench.py): an object with begin(name) and
 # end(name) methods, called around every C-ABI stage on the launch stream.
 _STAGE_TIMER = None
@@ -281,7 +285,15 @@ class _Preprocess(torch.autograd.Function):
         P = means3d.shape[0]
         f32 = dict(dtype=torch.float32, device=dev)
         c = lambda g: None if g is None else g.to(torch.float32).contiguous()  # noqa: E731
-        g_xys, g_rgb, g_conic, g_cov3d, g_vsp = c(g_xys), c(g_rgb), c(g_conic), c(g_cov3d), c(g_vsp)
+        # the xy cotangent is read with its row stride when its rows are
+        # float pairs (the rasterize backward's view of dL/dviewspace)
+        xys_stride = 0
+        if (g_xys is not None and g_xys.dtype == torch.float32 and g_xys.dim() == 2
+                and g_xys.shape[1] == 2 and g_xys.stride(1) == 1 and g_xys.stride(0) >= 2):
+            xys_stride = int(g_xys.stride(0))
+        else:
+            g_xys = c(g_xys)
+        g_rgb, g_conic, g_cov3d, g_vsp = c(g_rgb), c(g_conic), c(g_cov3d), c(g_vsp)
         d_means3d = torch.empty((P, 3), **f32)
         sh_path = not cfg["use_col"]
         d_dc = torch.empty((P, 3), **f32) if sh_path else None
@@ -304,7 +316,7 @@ class _Preprocess(torch.autograd.Function):
             None if raw else _p(d_opac), None if raw else _p(d_scales),
             None if raw else _p(d_rot), _p(d_vsp), _p(raw_rotations), None,
             _p(d_scales) if raw else None, _p(d_rot) if raw else None,
-            _p(d_opac) if raw else None, _p(log_scales), _p(opacity_logits))
+            _p(d_opac) if raw else None, _p(log_scales), _p(opacity_logits), xys_stride)
         if P > 0:
             with _stage("preprocess_bwd"):
                 _lib.check(lib.fgs_preprocess_bwd(ctypes.byref(prm), ctypes.byref(io),
@@ -381,16 +393,19 @@ class _Rasterize(torch.autograd.Function):
         if g_out is None:
             g_out = torch.zeros((C, W * H), **f32)
         g_out = g_out.to(torch.float32).contiguous()
-        d_means2d = torch.empty((P, 2), **f32)
         d_colors = torch.empty((P, colors.shape[1] if colors.dim() == 2 else C), **f32)
         d_conic = torch.empty((P, 4), **f32)
         d_vsp = torch.empty((P, 4), **f32)
+        # dL/dmeans2d is the first two components of dL/dviewspace: returned
+        # as that view (no copy); the preprocess backward reads it in place
+        d_means2d = d_vsp[:, :2] if MEANS2D_GRAD_VIEW else torch.empty((P, 2), **f32)
         tile_order = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
         prm = _lib.RasterParams(W, H, C, T, B, 0, 0, P, point_list.numel())
         io = _lib.RasterBwdIO(
             _p(ranges), _p(point_list), _p(means2d), _p(colors), _p(conic_opacity),
             _p(background), _p(final_t), _p(n_contrib), _p(max_contrib), _p(g_out),
-            _p(d_means2d), _p(d_colors), _p(d_conic), _p(d_vsp), _p(tile_order))
+            None if MEANS2D_GRAD_VIEW else _p(d_means2d), _p(d_colors), _p(d_conic), _p(d_vsp),
+            _p(tile_order))
         with _stage("rasterize_bwd"):
             _lib.check(lib.fgs_rasterize_bwd(ctypes.byref(prm), ctypes.byref(io), _stream(dev)))
         need = ctx.needs_input_grad

@@ -194,6 +194,12 @@ typedef struct {
   float* dL_dlogits;           /* [P] */
   const float* log_scales;     /* [P,3] */
   const float* opacity_logits; /* [P] */
+  /* Floats from one Gaussian's dL_dxys pair to the next (no reference
+   * counterpart; 0 = 2, a [P,2] array).  4 reads the first two components of
+   * a [P,4] array: the rasterize backward's dL_dviewspace, whose first two
+   * components are dL_dmeans2d, so a caller that chains the two backwards
+   * needs no copy.  At least 2 when not 0. */
+  int64_t dL_dxys_stride;
 } fgs_preprocess_bwd_io;
 
 /* Replaces FastGSPreprocess::vjp -> FastGSPreprocessBackward::eval_gpu
@@ -390,7 +396,9 @@ typedef struct {
   const uint32_t* n_contrib;    /* [H*W] from the forward */
   const uint32_t* max_contrib;  /* [T] from the forward */
   const float* dL_dout_color;   /* [C,H*W] */
-  float* dL_dmeans2d;           /* [P,2] */
+  float* dL_dmeans2d;           /* [P,2], or NULL: not written (it equals the first two
+                                   components of dL_dviewspace, which a caller may read in
+                                   place; fgs_preprocess_bwd_io.dL_dxys_stride = 4) */
   float* dL_dcolors;            /* [P,num_channels] */
   float* dL_dconic_opacity;     /* [P,4] */
   float* dL_dviewspace;         /* [P,4] */
