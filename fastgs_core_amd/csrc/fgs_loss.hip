@@ -270,9 +270,6 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
   float ring[11][3];
   RowRing<3> rq;
   rq.fill(dp, a, r0 - kLR, c0, l);
-  // x, y of the lane's pixel in image row r0 - 5 + i, loaded with input row i
-  // into slot i % 11 and used five rows later, when that row is the output
-  float qx[11], qy[11];
   auto row = [&](const int i, const int sl, const bool first) __attribute__((always_inline)) {
     float (*sd)[kRowIn] = s_d[i & 1];
 #pragma unroll
@@ -283,13 +280,6 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
     const int pf = i + 11 < kRows ? r0 - kLR + i + 11 : -1;  // -1: reads nothing
 #pragma unroll
     for (int m = 0; m < 3; ++m) load_row(dp[m], a, pf, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
-    {
-      const int irow = r0 - kLR + i;
-      const bool in = col_in && i >= kLR && i < kLR + kSH && irow < a.H;
-      const uint32_t o = in ? (uint32_t)(irow * a.W + gc) * 4u : kOob;
-      qx[sl] = buf_load(xp, o);
-      qy[sl] = buf_load(yp, o);
-    }
     lds_barrier();
 #pragma unroll
     for (int m = 0; m < 3; ++m) {
@@ -307,11 +297,14 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
 #pragma unroll
       for (int m = 0; m < 3; ++m) B[m] = __builtin_fmaf(a.win[k], ring[q][m], B[m]);
     }
-    const float x = qx[(sl + 6) % 11], y = qy[(sl + 6) % 11];  // loaded at row i - 5
+    // x, y of the output pixel, loaded in the row that uses them: kept five
+    // rows ahead in a register ring they took 29 VGPRs, two waves per SIMD
+    // instead of three (39 against 42 us at 1080p)
+    const uint32_t o = (orow < a.H && col_in) ? (uint32_t)(orow * a.W + gc) * 4u : kOob;
+    const float x = buf_load(xp, o), y = buf_load(yp, o);
     const float d = x - y;
     const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
     const float dssim = B[0] + 2.f * x * B[1] + y * B[2];
-    const uint32_t o = (orow < a.H && col_in) ? (uint32_t)(orow * a.W + gc) * 4u : kOob;
     buf_store(gp, o, g * inv_n * (a.w_l1 * sgn - a.w_ssim * dssim));
   };
   // rows are kept apart in the schedule: interleaving them lengthens
