@@ -272,6 +272,13 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
   rq.fill(dp, a, r0 - kLR, c0, l);
   auto row = [&](const int i, const int sl, const bool first) __attribute__((always_inline)) {
     float (*sd)[kRowIn] = s_d[i & 1];
+    // x, y of this row's output pixel, issued before the row's prefetch so
+    // that their use waits for them alone, not for the prefetch
+    const int orow0 = r0 + i - 2 * kLR;
+    const bool has_out = !(first && i < 2 * kLR);
+    const uint32_t ox = (has_out && orow0 < a.H && col_in) ? (uint32_t)(orow0 * a.W + gc) * 4u : kOob;
+    const float x = buf_load(xp, ox), y = buf_load(yp, ox);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int m = 0; m < 3; ++m) {
       sd[m][l] = rq.v0[m][sl];
@@ -297,11 +304,10 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
 #pragma unroll
       for (int m = 0; m < 3; ++m) B[m] = __builtin_fmaf(a.win[k], ring[q][m], B[m]);
     }
-    // x, y of the output pixel, loaded in the row that uses them: kept five
-    // rows ahead in a register ring they took 29 VGPRs, two waves per SIMD
-    // instead of three (39 against 42 us at 1080p)
-    const uint32_t o = (orow < a.H && col_in) ? (uint32_t)(orow * a.W + gc) * 4u : kOob;
-    const float x = buf_load(xp, o), y = buf_load(yp, o);
+    // x, y are loaded in the row that uses them: kept five rows ahead in a
+    // register ring they took 29 VGPRs, two waves per SIMD instead of three
+    // (39 against 42 us at 1080p)
+    const uint32_t o = ox;
     const float d = x - y;
     const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
     const float dssim = B[0] + 2.f * x * B[1] + y * B[2];
