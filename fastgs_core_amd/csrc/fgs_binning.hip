@@ -352,9 +352,12 @@ template <typename K, bool kDepthKeys>
 __global__ void __launch_bounds__(kThreads)
 radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* __restrict__ hist,
                   const float* __restrict__ depths, const uint32_t* __restrict__ tiles_touched,
-                  uint32_t* __restrict__ dkeys_out) {
+                  uint32_t* __restrict__ dkeys_out, uint32_t* __restrict__ nvis) {
   __shared__ uint32_t s_h[8][256];
+  __shared__ uint32_t s_vis;
   for (int p = 0; p < pl.passes; ++p) s_h[p][threadIdx.x] = 0;
+  if (threadIdx.x == 0) s_vis = 0;
+  uint32_t vis = 0;  // kDepthKeys: this thread's visible keys
   __syncthreads();
   // Grid-stride in batches of kHistBatch keys per thread, all loaded before
   // the first is counted (clamped indices, so the loads carry no branch).
@@ -380,7 +383,12 @@ radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* 
       const int64_t i = i0 + b * stride;
       if (i < n) {
         const K k = kk[b];
-        if (kDepthKeys) dkeys_out[i] = (uint32_t)k;
+        if (kDepthKeys) {
+          dkeys_out[i] = (uint32_t)k;
+          // culled keys (all ones) are dropped by the first pass: not counted
+          if ((uint32_t)k == 0xFFFFFFFFu) continue;
+          ++vis;
+        }
         int shift = pl.begin;
         for (int p = 0; p < pl.passes; ++p) {
           const uint32_t d = (uint32_t)(k >> shift) & ((1u << pl.bits[p]) - 1u);
@@ -390,21 +398,41 @@ radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* 
       }
     }
   }
+  if (kDepthKeys) {
+    vis = wave_sum_u32(vis);
+    if (lane_id() == 0 && vis) atomicAdd(&s_vis, vis);
+  }
   __syncthreads();
   for (int p = 0; p < pl.passes; ++p) {
     const uint32_t c = s_h[p][threadIdx.x];
     if (c) atomicAdd(&hist[p * 256 + threadIdx.x], c);
   }
+  if (kDepthKeys && threadIdx.x == 0 && s_vis) atomicAdd(nvis, s_vis);
 }
+
+// Per-pass options of radix_pass_kernel (all off for a plain sort).
+//  drop_ones: keys equal to all ones are not sorted; the pass writes the
+//    others densely (the depth sort's first pass drops the culled Gaussians,
+//    whose keys are all ones and which its histograms do not count).
+//  n_dev: the number of keys in play, read on the device (at most n_max):
+//    the passes after a dropping one, which the host sizes for n_max.
+//  fill_tail: the last pass writes the sentinel pair (all-ones key, value
+//    0xFFFFFFFF) at positions [n, n_max), so the output keeps n_max entries.
+struct SortPassOpts {
+  const uint32_t* n_dev;
+  bool drop_ones;
+  bool fill_tail;
+};
 
 // kT threads per workgroup, kT * kIt keys per chunk.  Digit-wise steps
 // (histograms, offsets, look-back) run on the first 256 threads.
 template <typename K, int kT, int kIt>
 __global__ void __launch_bounds__(kT)
 radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
-                  K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n, int shift,
-                  int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
-                  int64_t nchunks, uint32_t* ticket, uint32_t* err, uint32_t spin_limit) {
+                  K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n_max,
+                  int shift, int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
+                  int64_t nchunks, uint32_t* ticket, uint32_t* err, uint32_t spin_limit,
+                  SortPassOpts opt) {
   constexpr int kW = kT / kWave;
   constexpr int kC = kT * kIt;
   __shared__ uint32_t s_wh[kW][256];
@@ -412,6 +440,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   __shared__ uint32_t s_goff[256];
   __shared__ uint32_t s_tmp[kW + 1];
   __shared__ uint32_t s_slot;
+  __shared__ uint32_t s_total;
   __shared__ K s_keys[kC];
   __shared__ uint32_t s_vals[kC];
   const int t = (int)threadIdx.x;
@@ -422,12 +451,27 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   // the pass's global digit count, loaded now: its latency overlaps the
   // ticket, the key loads and the ranking
   const uint32_t gcount = (uint32_t)t <= mask ? hist[t] : 0u;
+  // the keys in play: n_max, or fewer when an earlier pass dropped some
+  int64_t n = n_max;
+  if (opt.n_dev) {
+    const int64_t nd = (int64_t)*opt.n_dev;
+    n = nd < n_max ? nd : n_max;
+  }
   const int64_t chunk = take_ticket(ticket, &s_slot);  // includes a barrier
+  if (opt.fill_tail) {
+    // positions [n, n_max) get the sentinel pair (all-ones key, value)
+    for (int64_t j = n + chunk * kC + t; j < n + (chunk + 1) * kC && j < n_max; j += kT) {
+      keys_out[j] = (K)~(K)0;
+      vals_out[j] = 0xFFFFFFFFu;
+    }
+  }
+  if (chunk * kC >= n) return;  // uniform: no key of this chunk is in play
   const int64_t base = chunk * kC + (int64_t)w * (kC / kW);
   const uint64_t lt = lanemask_lt();
   K key[kIt];
   uint32_t val[kIt];
   uint32_t rank[kIt];
+  bool vld[kIt];  // the item is a key in play (in range, not dropped)
   // Every load is issued before the first ranking step (indices past the end
   // are clamped to the last element, so the loads carry no branch); ranking
   // item by item through LDS would otherwise wait out one memory latency per
@@ -450,7 +494,8 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
     const int64_t idx = base + it * kWave + lane;
-    const bool valid = idx < n;
+    const bool valid = idx < n && !(opt.drop_ones && key[it] == (K)~(K)0);
+    vld[it] = valid;
     if (!valid) key[it] = (K)0;
     const uint32_t d = (uint32_t)(key[it] >> shift) & mask;
     uint64_t peers = __ballot(valid);
@@ -478,6 +523,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     const uint32_t gbase = block_excl_scan(gcount, s_tmp, nullptr);
     uint32_t total;
     const uint32_t ds = block_excl_scan(tot, s_tmp, &total);
+    if (t == 0) s_total = total;
     if (t < 256) {
       uint32_t run = ds;
 #pragma unroll
@@ -503,8 +549,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   __syncthreads();
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
-    const int64_t idx = base + it * kWave + lane;
-    if (idx < n) {
+    if (vld[it]) {
       const uint32_t d = (uint32_t)(key[it] >> shift) & mask;
       const uint32_t pos = s_wh[w][d] + rank[it];
       s_keys[pos] = key[it];
@@ -512,8 +557,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     }
   }
   __syncthreads();
-  const int64_t rem = n - chunk * kC;
-  const int cnt = rem < kC ? (int)rem : kC;
+  const int cnt = (int)s_total;  // the chunk's keys in play (all of them unless dropped)
   for (int j = t; j < cnt; j += kT) {
     const K k = s_keys[j];
     const uint32_t d = (uint32_t)(k >> shift) & mask;
@@ -617,8 +661,10 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   const uint32_t spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   const int64_t hn = (n + kChunk - 1) / kChunk;  // histogram workgroups: 4096 keys each
   const int64_t hb = hn < 1024 ? hn : 1024;
+  // the depth sort's visible-key count, beside the pass tickets in the zeroed state
+  uint32_t* nvis = tickets + 10;
   hipLaunchKernelGGL((radix_hist_kernel<K, kDepthKeys>), dim3((unsigned)hb), dim3(kThreads), 0, st,
-                     keys_in, n, pl, hist, depths, tiles_touched, dkeys_out);
+                     keys_in, n, pl, hist, depths, tiles_touched, dkeys_out, nvis);
   const K* src_k = kDepthKeys ? (const K*)dkeys_out : keys_in;
   const uint32_t* src_v = vals_in;
   int shift = begin;
@@ -626,14 +672,25 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
     const bool to_out = ((pl.passes - 1 - pass) % 2) == 0;
     K* dk = to_out ? keys_out : tk;
     uint32_t* dv = to_out ? vals_out : tv;
+    // depth keys: the culled Gaussians (all-ones keys) leave in the first
+    // pass; the later passes sort the visible ones, and the last fills the
+    // tail with sentinels
+    SortPassOpts opt{};
+    if (kDepthKeys) {
+      opt.drop_ones = pass == 0;
+      opt.n_dev = pass > 0 ? nvis : nullptr;
+      opt.fill_tail = pass == pl.passes - 1;
+    }
     if (items == 8)
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit);
+                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit,
+                         opt);
     else
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 4>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit);
+                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit,
+                         opt);
     const int32_t e2 = check_launch("radix_pass");
     if (e2 != FGS_OK) return e2;
     shift += pl.bits[pass];
@@ -930,7 +987,8 @@ __device__ __forceinline__ int rec_st(uint32_t w, int k, const StGrid& sg) {
 // kStRecSet mean a set) and sets[4i..4i+3] (the masks, or the set).
 __global__ void __launch_bounds__(kL1Group)
 l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ order,
-                const float* __restrict__ xys, const float* __restrict__ conic_opacity,
+                const uint32_t* __restrict__ nvis, const float* __restrict__ xys,
+                const float* __restrict__ conic_opacity,
                 const uint32_t* __restrict__ tiles_touched, const uint32_t* __restrict__ st_base,
                 const uint64_t* __restrict__ st_masks, uint32_t* __restrict__ recw,
                 uint64_t* __restrict__ sets, uint32_t* __restrict__ cnt1) {
@@ -940,7 +998,10 @@ l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
   s_cnt[t] = 0;
   uint64_t m[4] = {0ull, 0ull, 0ull, 0ull};
   uint32_t w = 0u;
-  if (i < P) {
+  // entries from the visible count on are the sort's sentinel tail (culled
+  // Gaussians): nothing to read, and l1_place does not read them back
+  const int nv = nvis ? (int)min((uint32_t)P, *nvis) : P;
+  if (i < nv) {
     const uint32_t g = order[i];
     if (g < (uint32_t)P) {
       w = st_base ? st_base[g] : 0u;
@@ -1067,6 +1128,7 @@ constexpr int kL1Pairs = 2048;  // LDS pair capacity per round
 template <bool kCarry>
 __global__ void __launch_bounds__(kL1Group)
 l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
+                const uint32_t* __restrict__ nvis,
                 const uint32_t* __restrict__ skeys, const uint32_t* __restrict__ recw,
                 const uint64_t* __restrict__ sets, const uint32_t* __restrict__ cnt1,
                 const uint32_t* __restrict__ segsum, const uint32_t* __restrict__ st_start,
@@ -1085,7 +1147,9 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
   const int i = (int)blockIdx.x * kL1Group + t;
   uint64_t m[4] = {0ull, 0ull, 0ull, 0ull};
   uint32_t g = 0, rw = 0, db = 0;
-  if (i < P) {
+  // the sentinel tail from the visible count on was not written by l1_count
+  const int nv = nvis ? (int)min((uint32_t)P, *nvis) : P;
+  if (i < nv) {
     const uint4* src = reinterpret_cast<const uint4*>(sets + 4 * (size_t)i);
     const uint4 a = src[0], b = src[1];
     m[0] = (uint64_t)a.x | ((uint64_t)a.y << 32);
@@ -1580,6 +1644,11 @@ static DepthLayout depth_layout(int32_t P) {
 static const uint32_t* depth_err_word(const char* dws, int32_t P) {
   return sort_err_word<uint32_t>((void*)(dws + depth_layout(P).sort), P);
 }
+// Its count of visible Gaussians (the entries of the order before the
+// sentinel tail), two words after the error word in the sort's state.
+static const uint32_t* depth_nvis_word(const char* dws, int32_t P) {
+  return depth_err_word(dws, P) + 2;
+}
 
 // The P Gaussians by depth bits, culled ones last (keys made inside the
 // histogram kernel); the order lands at D.order of dws.
@@ -1878,9 +1947,10 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     uint32_t* tile_start = (uint32_t*)(ws + L.tile_start);
     const unsigned nwg1 = ceil_div_u(P, kL1Group);
     uint32_t* recw = (uint32_t*)(ws + L.recw);
+    const uint32_t* nvis = depth_nvis_word(dws, P);
     hipLaunchKernelGGL(l1_count_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, io->mult, order,
-                       io->xys, io->conic_opacity, io->tiles_touched, io->st_base, io->st_masks,
-                       recw, sets, cnt1);
+                       nvis, io->xys, io->conic_opacity, io->tiles_touched, io->st_base,
+                       io->st_masks, recw, sets, cnt1);
     hipLaunchKernelGGL(l1_seg_scan_kernel, dim3(kL1Segs), dim3(kMaxSt), 0, st, (int)nwg1, sg.S,
                        cnt1, segsum);
     hipLaunchKernelGGL(l1_top_scan_kernel, dim3(1), dim3(kMaxSt), 0, st, sg.S, segsum, st_start,
@@ -1890,10 +1960,10 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     uint32_t* ldb = carry ? (uint32_t*)(ws + L.ldb) : nullptr;
     if (carry)
       hipLaunchKernelGGL(l1_place_kernel<true>, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order,
-                         skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
+                         nvis, skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
     else
       hipLaunchKernelGGL(l1_place_kernel<false>, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order,
-                         skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
+                         nvis, skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
     hipLaunchKernelGGL(l1_wide_masks_kernel, dim3(kWideGroups), dim3(256), 0, st, sg, io->mult,
                        st_start, P, io->xys, io->conic_opacity, list, K, masks);
     const unsigned nch = (unsigned)L.max_chunks;
