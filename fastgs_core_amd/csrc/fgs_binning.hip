@@ -626,6 +626,11 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
     return FGS_OK;
   }
   const SortPlan pl = sort_plan(begin, end);
+  // depth keys drop the culled Gaussians in pass 0 (which runs on all n) and
+  // fill the sentinel tail in the last pass over the visible count, so they
+  // need two distinct passes
+  if (kDepthKeys && pl.passes < 2)
+    return set_error(FGS_ERR_UNSUPPORTED, "radix_sort_pairs: depth keys need >= 2 passes");
   if (pl.passes == 0) {
     int64_t blocks = (n + 255) / 256;
     if (blocks > 65536) blocks = 65536;

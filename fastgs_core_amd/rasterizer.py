@@ -541,13 +541,20 @@ def _poll_host_word(word, dev, timeout_s: float = 5.0):
     v = int(view[0])
     if (v & 0xFFFFFFFF) == 0xFFFFFFFF:
         t0 = time.perf_counter()
+        spins = 0
         while (v & 0xFFFFFFFF) == 0xFFFFFFFF:
-            if time.perf_counter() - t0 > timeout_s:
+            el = time.perf_counter() - t0
+            if el > timeout_s:
                 torch.cuda.current_stream(dev).synchronize()
                 v = int(view[0])
                 if (v & 0xFFFFFFFF) == 0xFFFFFFFF:
                     raise RuntimeError("fgs_binning_sorted did not write its host result")
                 break
+            # a tight spin for the first ~50 us (the usual wait), then yield
+            # the GIL and the core to the process's other threads
+            spins += 1
+            if el > 5e-5:
+                time.sleep(0 if el < 1e-3 else 1e-4)
             v = int(view[0])
     _HOST_WORDS.free.append(word)
     return v & 0xFFFFFFFF, (v >> 32) & 0xFFFFFFFF

@@ -326,8 +326,11 @@ typedef struct {
 size_t fgs_binning_workspace_bytes(int32_t P, int64_t num_rendered, int32_t num_tiles);
 int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream);
 
-/* The first stage of fgs_binning_sorted on its own: the P Gaussians ordered
- * by depth bits (stable; culled ones, tiles_touched == 0, last).  It needs
+/* The first stage of fgs_binning_sorted on its own: the visible Gaussians
+ * (tiles_touched > 0) ordered by depth bits (stable).  The order buffer holds
+ * them in its first nvis entries, followed by 0xFFFFFFFF sentinels up to P
+ * (the culled Gaussians are dropped, so it is not a permutation of [0, P));
+ * the count nvis stays in depth_workspace for fgs_binning_sorted.  It needs
  * only P, so a caller can enqueue it before the blocking read of
  * K = point_offsets[P-1] (binding.cpp:25-31,153-154) and the GPU sorts while
  * the host waits; the result is passed as fgs_binning_io.depth_order.  No

@@ -46,6 +46,7 @@ typedef double real;
 #define ORC_LOG2E 1.4426950408889634
 #define RFMA(a, b, c) fma(a, b, c)
 #define RLOG(x) log(x)
+#define REXP_LIBM(x) exp(x)
 #else
 typedef float real;
 #define RSQRT(x) sqrtf(x)
@@ -59,6 +60,7 @@ typedef float real;
 #define ORC_LOG2E 1.44269504088896341f
 #define RFMA(a, b, c) fmaf(a, b, c)
 #define RLOG(x) orc_logf(x)
+#define REXP_LIBM(x) expf(x)
 #endif
 
 #define ORC_TILE 16
@@ -664,6 +666,13 @@ typedef struct {
   int64_t bucket_sum;
   int32_t get_flag;
   int32_t write_sampled;
+  /* 0: the blend in the HIP kernels' operation order (base-2 exponent,
+   * orc_blend_exp2f, T (1 - alpha) as one fused multiply-add): the parity
+   * oracle.  1: the reference's own order (fastgs_rasterize.metal:104-118):
+   * power = -1/2 (a dx dx + c dy dy) - b dx dy, alpha = min(0.99, o exp(power))
+   * with libm expf, test_T = T (1 - alpha) rounded twice.  Mode 1 exists to
+   * measure how often the two orders take a different blend decision. */
+  int32_t ref_order;
 } orc_rparams;
 
 /* All outputs zero-filled by the caller.  colors has row stride
@@ -719,12 +728,21 @@ void orc_rasterize_fwd(const orc_rparams* rp, const uint32_t* ranges, const uint
           real dx = means2d[2 * (size_t)g] - pxf;
           real dy = means2d[2 * (size_t)g + 1] - pyf;
           const real* co = conic_opacity + 4 * (size_t)g;
-          real t2 = splat_power(co, dx, dy); /* log2(e) power */
-          if (t2 > (real)0) continue;
-          real alpha = RMIN((real)0.99, co[3] * RBEXP2(t2));
-          if (alpha < (real)1 / (real)255) continue;
-          /* T (1 - alpha) as one fused multiply-add, the HIP kernel's form */
-          real test_t = RFMA(-alpha, T, T);
+          real alpha, test_t;
+          if (rp->ref_order) {
+            real power = (real)-0.5 * (co[0] * dx * dx + co[2] * dy * dy) - co[1] * dx * dy;
+            if (power > (real)0) continue;
+            alpha = RMIN((real)0.99, co[3] * REXP_LIBM(power));
+            if (alpha < (real)1 / (real)255) continue;
+            test_t = T * ((real)1 - alpha);
+          } else {
+            real t2 = splat_power(co, dx, dy); /* log2(e) power */
+            if (t2 > (real)0) continue;
+            alpha = RMIN((real)0.99, co[3] * RBEXP2(t2));
+            if (alpha < (real)1 / (real)255) continue;
+            /* T (1 - alpha) as one fused multiply-add, the HIP kernel's form */
+            test_t = RFMA(-alpha, T, T);
+          }
           if (test_t < (real)0.0001) break;
           for (int c = 0; c < C; ++c) acc[c] += colors[(size_t)g * NC + c] * alpha * T;
           if (rp->get_flag && metric_map[pix] == 1) {

@@ -25,7 +25,15 @@ Parity status of each C function (how it is pinned; see tests/test_oracle_*):
   orc_sort_pairs_u64       : numpy stable argsort.
   orc_tile_ranges          : reference KAT (tile_prep_smoke, hand-derived).
   orc_rasterize_fwd        : closed form single splat (rasterize_smoke), brute
-                             force per-pixel compositing on tiny scenes.
+                             force per-pixel compositing on tiny scenes, and a
+                             float64 array formulation (cumulative products
+                             over list positions) of n_contrib as a position,
+                             max_contrib, metric_count, final_T, the sampled
+                             state (including the slots left zero after a
+                             break) on multi-bucket ragged tiles
+                             (test_oracle_raster_state).  ref_order=True: the
+                             reference's operation order, used to measure how
+                             often the mirrored order decides differently.
   orc_rasterize_bwd        : central finite differences of the double build.
   orc_rasterize_bwd_mag    : equal to the per-pixel sums of |gradient| of the
   orc_preprocess_bwd_mag     FD-pinned backward, bound the gradients, bound the
@@ -73,6 +81,7 @@ class OrcRParams(ctypes.Structure):
         ("bucket_sum", c_int64),
         ("get_flag", c_int32),
         ("write_sampled", c_int32),
+        ("ref_order", c_int32),
     ]
 
 
@@ -235,7 +244,10 @@ class Oracle:
     def rasterize_fwd(self, ranges, point_list, bucket_offsets, means2d, colors, conic_opacity,
                       background, metric_map, image_width, image_height, num_channels=3,
                       num_tiles=None, bucket_sum=None, get_flag=False, write_sampled=False,
-                      num_points=None):
+                      num_points=None, ref_order=False):
+        """orc_rasterize_fwd.  ``ref_order``: evaluate the blend in the
+        reference's operation order (libm expf of the natural-base power,
+        T (1 - alpha) with two roundings) in place of the HIP kernels' order."""
         gx = (image_width + TILE - 1) // TILE
         gy = (image_height + TILE - 1) // TILE
         if num_tiles is None:
@@ -260,7 +272,7 @@ class Oracle:
             "metric_count": np.zeros(P if get_flag else 0, np.int32),
         }
         rp = OrcRParams(image_width, image_height, num_channels, num_tiles, bucket_sum,
-                        int(get_flag), int(write_sampled))
+                        int(get_flag), int(write_sampled), int(ref_order))
         mm = np.ascontiguousarray(metric_map, np.int32) if metric_map is not None else \
             np.zeros(HW, np.int32)
         self.lib.orc_rasterize_fwd(
@@ -296,7 +308,7 @@ class Oracle:
             "conic_opacity": np.zeros((P, 4), dt),
             "viewspace_points": np.zeros((P, 4), dt),
         }
-        rp = OrcRParams(image_width, image_height, num_channels, num_tiles, 0, 0, 0)
+        rp = OrcRParams(image_width, image_height, num_channels, num_tiles, 0, 0, 0, 0)
         aw = 10 + num_channels
         mag = np.zeros((P, 2, aw), np.float64) if magnitude else None
         fn = self.lib.orc_rasterize_bwd_mag

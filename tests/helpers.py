@@ -7,7 +7,10 @@ gradients within 1e-3 relative.  A gradient entry is a sum of per-(pixel,
 splat) terms that the GPU adds with float atomics in no fixed order, so
 "relative" is taken to the sum of the magnitudes of those terms, which the
 oracle computes alongside the gradients (Oracle.render_backward(...,
-magnitude=True)): |got - ref| <= 1e-3 * sum |terms| for every entry.
+magnitude=True)): |got - ref| <= 1e-3 * sum |terms| for every entry.  On
+the well-conditioned entries, whose |ref| is at least a tenth of sum |terms|,
+the plain relative bound |got - ref| <= 1e-3 * |ref| must hold as well, so a
+wrong sign or a dropped term there cannot hide in a large magnitude sum.
 """
 from __future__ import annotations
 
@@ -54,10 +57,15 @@ def scene_small(seed=0, P=2000, degree=3, W=128, H=96, eye=None):
     return sc, cam
 
 
+WELL_CONDITIONED = 0.1
+
+
 def assert_grad_gate(name, got, ref, mag, rtol=GRAD_RTOL):
     """Every entry: |got - ref| <= rtol * mag, mag = the sum of the magnitudes
     of the entry's terms (the oracle's ``mag_terms``).  Entries with no terms
-    must match exactly.  Prints the worst entry relative to its gate."""
+    must match exactly.  Entries with |ref| >= WELL_CONDITIONED * mag must
+    also satisfy |got - ref| <= rtol * |ref|.  Prints the worst entry relative
+    to its gate."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     mag = np.asarray(mag, np.float64)
@@ -67,14 +75,19 @@ def assert_grad_gate(name, got, ref, mag, rtol=GRAD_RTOL):
     err = np.abs(got - ref)
     tol = rtol * mag
     bad = ~(err <= tol)
+    well = np.abs(ref) >= WELL_CONDITIONED * mag
+    bad_rel = well & ~(err <= rtol * np.abs(ref))
     with np.errstate(divide="ignore", invalid="ignore"):
         r = np.where(mag > 0, err / mag, np.where(err > 0, np.inf, 0.0))
+        rr = np.where(well & (ref != 0), err / np.abs(ref), 0.0)
     i = int(np.argmax(r))
+    j = int(np.argmax(rr))
     info = (f"{name}: {int(bad.sum())}/{ref.size} entries outside 1e-3 * sum|terms|; worst flat "
             f"index {i}: got {got.flat[i]!r} ref {ref.flat[i]!r} sum|terms| {mag.flat[i]!r} "
-            f"(err / sum|terms| = {r.flat[i]:.2e})")
+            f"(err / sum|terms| = {r.flat[i]:.2e}); {int(bad_rel.sum())}/{int(well.sum())} "
+            f"well-conditioned entries outside 1e-3 * |ref| (worst {rr.flat[j]:.2e} at {j})")
     print("[gate]", info, flush=True)
-    if bad.any():
+    if bad.any() or bad_rel.any():
         raise AssertionError(info)
 
 
