@@ -23,6 +23,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3]
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import gc
 import json
 import math
@@ -148,20 +149,22 @@ def reference_init(torch, dev, seed, P, degree):
 
 def run_densify_loop(args):
     """the training loop of train_scanner_fastgs.py:968-1060
-    on the GPU state.  Per iteration: a camera popped from a seeded viewpoint
-    stack, render at the active SH degree (0 below iteration 1000, +1 per
-    1000), MSE loss (the reference's loss up to --mse-until 600; fused kernels), backward,
-    the densification statistics from this render's radii and viewspace
-    gradient, the learning-rate schedule and the FastGS Adam cadence.  Every
-    ``interval`` iterations: the metric-map scores over 10 sampled cameras
-    (two renders each) and densify_and_prune_fastgs.  The timed region is the
-    whole loop, densification included; targets are rendered beforehand."""
+    on the GPU state (fastgs_core_amd.densify.FastGSTrainLoop).  Per iteration:
+    a camera popped from a seeded viewpoint stack, render at the active SH
+    degree (0 below iteration 1000, +1 per 1000), MSE loss (the reference's
+    loss up to --mse-until 600; fused kernels), backward, the learning-rate
+    schedule and the FastGS Adam cadence, then the densification statistics
+    from the viewspace gradient and the radii of --stats-render (default: the
+    reference's second render after the optimizer step).  Every ``interval``
+    iterations: the metric-map scores over 10 sampled cameras (two renders
+    each) and densify_and_prune_fastgs.  The timed region is the whole loop,
+    densification included; targets are rendered beforehand."""
     import torch
 
     import fastgs_core
-    import fastgs_core_amd
     from fastgs_core_amd import synthetic as syn
-    from fastgs_core_amd.densify import DensifyConfig, GaussianTrainState, compute_scene_extent
+    from fastgs_core_amd.densify import (DensifyConfig, FastGSTrainLoop, GaussianTrainState,
+                                         LoopConfig, compute_scene_extent)
 
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
     dev = torch.device("cuda", 0)
@@ -204,51 +207,35 @@ def run_densify_loop(args):
     del hidden
     start = reference_init(torch, dev, c["start_seed"], c["P_start"], deg)
     dcfg = DensifyConfig(grad_thresh=c["grad_thresh"])
-    mse_until, sh_interval = c["mse_until"], 1000
+    lcfg = LoopConfig(interval=c["interval"], densify_from=0, mse_until=c["mse_until"],
+                      stats_render=args.stats_render)
 
     def loop(n_iter, record, interval):
         ts = GaussianTrainState(start)
-        extent = compute_scene_extent(ts.param("means3d").detach())
         gen = torch.Generator(device=dev)
         gen.manual_seed(5)
-        rng = np.random.default_rng(42)
-        stack = []
+        tl = FastGSTrainLoop(ts, render, targets, len(cams), deg, dcfg,
+                             dataclasses.replace(lcfg, interval=interval),
+                             compute_scene_extent(ts.param("means3d").detach()), seed=42,
+                             generator=gen)
         losses = torch.zeros(max(n_iter, 1), device=dev)
         events = []
         for it in range(1, n_iter + 1):
-            ts.update_learning_rate(it)
-            active = min(it // sh_interval, deg)
-            if not stack:
-                stack = list(range(len(cams)))
-            idx = stack.pop(int(rng.integers(0, len(stack))))
-            vsp = torch.zeros((ts.P, 4), device=dev, requires_grad=True)
-            out = render(ts, idx, active, vsp=vsp)
-            img = out["out_color"].reshape(3, HW)
-            loss = (fastgs_core_amd.mse_loss(img, targets[idx]) if it <= mse_until
-                    else fastgs_core_amd.l1_loss(img, targets[idx]))
-            ts.zero_grad()
-            loss.backward()
-            losses[it - 1] = loss.detach()
-            ts.update_densification_stats(out["radii"], vsp.grad)
-            ts.step(it)
-            if it % interval == 0:
+            loss, _ = tl.train_iteration(it)
+            losses[it - 1] = loss
+            if tl.is_densify_event(it):
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)
                 e0.record()
-                ids = rng.choice(len(cams), size=min(dcfg.densify_camera_sample, len(cams)),
-                                 replace=False)
-                with torch.no_grad():
-                    imp, prn = ts.compute_gaussian_scores_fastgs(
-                        lambda i, mm: render(ts, i, active, metric_map=mm), targets,
-                        [int(i) for i in ids], dcfg.loss_thresh, True)
                 before = ts.P
-                info = ts.densify_and_prune_fastgs(dcfg, extent, imp, prn, generator=gen)
+                info = tl.densify_event(it)
                 e1.record()
                 if record:
                     events.append(dict(iteration=it, before=before, after=ts.P, start=e0,
                                        end=e1, **{k: info[k] for k in (
                                            "metric_hits", "cloned", "split_sources",
                                            "total_prune_candidates", "actual_removed")}))
+            tl.after_iteration(it)
         return ts, losses, events
 
     # warm-up on a throwaway state, its last iteration a densification
@@ -272,7 +259,8 @@ def run_densify_loop(args):
         "config": {"workload": c["desc"], "gaussians_start": c["P_start"],
                    "gaussians_hidden": c["P_hidden"], "width": W, "height": H,
                    "sh_degree": deg, "cameras": c["cameras"], "interval": c["interval"],
-                   "grad_thresh": c["grad_thresh"], "mse_until": c["mse_until"]},
+                   "grad_thresh": c["grad_thresh"], "mse_until": c["mse_until"],
+                   "stats_render": args.stats_render},
         "final_gaussians": ts.P, "capacity": ts.capacity, "reallocations": ts.reallocations,
         "densify_events": events, "densify_ms_total": float(sum(dens_ms)),
         "train_ms_per_iter": (dt * 1e3 - float(sum(dens_ms))) / max(iterations, 1),
@@ -413,9 +401,28 @@ def measured_traffic(config, stage):
 
 
 def _cpu_model() -> str:
+    """The host CPU as lscpu names it (model name, family / model / stepping,
+    sockets), else /proc/cpuinfo's model name."""
+    import subprocess
+
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        f = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                f[k.strip()] = v.strip()
+        if f.get("Model name"):
+            desc = f["Model name"]
+            extra = [f"{k.lower()} {f[k]}" for k in ("CPU family", "Model", "Stepping") if k in f]
+            if "Socket(s)" in f:
+                extra.append(f"{f['Socket(s)']} socket(s)")
+            return f"{desc} ({', '.join(extra)})" if extra else desc
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
                 if line.startswith("model name"):
                     return line.split(":", 1)[1].strip()
     except OSError:
@@ -447,34 +454,44 @@ def cpu_baseline(cfg, sc, cams, seed=0):
     win = gaussian_window(torch)
 
     def one_step():
+        tm = {}
         t0 = time.perf_counter()
-        fwd = orc.render(inp, W, H, cam.tan_fovx, cam.tan_fovy, cfg["degree"])
+        fwd = orc.render(inp, W, H, cam.tan_fovx, cam.tan_fovy, cfg["degree"], timings=tm)
+        t1 = time.perf_counter()
         img = torch.from_numpy(fwd["out_color"].reshape(3, H, W).copy()).requires_grad_(True)
         loss = (img - target).abs().mean() + 0.2 * (1 - ssim(torch, F, img, target, win))
         loss.backward()
-        orc.render_backward(inp, fwd, img.grad.numpy().reshape(3, -1), W, H, cam.tan_fovx,
-                            cam.tan_fovy, cfg["degree"])
-        return time.perf_counter() - t0
+        dL = img.grad.numpy().reshape(3, -1)
+        tm["loss_fwd_bwd"] = time.perf_counter() - t1
+        orc.render_backward(inp, fwd, dL, W, H, cam.tan_fovx, cam.tan_fovy, cfg["degree"],
+                            timings=tm)
+        return time.perf_counter() - t0, tm
+
+    def ms(tm):
+        return {k: round(v * 1e3, 2) for k, v in tm.items()}
 
     torch_threads = torch.get_num_threads()
     orc.lib.orc_set_num_threads(ncpu)
     torch.set_num_threads(ncpu)
-    multi = sorted(one_step() for _ in range(3))
+    runs = [one_step() for _ in range(3)]
     orc.lib.orc_set_num_threads(1)
     torch.set_num_threads(1)
-    single = one_step()
+    single, single_tm = one_step()
     orc.lib.orc_set_num_threads(ncpu)
     torch.set_num_threads(torch_threads)
+    multi = sorted(r[0] for r in runs)
     dt = multi[1]
+    stages = {k: float(np.median([r[1][k] for r in runs])) for k in runs[0][1]}
     model = _cpu_model()
     return {"value": 1.0 / dt, "unit": "iters/s", "cores": ncpu, "kind": "port",
-            "model": model, "single_thread": {"value": 1.0 / single, "unit": "iters/s",
-                                              "cores": 1, "seconds": single},
+            "model": model, "stages_ms": ms(stages),
+            "single_thread": {"value": 1.0 / single, "unit": "iters/s", "cores": 1,
+                              "seconds": single, "stages_ms": ms(single_tm)},
             "sample": f"pose 0 of {cfg['desc']}: full training step (forward, L1+SSIM loss "
                       f"gradient, backward) of the C oracle (CPU restatement of the reference "
                       f"Metal semantics); median of 3 steps on {ncpu} threads of {model} "
-                      f"({', '.join(f'{x:.2f}' for x in multi)} s), and 1 step on 1 thread "
-                      f"({single:.2f} s)"}
+                      f"({', '.join(f'{x:.2f}' for x in multi)} s; stages_ms: the per-stage "
+                      f"medians), and 1 step on 1 thread ({single:.2f} s)"}
 
 
 def main():
@@ -484,6 +501,9 @@ def main():
                     help="timed steps (default 20; the cfg5 loop runs its 500 iterations)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg5", "cfg5-grow"])
+    ap.add_argument("--stats-render", default="post_step", choices=("post_step", "train"),
+                    help="cfg5: radii of the densification statistics from a second render "
+                         "after the optimizer step (the reference's) or from the training render")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-profile", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
@@ -662,6 +682,9 @@ def main():
             if mb is not None:  # FETCH_SIZE + WRITE_SIZE of the stage's main kernel(s)
                 stages[name]["measured_bytes"] = mb
                 stages[name]["measured_GBps"] = mb / ((kms if kms is not None else ms) * 1e-3) / 1e9
+                # the measured bytes over the same time against the HBM peak
+                # (beside frac, which counts the algorithmic bytes or flops)
+                stages[name]["frac_measured"] = stages[name]["measured_GBps"] / HBM_PEAK_GBS
         # roofline of the dominant kernel: the longest of the stages' main
         # kernels (the binning stage is a chain of kernels and has none), over
         # its own launch time

@@ -501,3 +501,139 @@ class GaussianTrainState:
         d.update(means3d=self._leaves["means3d"], dc=self._leaves["features_dc"],
                  sh=self._leaves["features_rest"], opacities=o.view(-1), scales=s, rotations=r)
         return d
+
+
+# ---------------------------------------------------------------------- loop
+@dataclass
+class LoopConfig:
+    """The schedule of the FastGS training loop (train_scanner_fastgs.py:968-1060,
+    defaults of :799-849 except where a workload sets them).
+
+    ``stats_render``: where the densification statistics take their radii.
+    "post_step" is the reference's: a second forward render of the same
+    camera after the optimizer step (:1014-1019).  "train" takes them from the
+    training render itself (one render fewer per iteration; the radii then
+    describe the pre-step parameters, so ``max_radii2d`` and the ``radii > 0``
+    mask can differ from the reference's on the same draws)."""
+    interval: int = 500
+    densify_from: int = 500
+    densify_until: int = 15000
+    mse_until: int = 600
+    sh_interval: int = 1000
+    opacity_reset_interval: int = 3000
+    final_prune_start: int = 15000
+    final_prune_end: int = 30000
+    final_prune_interval: int = 3000
+    stats_render: str = "post_step"
+
+
+class FastGSTrainLoop:
+    """One iteration of the reference loop at a time on a GaussianTrainState.
+
+    ``render(ts, idx, degree, metric_map=None, vsp=None)`` renders camera
+    ``idx`` with the state's current rows and returns the
+    ``rasterize_gaussians`` dict; ``targets[idx]`` is ``[3, H*W]``.  Cameras
+    are popped from a seeded viewpoint stack (:974-978); the loss is MSE up to
+    ``mse_until`` and L1 after (:960-963); Adam follows the FastGS cadence.
+    The statistics accumulate while ``it < densify_until``; a densification
+    event runs at ``it > densify_from`` and ``it % interval == 0`` (:1021):
+    metric-map scores over ``densify_camera_sample`` sampled cameras, then
+    densify_and_prune_fastgs.  The opacity reset (:1047-1049) and the final
+    prune (:1051-1060) follow their intervals."""
+
+    def __init__(self, ts: GaussianTrainState, render: Callable, targets: Sequence[torch.Tensor],
+                 n_cameras: int, degree: int, dcfg: DensifyConfig, lcfg: LoopConfig,
+                 scene_extent: float, seed: int = 42,
+                 generator: Optional[torch.Generator] = None):
+        import numpy as np
+
+        from .loss import l1_loss, mse_loss
+
+        if lcfg.stats_render not in ("post_step", "train"):
+            raise ValueError("stats_render must be 'post_step' or 'train'")
+        self.ts, self.render, self.targets = ts, render, targets
+        self.n_cameras, self.degree = int(n_cameras), int(degree)
+        self.dcfg, self.lcfg, self.extent = dcfg, lcfg, float(scene_extent)
+        self.rng = np.random.default_rng(seed)
+        self.gen = generator
+        self.stack: List[int] = []
+        self._losses = (mse_loss, l1_loss)
+        self.last_stats = None  # (radii, d_viewspace) of the last statistics update
+
+    def active_degree(self, it: int) -> int:
+        return min(it // self.lcfg.sh_interval, self.degree)
+
+    def train_iteration(self, it: int):
+        """Forward, loss, backward, Adam step and the statistics of iteration
+        ``it`` (1-based).  Returns (loss tensor, camera index)."""
+        ts, lc = self.ts, self.lcfg
+        ts.update_learning_rate(it)
+        active = self.active_degree(it)
+        if not self.stack:
+            self.stack = list(range(self.n_cameras))
+        idx = self.stack.pop(int(self.rng.integers(0, len(self.stack))))
+        vsp = torch.zeros((ts.P, 4), device=ts.dev, requires_grad=True)
+        out = self.render(ts, idx, active, vsp=vsp)
+        img = out["out_color"].reshape(3, -1)
+        mse_loss, l1_loss = self._losses
+        loss = mse_loss(img, self.targets[idx]) if it <= lc.mse_until else \
+            l1_loss(img, self.targets[idx])
+        ts.zero_grad()
+        loss.backward()
+        ts.step(it)
+        self.last_stats = None
+        if it < lc.densify_until:
+            if lc.stats_render == "post_step":
+                with torch.no_grad():
+                    radii = self.render(ts, idx, active)["radii"]
+            else:
+                radii = out["radii"]
+            ts.update_densification_stats(radii, vsp.grad)
+            self.last_stats = (radii, vsp.grad)
+        return loss.detach(), idx
+
+    def is_densify_event(self, it: int) -> bool:
+        lc = self.lcfg
+        return it < lc.densify_until and it > lc.densify_from and it % lc.interval == 0
+
+    def sample_cameras(self) -> List[int]:
+        """sample_camera_indices (:262-276)."""
+        n = min(self.dcfg.densify_camera_sample, self.n_cameras)
+        return [int(i) for i in self.rng.choice(self.n_cameras, size=n, replace=False)]
+
+    def scores(self, it: int, ids: Sequence[int], densify: bool = True, on_render=None):
+        """compute_gaussian_scores_fastgs over cameras ``ids`` at the active
+        degree.  ``on_render(out)`` sees each render (tests)."""
+        active = self.active_degree(it)
+
+        def r(i, mm):
+            o = self.render(self.ts, i, active, metric_map=mm)
+            if on_render is not None:
+                on_render(o)
+            return o
+
+        with torch.no_grad():
+            return self.ts.compute_gaussian_scores_fastgs(r, self.targets, ids,
+                                                          self.dcfg.loss_thresh, densify)
+
+    def densify_event(self, it: int) -> Dict[str, int]:
+        """The event of iteration ``it``: scores over the sampled cameras, then
+        densify_and_prune_fastgs with draws from the loop's generator."""
+        imp, prn = self.scores(it, self.sample_cameras(), True)
+        return self.ts.densify_and_prune_fastgs(self.dcfg, self.extent, imp, prn,
+                                                generator=self.gen)
+
+    def after_iteration(self, it: int) -> Optional[Dict[str, int]]:
+        """The opacity reset and the final prune of iteration ``it`` (run after
+        any densification event of the same iteration)."""
+        lc = self.lcfg
+        if it < lc.densify_until and lc.opacity_reset_interval > 0 and \
+                it % lc.opacity_reset_interval == 0:
+            self.ts.reset_opacity_logits(self.dcfg.opacity_reset_value)
+        if lc.final_prune_interval > 0 and it % lc.final_prune_interval == 0 and \
+                lc.final_prune_start < it < lc.final_prune_end:
+            _, prn = self.scores(it, self.sample_cameras(), False)
+            return self.ts.final_prune_fastgs(self.dcfg.final_prune_min_opacity, prn,
+                                              self.dcfg.final_prune_score_thresh,
+                                              self.dcfg.final_prune_min_gaussians)
+        return None

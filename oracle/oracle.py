@@ -408,8 +408,19 @@ class Oracle:
     # -- full pipeline (binding.cpp:33-282) ------------------------------
     def render(self, inputs: dict, image_width: int, image_height: int, tan_fovx=1.0,
                tan_fovy=1.0, degree=0, scale_modifier=1.0, mult=1.0, get_flag=False,
-               write_sampled=False):
-        """Forward of ``rasterize_gaussians`` on numpy inputs (reference key names)."""
+               write_sampled=False, timings: dict | None = None):
+        """Forward of ``rasterize_gaussians`` on numpy inputs (reference key names).
+        ``timings``: a dict that receives the wall seconds of each stage
+        (preprocess_fwd, scan, duplicate, sort, ranges, rasterize_fwd)."""
+        import time
+
+        clock = [time.perf_counter()]
+
+        def lap(name):
+            if timings is not None:
+                t = time.perf_counter()
+                timings[name] = timings.get(name, 0.0) + t - clock[0]
+                clock[0] = t
         col = inputs.get("colors_precomp", inputs.get("colors"))
         has_col = col is not None and np.asarray(col).size != 0
         has_sh = "dc" in inputs and "sh" in inputs
@@ -438,8 +449,10 @@ class Oracle:
             sh=inputs.get("sh") if not has_col else None, colors_precomp=col if has_col else None,
             scales=sc if not has_cov else None, rotations=rot if not has_cov else None,
             cov3d_precomp=cov if has_cov else None)
+        lap("preprocess_fwd")
         point_offsets = self.inclusive_scan(pre["tiles_touched"])
         K = int(point_offsets[-1]) if P else 0
+        lap("scan")
         out = {"rendered": K, "num_buckets": 0, "radii": pre["radii"],
                "point_offsets": point_offsets, "pre": pre, "num_tiles": T,
                "viewspace_points": pre["viewspace_points"], "geom_means2d": pre["xys"],
@@ -451,10 +464,13 @@ class Oracle:
         keys_u, vals_u = self.duplicate_with_keys(pre["xys"], pre["depths"], point_offsets,
                                                   pre["conic_opacity"], pre["tiles_touched"],
                                                   mult, gx, gy, K)
+        lap("duplicate")
         keys, vals = self.sort_pairs(keys_u, vals_u)
+        lap("sort")
         ranges, bucket_count = self.tile_ranges(keys, T)
         bucket_offsets = self.inclusive_scan(bucket_count)
         B = int(bucket_offsets[-1])
+        lap("ranges")
         out.update({"point_list_keys_unsorted": keys_u, "point_list_unsorted": vals_u,
                     "point_list_keys": keys, "point_list": vals, "ranges": ranges,
                     "bucket_count": bucket_count, "bucket_offsets": bucket_offsets,
@@ -465,6 +481,7 @@ class Oracle:
         r = self.rasterize_fwd(ranges, vals, bucket_offsets, pre["xys"], pre["rgb"],
                                pre["conic_opacity"], inputs["background"], metric_map,
                                image_width, image_height, 3, T, B, get_flag, write_sampled, P)
+        lap("rasterize_fwd")
         out["raster"] = r
         out.update({"out_color": r["out_color"], "metric_count": r["metric_count"],
                     "sample_bucket_to_tile": r["bucket_to_tile"], "sample_t": r["sampled_t"],
@@ -475,7 +492,8 @@ class Oracle:
 
     def render_backward(self, inputs: dict, fwd: dict, dL_dout_color, image_width, image_height,
                         tan_fovx=1.0, tan_fovy=1.0, degree=0, scale_modifier=1.0,
-                        dL_dvsp_out=None, dL_dxys_extra=None, magnitude=False):
+                        dL_dvsp_out=None, dL_dxys_extra=None, magnitude=False,
+                        timings: dict | None = None):
         """Gradients of sum(dL_dout_color * out_color) (+ optional direct cotangents of the
         preprocess outputs) w.r.t. the differentiable inputs, chained exactly as
         FastGSRasterize::vjp -> FastGSPreprocess::vjp.
@@ -486,7 +504,11 @@ class Oracle:
         terms come from rasterize_bwd; orc_preprocess_bwd_mag carries them
         through the preprocess backward's own sums and products (each sum
         taken over magnitudes), so an entry's value is the sum of |term| over
-        the fully expanded chain rule."""
+        the fully expanded chain rule.  ``timings``: receives the wall seconds of
+        rasterize_bwd and preprocess_bwd."""
+        import time
+
+        t0 = time.perf_counter()
         pre = fwd["pre"]
         P = pre["xys"].shape[0]
         dt = self.dt
@@ -502,6 +524,7 @@ class Oracle:
                   "conic_opacity": np.zeros((P, 4), dt), "viewspace_points": np.zeros((P, 4), dt)}
             if magnitude:
                 g2["mag"] = {k: np.zeros(v.shape, np.float64) for k, v in g2.items()}
+        t1 = time.perf_counter()
         dvsp = g2["viewspace_points"].copy()
         if dL_dvsp_out is not None:
             dvsp += np.asarray(dL_dvsp_out, dt)
@@ -520,6 +543,10 @@ class Oracle:
             scales=inputs.get("scales") if not has_cov else None,
             rotations=inputs.get("rotations") if not has_cov else None,
             cov3d_precomp=cov if has_cov else None, use_colors_precomp=has_col)
+        if timings is not None:
+            t2 = time.perf_counter()
+            timings["rasterize_bwd"] = timings.get("rasterize_bwd", 0.0) + t1 - t0
+            timings["preprocess_bwd"] = timings.get("preprocess_bwd", 0.0) + t2 - t1
         g["raster"] = g2
         if magnitude:
             if "mag_terms" not in g2:

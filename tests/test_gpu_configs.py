@@ -3,15 +3,16 @@ oracle on the same seeded inputs (configs[2], cfg3, is test_gpu_fullsize.py).
 
 * cfg1 (plumbing): 16,384 Gaussians at 256x256, SH 0, one forward render and
   the backward of an L1 loss against a seeded U(0,1) target.
-* cfg2: 200,000 Gaussians at 1280x720, SH 3, forward-only, two of its eight
-  seeded poses.
+* cfg2: 200,000 Gaussians at 1280x720, SH 3, forward-only, all eight seeded
+  poses.
 * cfg4 (heavy-overlap stress): 3,000,000 Gaussians at 1920x1080, SH 3, 2 % of
   them large (about 1.9e8 tile duplicates, the largest touching all 8,160
   tiles), forward and backward.
 * cfg5 (densification loop): 100,000 Gaussians from the reference's initial
-  model at 1280x720, trained for 100 iterations against targets rendered
-  from a hidden 300k scene, then the scores and one densify-and-prune event
-  against the densification oracle on the same random draws.
+  model at 1280x720, trained for its 500 iterations against targets rendered
+  from a hidden 300k scene; the scores and each of the five densify-and-prune
+  events against the densification oracle on the same random draws, then a
+  sixth event with thresholds that split and prune.
 
 Gates: integer outputs (radii, tile counts, offsets, sorted keys and
 values, ranges, bucket arrays, contributor counts) bit-exact; the image
@@ -96,10 +97,10 @@ def test_cfg1_plumbing_l1_step(oracle):
                            "viewspace_points"))
 
 
-@pytest.mark.parametrize("pose", [0, 5])
+@pytest.mark.parametrize("pose", list(range(8)))
 def test_cfg2_forward_poses(oracle, pose):
-    """200,000 Gaussians, 1280x720, SH 3, forward only; poses 0 and 5
-    of the bench's eight seeded sphere cameras."""
+    """200,000 Gaussians, 1280x720, SH 3, forward only; each of the
+    bench's eight seeded sphere cameras."""
     import fastgs_core
 
     P, W, H = 200_000, 1280, 720
@@ -162,21 +163,90 @@ def _cfg5_state(torch, dev, P_start, seed=0):
                                for k, v in scanner.init_model(pts, colors, 3).items()})
 
 
-@pytest.mark.timeout(600)
-def test_cfg5_densify_event_at_size():
-    """the reference's initial model of 100,000 points at 1280x720,
-    100 training iterations (one sphere camera each, MSE against targets of a
-    hidden 300k scene, statistics from the viewspace gradients, the Adam
-    cadence), then the event of iteration 100: metric-map scores over 10
-    sampled cameras checked against the oracle's score functions on the same
-    renders, and densify_and_prune_fastgs against the densification oracle on
-    the same draws -- every parameter row, Adam moment and statistic bit-exact."""
+def _snapshot(ts):
+    from fastgs_core_amd.densify import PARAM_NAMES, STAT_NAMES
+
+    model = {n: to_np(ts.param(n)).copy() for n in PARAM_NAMES}
+    adam = {n: tuple(to_np(x).reshape(model[n].shape).copy() for x in ts.moments(n))
+            for n in PARAM_NAMES}
+    st = {n: to_np(ts.stat(n)).copy() for n in STAT_NAMES}
+    st["tmp_radii"] = to_np(ts.tmp_radii()).copy()
+    return model, adam, st
+
+
+def _check_event(ts, loop, dor, dcfg, it, targets, HW, draws):
+    """One densification event of the loop against the oracles: the scores
+    over the sampled cameras from the GPU renders, then densify_and_prune_fastgs
+    on the same draws -- every row, Adam moment and statistic bit-exact."""
+    import torch
+
+    from fastgs_core_amd.densify import PARAM_NAMES, STAT_NAMES
+
+    renders = []
+    ids = loop.sample_cameras()
+    imp, prn = loop.scores(it, ids, True, on_render=renders.append)
+    counts = np.zeros(ts.P, np.float32)
+    score = np.zeros(ts.P, np.float32)
+    for c, i in enumerate(ids):
+        pred = to_np(renders[2 * c]["out_color"]).reshape(3, HW)
+        _, ploss = dor.metric_map(pred, to_np(targets[i]), dcfg.loss_thresh)
+        counts, score = dor.score_accumulate(counts, score,
+                                             to_np(renders[2 * c + 1]["metric_count"]), ploss)
+    want_imp, want_prn = dor.score_finalize(counts, score, len(ids))
+    imp_np, prn_np = to_np(imp), to_np(prn)
+    np.testing.assert_array_equal(imp_np, want_imp)
+    np.testing.assert_allclose(prn_np, want_prn, rtol=1e-5, atol=1e-6)
+    model, adam, st = _snapshot(ts)
+    cf, sf = dor.classify(dcfg, loop.extent, st, model["log_scales"], imp_np)
+    nc, ns = int(cf.sum()), int(sf.sum())
+    normals = draws.normal(0, 1, (ns * dcfg.split_factor, 3)).astype(np.float32)
+    uniforms = draws.random(ts.P - ns + nc + ns * dcfg.split_factor).astype(np.float32)
+    nm, na, nst, info = dor.densify_and_prune(dcfg, loop.extent, model, adam, st, imp_np, prn_np,
+                                              normals, uniforms)
+    got = ts.densify_and_prune_fastgs(dcfg, loop.extent, imp, torch.from_numpy(prn_np).cuda(),
+                                      normals=torch.from_numpy(normals).cuda(),
+                                      uniforms=torch.from_numpy(uniforms).cuda())
+    _say(f"cfg5 event it={it}:", {k: got[k] for k in ("cloned", "split_sources",
+                                                      "total_prune_candidates", "actual_removed",
+                                                      "points")})
+    for k in ("cloned", "split_sources", "split_children", "total_prune_candidates",
+              "prune_budget", "actual_removed", "points"):
+        assert got[k] == info[k], (it, k, got[k], info[k])
+    for n in PARAM_NAMES:
+        g = to_np(ts.param(n))
+        np.testing.assert_array_equal(g.view(np.uint32),
+                                      np.asarray(nm[n], np.float32).reshape(g.shape).view(np.uint32),
+                                      err_msg=f"it {it} {n}")
+        m, v = ts.moments(n)
+        np.testing.assert_array_equal(to_np(m).reshape(g.shape), na[n][0].reshape(g.shape))
+        np.testing.assert_array_equal(to_np(v).reshape(g.shape), na[n][1].reshape(g.shape))
+    for n in STAT_NAMES:
+        np.testing.assert_array_equal(to_np(ts.stat(n)), nst[n], err_msg=f"it {it} {n}")
+    np.testing.assert_array_equal(to_np(ts.tmp_radii()), nst["tmp_radii"])
+    return got
+
+
+@pytest.mark.timeout(900)
+def test_cfg5_full_schedule_at_size(oracle):
+    """configs[4] through its whole schedule: the reference's initial model of
+    100,000 points at 1280x720, 500 iterations of the FastGS loop
+    (train_scanner_fastgs.py:968-1060: one sphere camera per iteration, MSE
+    against targets of a hidden 300k scene, the Adam cadence, the statistics
+    from the viewspace gradients and the post-step statistics render of
+    :1014-1019), a densification event every 100 iterations -- all five
+    checked against the densification oracle on the same draws, scores
+    included -- then, after 50 more iterations, one more event at the same
+    size with thresholds that split and prune (densify_and_split_fastgs :567-587 and the budgeted prune
+    draw :700-723 at size).  On three iterations the statistics render is
+    checked against the oracle: its radii are the oracle's preprocess radii
+    of the post-step parameters, and the statistics update is the oracle's."""
+    import dataclasses
+
     import torch
 
     import fastgs_core
-    import fastgs_core_amd
-    from fastgs_core_amd.densify import (PARAM_NAMES, STAT_NAMES, DensifyConfig,
-                                         GaussianTrainState, compute_scene_extent)
+    from fastgs_core_amd.densify import (DensifyConfig, FastGSTrainLoop, GaussianTrainState,
+                                         LoopConfig, STAT_NAMES, compute_scene_extent)
     from oracle.densify import DensifyOracle
 
     dev = torch.device("cuda")
@@ -213,78 +283,54 @@ def test_cfg5_densify_event_at_size():
                    for i in range(len(cams))]
     del hidden
     ts = _cfg5_state(torch, dev, 100_000)
-    extent = compute_scene_extent(ts.param("means3d").detach())
-    rng = np.random.default_rng(42)
-    stack = []
-    _say("cfg5 100 iterations")
-    for it in range(1, 101):
-        ts.update_learning_rate(it)
-        if not stack:
-            stack = list(range(len(cams)))
-        idx = stack.pop(int(rng.integers(0, len(stack))))
-        vsp = torch.zeros((ts.P, 4), device=dev, requires_grad=True)
-        out = render(ts, idx, 0, vsp=vsp)
-        loss = fastgs_core_amd.mse_loss(out["out_color"].reshape(3, HW), targets[idx])
-        ts.zero_grad()
-        loss.backward()
-        ts.update_densification_stats(out["radii"], vsp.grad)
-        ts.step(it)
-    assert np.isfinite(float(loss.detach()))
-    dor = DensifyOracle()
     dcfg = DensifyConfig()
-    ids = [int(i) for i in rng.choice(len(cams), size=dcfg.densify_camera_sample, replace=False)]
-    renders = []
-
-    def scoring_render(i, mm):
-        o = render(ts, i, 0, metric_map=mm)
-        renders.append(o)
-        return o
-
-    _say("cfg5 scores over", len(ids), "cameras")
-    with torch.no_grad():
-        imp, prn = ts.compute_gaussian_scores_fastgs(scoring_render, targets, ids,
-                                                     dcfg.loss_thresh, True)
-    counts = np.zeros(ts.P, np.float32)
-    score = np.zeros(ts.P, np.float32)
-    for c, i in enumerate(ids):
-        pred = to_np(renders[2 * c]["out_color"]).reshape(3, HW)
-        _, ploss = dor.metric_map(pred, to_np(targets[i]), dcfg.loss_thresh)
-        counts, score = dor.score_accumulate(counts, score, to_np(renders[2 * c + 1]["metric_count"]),
-                                             ploss)
-    want_imp, want_prn = dor.score_finalize(counts, score, len(ids))
-    imp_np, prn_np = to_np(imp), to_np(prn)
-    np.testing.assert_array_equal(imp_np, want_imp)
-    np.testing.assert_allclose(prn_np, want_prn, rtol=1e-5, atol=1e-6)
-
-    model = {n: to_np(ts.param(n)).copy() for n in PARAM_NAMES}
-    adam = {n: tuple(to_np(x).reshape(model[n].shape).copy() for x in ts.moments(n))
-            for n in PARAM_NAMES}
-    st = {n: to_np(ts.stat(n)).copy() for n in STAT_NAMES}
-    st["tmp_radii"] = to_np(ts.tmp_radii()).copy()
-    cf, sf = dor.classify(dcfg, extent, st, model["log_scales"], imp_np)
-    nc, ns = int(cf.sum()), int(sf.sum())
+    lcfg = LoopConfig(interval=100, densify_from=0, stats_render="post_step")
+    loop = FastGSTrainLoop(ts, render, targets, len(cams), 3, dcfg, lcfg,
+                           compute_scene_extent(ts.param("means3d").detach()), seed=42)
+    dor = DensifyOracle()
     draws = np.random.default_rng(7)
-    normals = draws.normal(0, 1, (ns * dcfg.split_factor, 3)).astype(np.float32)
-    P2 = ts.P - ns + nc + ns * dcfg.split_factor
-    uniforms = draws.random(P2).astype(np.float32)
-    _say(f"cfg5 densify event: P={ts.P} clones={nc} splits={ns}")
-    nm, na, nst, info = dor.densify_and_prune(dcfg, extent, model, adam, st, imp_np, prn_np,
-                                              normals, uniforms)
-    got = ts.densify_and_prune_fastgs(dcfg, extent, imp, torch.from_numpy(prn_np).cuda(),
-                                      normals=torch.from_numpy(normals).cuda(),
-                                      uniforms=torch.from_numpy(uniforms).cuda())
-    for k in ("cloned", "split_sources", "split_children", "total_prune_candidates",
-              "prune_budget", "actual_removed", "points"):
-        assert got[k] == info[k], (k, got[k], info[k])
-    assert info["cloned"] + info["split_sources"] > 0
-    for n in PARAM_NAMES:
-        g = to_np(ts.param(n))
-        np.testing.assert_array_equal(g.view(np.uint32),
-                                      np.asarray(nm[n], np.float32).reshape(g.shape).view(np.uint32),
-                                      err_msg=n)
-        m, v = ts.moments(n)
-        np.testing.assert_array_equal(to_np(m).reshape(g.shape), na[n][0].reshape(g.shape))
-        np.testing.assert_array_equal(to_np(v).reshape(g.shape), na[n][1].reshape(g.shape))
-    for n in STAT_NAMES:
-        np.testing.assert_array_equal(to_np(ts.stat(n)), nst[n], err_msg=n)
-    np.testing.assert_array_equal(to_np(ts.tmp_radii()), nst["tmp_radii"])
+    events = []
+    radii_moved = 0
+    for it in range(1, 501):
+        check = it in (1, 137, 333)
+        if check:
+            _, _, st0 = _snapshot(ts)
+        loss, idx = loop.train_iteration(it)
+        if check:
+            radii, dvsp = loop.last_stats
+            d = ts.render_inputs(cam_in[idx])
+            c = cams[idx]
+            kw = dict(dc=to_np(d["dc"]), sh=to_np(d["sh"]), scales=to_np(d["scales"]),
+                      rotations=to_np(d["rotations"]))
+            pre = oracle.preprocess_fwd(to_np(d["means3d"]), to_np(d["opacities"]),
+                                        c.viewmatrix.reshape(-1), c.projmatrix.reshape(-1),
+                                        c.campos, np.zeros((ts.P, 4), np.float32), W, H,
+                                        c.tan_fovx, c.tan_fovy, 0, **kw)
+            np.testing.assert_array_equal(to_np(radii), pre["radii"], err_msg=f"it {it} radii")
+            want = dor.update_stats(dict(st0), to_np(radii), to_np(dvsp))
+            for n in STAT_NAMES:
+                np.testing.assert_array_equal(to_np(ts.stat(n)), want[n], err_msg=f"it {it} {n}")
+            _say(f"cfg5 it={it}: statistics render checked, loss {float(loss):.5f}")
+        if loop.is_densify_event(it):
+            events.append(_check_event(ts, loop, dor, dcfg, it, targets, HW, draws))
+        loop.after_iteration(it)
+    assert np.isfinite(float(loss))
+    assert len(events) == 5
+    assert sum(e["cloned"] + e["split_sources"] for e in events) > 0
+    # 50 more iterations refill the statistics (the event of iteration 500
+    # reset them), then one more event at this size with thresholds that
+    # split and prune: rows above 0.05 % of the extent split when their mean
+    # |viewspace gradient| passes 2e-4; the prune thresholds come from the
+    # state itself (training moves every opacity above the initial 0.1): the
+    # 5 % quantile of the opacities and 1.5x the median largest world scale
+    for it in range(501, 551):
+        loop.train_iteration(it)
+    model, _, _ = _snapshot(ts)
+    opac = 1.0 / (1.0 + np.exp(-model["opacity_logits"].astype(np.float64).reshape(-1)))
+    big = np.exp(model["log_scales"].astype(np.float64)).max(1)
+    forced = dataclasses.replace(dcfg, dense=0.0005, grad_abs_thresh=2.0e-4,
+                                 min_opacity=float(np.quantile(opac, 0.05)),
+                                 max_world_scale_factor=float(1.5 * np.median(big) / loop.extent))
+    got = _check_event(ts, loop, dor, forced, 550, targets, HW, draws)
+    assert got["split_sources"] > 0 and got["total_prune_candidates"] > 0
+    assert got["actual_removed"] > 0
