@@ -7,7 +7,9 @@ hand-written HIP kernels in ``libfastgs_hip.so``.
 """
 from .densify import (  # noqa: F401
     DensifyConfig,
+    FastGSTrainLoop,
     GaussianTrainState,
+    LoopConfig,
     OptimConfig,
     compute_scene_extent,
 )
