@@ -302,6 +302,10 @@ __device__ __forceinline__ void wave_reduce_terms(float (&v)[kGradTerms], float*
     w[m] += dpp_mov<0x4E>(w[m]);
     w[m] += dpp_mov<0x114>(w[m]);
     w[m] += dpp_mov<0x118>(w[m]);
+    // the sums are formed here, by every lane: sunk into the lane-15 branch
+    // below, the last add could not take its DPP operand directly (a zeroed
+    // register, a DPP move and a plain add instead of one DPP add)
+    asm volatile("" : "+v"(w[m]));
   }
   if ((l & 15) == 15) {
     const int r = l >> 4;
