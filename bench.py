@@ -155,9 +155,10 @@ def run_densify_loop(args):
     loss up to --mse-until 600; fused kernels), backward, the learning-rate
     schedule and the FastGS Adam cadence, then the densification statistics
     from the viewspace gradient and the radii of --stats-render (default: the
-    reference's second render after the optimizer step).  Every ``interval``
-    iterations: the metric-map scores over 10 sampled cameras (two renders
-    each) and densify_and_prune_fastgs.  The timed region is the whole loop,
+    reference's post-step radii of the same camera, train_scanner_fastgs.py:
+    1014-1019, here from the preprocess alone, which yields the radii of its
+    full render).  Every ``interval`` iterations: the metric-map scores over
+    10 sampled cameras (two renders each) and densify_and_prune_fastgs.  The timed region is the whole loop,
     densification included; targets are rendered beforehand."""
     import torch
 
@@ -199,6 +200,10 @@ def run_densify_loop(args):
         return fastgs_core.rasterize_gaussians(d, W, H, 16, 16, cm.tan_fovx, cm.tan_fovy, degree,
                                                get_flag=metric_map is not None)
 
+    def radii(ts, idx):  # the post-step statistics' radii: the preprocess alone
+        cm = cams[idx]
+        return ts.preprocess_radii(cam_in[idx], W, H, cm.tan_fovx, cm.tan_fovy)
+
     # targets: the hidden scene rendered at full SH degree (untimed)
     hidden = GaussianTrainState(to_params(syn.scene_config2(c["hidden_seed"], c["P_hidden"], deg)))
     with torch.no_grad():
@@ -217,7 +222,7 @@ def run_densify_loop(args):
         tl = FastGSTrainLoop(ts, render, targets, len(cams), deg, dcfg,
                              dataclasses.replace(lcfg, interval=interval),
                              compute_scene_extent(ts.param("means3d").detach()), seed=42,
-                             generator=gen)
+                             generator=gen, radii=radii)
         losses = torch.zeros(max(n_iter, 1), device=dev)
         events = []
         for it in range(1, n_iter + 1):

@@ -490,6 +490,21 @@ class GaussianTrainState:
         return importance, pruning
 
     # ----------------------------------------------------------------- render
+    @torch.no_grad()
+    def preprocess_radii(self, camera_inputs: Dict[str, torch.Tensor], width: int, height: int,
+                         tan_fovx: float, tan_fovy: float) -> torch.Tensor:
+        """The current rows' radii for one camera from the preprocess alone
+        (``preprocess_forward``, binding.cpp:397-508): the radii a full render
+        of the same camera returns, without its binning and blend."""
+        from .rasterizer import preprocess_forward
+
+        d = self.render_inputs(camera_inputs)
+        pf = {"means3d": d["means3d"], "opacities": d["opacities"],
+              "viewmat": d["viewmatrix"], "projmat": d["projmatrix"], "cam_pos": d["campos"],
+              "viewspace_points": torch.zeros((self.P, 4), dtype=torch.float32, device=self.dev),
+              "scales": d["scales"], "quats": d["rotations"], "dc": d["dc"], "sh": d["sh"]}
+        return preprocess_forward(pf, width, height, 16, 16, tan_fovx, tan_fovy, 0)["radii"]
+
     def render_inputs(self, camera_inputs: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
         """The ``rasterize_gaussians`` input dict of the current rows (the
         activations of :523-536 through ``fastgs_core_amd.activate``)."""
@@ -532,7 +547,10 @@ class FastGSTrainLoop:
 
     ``render(ts, idx, degree, metric_map=None, vsp=None)`` renders camera
     ``idx`` with the state's current rows and returns the
-    ``rasterize_gaussians`` dict; ``targets[idx]`` is ``[3, H*W]``.  Cameras
+    ``rasterize_gaussians`` dict; ``targets[idx]`` is ``[3, H*W]``.
+    ``radii(ts, idx)`` (optional) returns camera ``idx``'s radii for the
+    post-step statistics (``GaussianTrainState.preprocess_radii`` gives them
+    from the preprocess alone); without it a full render is made.  Cameras
     are popped from a seeded viewpoint stack (:974-978); the loss is MSE up to
     ``mse_until`` and L1 after (:960-963); Adam follows the FastGS cadence.
     The statistics accumulate while ``it < densify_until``; a densification
@@ -544,7 +562,8 @@ class FastGSTrainLoop:
     def __init__(self, ts: GaussianTrainState, render: Callable, targets: Sequence[torch.Tensor],
                  n_cameras: int, degree: int, dcfg: DensifyConfig, lcfg: LoopConfig,
                  scene_extent: float, seed: int = 42,
-                 generator: Optional[torch.Generator] = None):
+                 generator: Optional[torch.Generator] = None,
+                 radii: Optional[Callable] = None):
         import numpy as np
 
         from .loss import l1_loss, mse_loss
@@ -552,6 +571,7 @@ class FastGSTrainLoop:
         if lcfg.stats_render not in ("post_step", "train"):
             raise ValueError("stats_render must be 'post_step' or 'train'")
         self.ts, self.render, self.targets = ts, render, targets
+        self.radii = radii
         self.n_cameras, self.degree = int(n_cameras), int(degree)
         self.dcfg, self.lcfg, self.extent = dcfg, lcfg, float(scene_extent)
         self.rng = np.random.default_rng(seed)
@@ -585,7 +605,8 @@ class FastGSTrainLoop:
         if it < lc.densify_until:
             if lc.stats_render == "post_step":
                 with torch.no_grad():
-                    radii = self.render(ts, idx, active)["radii"]
+                    radii = (self.radii(ts, idx) if self.radii is not None
+                             else self.render(ts, idx, active)["radii"])
             else:
                 radii = out["radii"]
             ts.update_densification_stats(radii, vsp.grad)

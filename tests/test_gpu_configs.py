@@ -285,8 +285,13 @@ def test_cfg5_full_schedule_at_size(oracle):
     ts = _cfg5_state(torch, dev, 100_000)
     dcfg = DensifyConfig()
     lcfg = LoopConfig(interval=100, densify_from=0, stats_render="post_step")
+    def radii(ts, idx):
+        c = cams[idx]
+        return ts.preprocess_radii(cam_in[idx], W, H, c.tan_fovx, c.tan_fovy)
+
     loop = FastGSTrainLoop(ts, render, targets, len(cams), 3, dcfg, lcfg,
-                           compute_scene_extent(ts.param("means3d").detach()), seed=42)
+                           compute_scene_extent(ts.param("means3d").detach()), seed=42,
+                           radii=radii)
     dor = DensifyOracle()
     draws = np.random.default_rng(7)
     events = []
@@ -307,6 +312,10 @@ def test_cfg5_full_schedule_at_size(oracle):
                                         c.campos, np.zeros((ts.P, 4), np.float32), W, H,
                                         c.tan_fovx, c.tan_fovy, 0, **kw)
             np.testing.assert_array_equal(to_np(radii), pre["radii"], err_msg=f"it {it} radii")
+            # the preprocess-only radii are those of a full render of the camera
+            with torch.no_grad():
+                full = render(ts, idx, loop.active_degree(it))["radii"]
+            np.testing.assert_array_equal(to_np(radii), to_np(full), err_msg=f"it {it} full")
             want = dor.update_stats(dict(st0), to_np(radii), to_np(dvsp))
             for n in STAT_NAMES:
                 np.testing.assert_array_equal(to_np(ts.stat(n)), want[n], err_msg=f"it {it} {n}")
