@@ -40,7 +40,11 @@ constexpr int kWavesPerBlock = kThreads / kWave;
 // back over its predecessors adding aggregates until it meets an inclusive
 // prefix.  Status words and tickets start at zero (one fill kernel per call).
 // Radix passes keep their status words chunk-major ([chunk][digit]): a
-// chunk's 256 counters are published and read as one contiguous block.
+// chunk's 256 counters are published and read as one contiguous block.  They
+// look back in two levels: a chunk sums its predecessors inside its group of
+// kLbGroup chunks directly and looks back over group totals, which the last
+// chunk of each group publishes (a walk over every earlier chunk had made the
+// last chunks of a 1M-key pass wait about 13 us longer than the first).
 // The spin is bounded as a backstop; it cannot run out while chunks are
 // taken in ticket order.
 // ---------------------------------------------------------------------------
@@ -161,6 +165,52 @@ __device__ __forceinline__ uint32_t block_sum_predecessors(const uint64_t* statu
   return total;
 }
 
+// Sum of the published counts of chunks first .. first + q - 1 (one status
+// word each, `stride` apart): all of them are loaded at once, and the ones
+// not yet published are polled again.  Bounded like look_back.
+constexpr int kLbGroup = 16;  // chunks per look-back group
+__device__ __forceinline__ uint32_t sum_group_preds(const uint64_t* status, int64_t first, int q,
+                                                    int64_t stride, uint32_t* err,
+                                                    uint32_t spin_limit) {
+  if (spin_limit == 0u) {  // the forced error path: give up at once, as look_back
+    if (q > 0) wait_gave_up(err, kWaitLookBack);
+    return 0u;
+  }
+  uint32_t sum = 0;
+  uint32_t pending = (1u << q) - 1u;  // q < kLbGroup
+  uint32_t spins = 0;
+  while (pending) {
+    uint64_t w[kLbGroup];
+#pragma unroll
+    for (int i = 0; i < kLbGroup; ++i)
+      w[i] = ((pending >> i) & 1u) ? __hip_atomic_load(status + (first + i) * stride,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0ull;
+#pragma unroll
+    for (int i = 0; i < kLbGroup; ++i) {
+      if (((pending >> i) & 1u) && (uint32_t)(w[i] >> 32) != 0u) {
+        sum += (uint32_t)w[i];
+        pending &= ~(1u << i);
+      }
+    }
+    if (pending) {
+      if (++spins > spin_limit) {
+        wait_gave_up(err, kWaitLookBack);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  return sum;
+}
+
+// take_ticket with a barrier that orders LDS only: the workgroup's other
+// loads (issued before it) stay in flight.
+__device__ __forceinline__ int64_t take_ticket_lds(uint32_t* ticket, uint32_t* s_slot) {
+  if (threadIdx.x == 0) *s_slot = atomicAdd(ticket, 1u);
+  lds_barrier();
+  return (int64_t)*s_slot;
+}
 __device__ __forceinline__ int64_t take_ticket(uint32_t* ticket, uint32_t* s_slot) {
   if (threadIdx.x == 0) *s_slot = atomicAdd(ticket, 1u);
   __syncthreads();
@@ -431,14 +481,15 @@ __global__ void __launch_bounds__(kT)
 radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                   K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n_max,
                   int shift, int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
-                  int64_t nchunks, uint32_t* ticket, uint32_t* err, uint32_t spin_limit,
-                  SortPassOpts opt) {
+                  uint64_t* gstatus, int64_t nchunks, uint32_t* ticket, uint32_t* err,
+                  uint32_t spin_limit, SortPassOpts opt) {
   constexpr int kW = kT / kWave;
   constexpr int kC = kT * kIt;
   __shared__ uint32_t s_wh[kW][256];
   __shared__ uint32_t s_dstart[256];
   __shared__ uint32_t s_goff[256];
   __shared__ uint32_t s_tmp[kW + 1];
+  __shared__ uint32_t s_tmp2[kW + 1];
   __shared__ uint32_t s_slot;
   __shared__ uint32_t s_total;
   __shared__ K s_keys[kC];
@@ -457,7 +508,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     const int64_t nd = (int64_t)*opt.n_dev;
     n = nd < n_max ? nd : n_max;
   }
-  const int64_t chunk = take_ticket(ticket, &s_slot);  // includes a barrier
+  const int64_t chunk = take_ticket_lds(ticket, &s_slot);  // includes a barrier
   if (opt.fill_tail) {
     // positions [n, n_max) get the sentinel pair (all-ones key, value)
     for (int64_t j = n + chunk * kC + t; j < n + (chunk + 1) * kC && j < n_max; j += kT) {
@@ -510,7 +561,10 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     if (valid && r == 0) s_wh[w][d] = old + (uint32_t)__popcll(peers);
     rank[it] = old + r;
   }
-  __syncthreads();
+  // The pass's barriers order LDS only: its global stores (the sentinel tail,
+  // the status words) stay in flight instead of being waited out at each
+  // barrier, which the full __syncthreads() would do.
+  lds_barrier();
   {
     const bool dig = (uint32_t)t <= mask;  // t < 256 as nbits <= 8
     uint32_t c[kW];
@@ -520,9 +574,33 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
       c[k] = dig ? s_wh[k][t] : 0u;
       tot += c[k];
     }
-    const uint32_t gbase = block_excl_scan(gcount, s_tmp, nullptr);
-    uint32_t total;
-    const uint32_t ds = block_excl_scan(tot, s_tmp, &total);
+    uint64_t* st = status + (size_t)t;  // chunk-major: [chunk][digit]
+    // the chunk's digit counts are published before the scans, so that the
+    // look-backs of later chunks can pass this one sooner
+    if (dig) status_store(st + chunk * 256, kFlagAggregate, tot);
+    // both exclusive scans (global digit bases, chunk digit starts) at once
+    uint32_t gbase, ds, total;
+    {
+      const uint32_t ia = wave_incl_scan(gcount), ib = wave_incl_scan(tot);
+      if (lane == kWave - 1) {
+        s_tmp[w] = ia;
+        s_tmp2[w] = ib;
+      }
+      lds_barrier();
+      if (w == 0) {
+        const uint32_t xa = lane < kW ? s_tmp[lane] : 0u, xb = lane < kW ? s_tmp2[lane] : 0u;
+        const uint32_t ya = wave_incl_scan(xa), yb = wave_incl_scan(xb);
+        if (lane < kW) {
+          s_tmp[lane] = ya - xa;
+          s_tmp2[lane] = yb - xb;
+        }
+        if (lane == kW - 1) s_tmp2[kW] = yb;
+      }
+      lds_barrier();
+      gbase = s_tmp[w] + ia - gcount;
+      ds = s_tmp2[w] + ib - tot;
+      total = s_tmp2[kW];
+    }
     if (t == 0) s_total = total;
     if (t < 256) {
       uint32_t run = ds;
@@ -534,19 +612,26 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
       s_dstart[t] = ds;
     }
     if (dig) {
-      uint32_t excl = 0;
-      uint64_t* st = status + (size_t)t;  // chunk-major: [chunk][digit]
-      if (chunk == 0) {
-        status_store(st, kFlagPrefix, tot);
-      } else {
-        status_store(st + chunk * 256, kFlagAggregate, tot);
-        excl = look_back(st, chunk, 256, err, spin_limit);
-        status_store(st + chunk * 256, kFlagPrefix, excl + tot);
-      }
+      // Two-level offsets: the chunk's predecessors in its group of
+      // kLbGroup chunks are summed directly; the group's offset comes from a
+      // look-back over group totals, which the last chunk of each group
+      // publishes.  A chunk thus waits a few memory round trips, not a chain
+      // of windows over every earlier chunk.
+      const int64_t g = chunk / kLbGroup;
+      const int q = (int)(chunk - g * kLbGroup);
+      const uint32_t in_group =
+          q ? sum_group_preds(st, g * kLbGroup, q, 256, err, spin_limit) : 0u;
+      uint64_t* gst = gstatus + (size_t)t;
+      const bool last_in_group = q == kLbGroup - 1;
+      if (last_in_group)
+        status_store(gst + g * 256, g == 0 ? kFlagPrefix : kFlagAggregate, in_group + tot);
+      const uint32_t gexcl = g ? look_back(gst, g, 256, err, spin_limit) : 0u;
+      if (last_in_group && g > 0) status_store(gst + g * 256, kFlagPrefix, gexcl + in_group + tot);
+      const uint32_t excl = gexcl + in_group;
       s_goff[t] = gbase + excl;
     }
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
     if (vld[it]) {
@@ -556,7 +641,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
       s_vals[pos] = val[it];
     }
   }
-  __syncthreads();
+  lds_barrier();
   const int cnt = (int)s_total;  // the chunk's keys in play (all of them unless dropped)
   for (int j = t; j < cnt; j += kT) {
     const K k = s_keys[j];
@@ -586,10 +671,12 @@ static int64_t sort_chunks(int64_t n) {
 }
 
 // Zero-initialised state of one sort: histograms (8 x 256), tickets (8),
-// error word, then the status words of every pass.
+// error word, then the status words of every pass (per chunk), then those of
+// the look-back groups of every pass.
 static size_t sort_state_bytes(int64_t n, int passes) {
   const int64_t nc = sort_chunks(n);
-  return (size_t)((8 * 256 * 4 + 64 + (int64_t)passes * (nc < 1 ? 1 : nc) * 256 * 8 + 255) &
+  const int64_t ng = (nc + kLbGroup - 1) / kLbGroup;
+  return (size_t)((8 * 256 * 4 + 64 + (int64_t)passes * ((nc < 1 ? 1 : nc) + ng) * 256 * 8 + 255) &
                   ~(int64_t)255);
 }
 
@@ -650,6 +737,8 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   uint32_t* tickets = hist + 8 * 256;
   uint32_t* err = werr ? werr : tickets + 8;
   uint64_t* status = (uint64_t*)(p + 8 * 256 * 4 + 64);
+  const int64_t ngr = (nc + kLbGroup - 1) / kLbGroup;
+  uint64_t* gstat = status + (size_t)pl.passes * nc * 256;
   {
     FillSpans f{};
     f.value = 0u;
@@ -689,12 +778,14 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
     if (items == 8)
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit,
+                         status + (size_t)pass * nc * 256, gstat + (size_t)pass * ngr * 256, nc,
+                         tickets + pass, err, spin_limit,
                          opt);
     else
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 4>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, nc, tickets + pass, err, spin_limit,
+                         status + (size_t)pass * nc * 256, gstat + (size_t)pass * ngr * 256, nc,
+                         tickets + pass, err, spin_limit,
                          opt);
     const int32_t e2 = check_launch("radix_pass");
     if (e2 != FGS_OK) return e2;
