@@ -1641,48 +1641,62 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
   }
   const uint32_t q0 = e0 + (uint32_t)w * (kL2Chunk / kWavesPerBlock);
   const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
+  // the wavefront's entries, two rounds of 64, all loaded at once (the depth
+  // gathers follow the indices and stay in flight across the barrier)
+  constexpr int kRounds = kL2Chunk / kWavesPerBlock / kWave;
+  static_assert(kRounds == 2, "two rounds of 64 entries per wavefront");
+  uint64_t m[kRounds], bt[kRounds];
+  uint32_t g[kRounds], db[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const uint32_t e = q0 + (uint32_t)(r * kWave + l);
+    const bool in = e < q1;
+    m[r] = in ? masks[e] : 0ull;
+    g[r] = in ? list[e] : 0u;
+    if (kCarry) db[r] = in ? ldb[e] : 0u;
+  }
+  if (!kCarry) {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const uint32_t e = q0 + (uint32_t)(r * kWave + l);
+      db[r] = (e < q1 && g[r] < (uint32_t)P) ? __float_as_uint(depths[g[r]]) : 0xFFFFFFFFu;
+    }
+  }
   // this wavefront's entries per tile (lane j)
   {
     uint32_t cnt = 0;
-    for (uint32_t base = q0; base < q1; base += kWave) {
-      const uint32_t e = base + (uint32_t)l;
-      cnt += (uint32_t)__popcll(transpose64(e < q1 ? masks[e] : 0ull));
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      bt[r] = transpose64(m[r]);
+      cnt += (uint32_t)__popcll(bt[r]);
     }
     s_wc[w][l] = cnt;
   }
   const uint32_t soff = ci - cj;
-  __syncthreads();
+  lds_barrier();
   uint32_t cur = soff;
   for (int k = 0; k < w; ++k) cur += s_wc[k][l];
-  for (uint32_t base = q0; base < q1; base += kWave) {
-    const uint32_t e = base + (uint32_t)l;
-    uint64_t m = 0ull;
-    uint32_t g = 0, db = 0;
-    if (e < q1) {
-      m = masks[e];
-      g = list[e];
-      db = kCarry ? ldb[e] : (g < (uint32_t)P ? __float_as_uint(depths[g]) : 0xFFFFFFFFu);
-    }
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
     // lane j: the round's entries having tile j (bit i = entry i).  Lane j
     // walks them in entry (depth) order and fetches each entry's index and
     // depth bits from its lane; the loop runs as often as the busiest tile
     // of the round has entries.
-    const uint64_t bt = transpose64(m);
-    uint64_t b = bt;
+    uint64_t b = bt[r];
     uint32_t at = cur;
     while (__ballot(b != 0ull) != 0ull) {
       const bool act = b != 0ull;
       const int src = act ? ((int)__builtin_ctzll(b) << 2) : 0;
       b &= b - 1ull;
-      const uint32_t gi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)g);
-      const uint32_t dbi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)db);
+      const uint32_t gi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)g[r]);
+      const uint32_t dbi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)db[r]);
       if (act && at < (uint32_t)kL2Stage) {
         s_g[at] = gi;
         s_db[at] = dbi;
       }
       if (act) ++at;
     }
-    cur += (uint32_t)__popcll(bt);  // lane j: tile j's entries in this round
+    cur += (uint32_t)__popcll(bt[r]);  // lane j: tile j's entries in this round
   }
   __syncthreads();
   for (int j = w; j < kWave; j += kWavesPerBlock) {
