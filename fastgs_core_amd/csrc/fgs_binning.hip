@@ -439,11 +439,16 @@ radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* 
           if ((uint32_t)k == 0xFFFFFFFFu) continue;
           ++vis;
         }
-        int shift = pl.begin;
-        for (int p = 0; p < pl.passes; ++p) {
-          const uint32_t d = (uint32_t)(k >> shift) & ((1u << pl.bits[p]) - 1u);
-          atomicAdd(&s_h[p][d], 1u);
-          shift += pl.bits[p];
+        if (kDepthKeys) {  // the depth sort's plan: four 8-bit digits from bit 0
+#pragma unroll
+          for (int p = 0; p < 4; ++p) atomicAdd(&s_h[p][(uint32_t)(k >> (8 * p)) & 0xFFu], 1u);
+        } else {
+          int shift = pl.begin;
+          for (int p = 0; p < pl.passes; ++p) {
+            const uint32_t d = (uint32_t)(k >> shift) & ((1u << pl.bits[p]) - 1u);
+            atomicAdd(&s_h[p][d], 1u);
+            shift += pl.bits[p];
+          }
         }
       }
     }
@@ -452,7 +457,8 @@ radix_hist_kernel(const K* __restrict__ keys, int64_t n, SortPlan pl, uint32_t* 
     vis = wave_sum_u32(vis);
     if (lane_id() == 0 && vis) atomicAdd(&s_vis, vis);
   }
-  __syncthreads();
+  // orders LDS only: the key stores stay in flight
+  lds_barrier();
   for (int p = 0; p < pl.passes; ++p) {
     const uint32_t c = s_h[p][threadIdx.x];
     if (c) atomicAdd(&hist[p * 256 + threadIdx.x], c);
@@ -715,9 +721,10 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   const SortPlan pl = sort_plan(begin, end);
   // depth keys drop the culled Gaussians in pass 0 (which runs on all n) and
   // fill the sentinel tail in the last pass over the visible count, so they
-  // need two distinct passes
-  if (kDepthKeys && pl.passes < 2)
-    return set_error(FGS_ERR_UNSUPPORTED, "radix_sort_pairs: depth keys need >= 2 passes");
+  // need two distinct passes; their histogram kernel counts the four 8-bit
+  // digits of a 32-bit key
+  if (kDepthKeys && (begin != 0 || end != 32 || pl.passes != 4))
+    return set_error(FGS_ERR_UNSUPPORTED, "radix_sort_pairs: depth keys take 32 bits from bit 0");
   if (pl.passes == 0) {
     int64_t blocks = (n + 255) / 256;
     if (blocks > 65536) blocks = 65536;
