@@ -1017,6 +1017,7 @@ constexpr int kMaxSt = 256;     // super-tiles of the two-level path
 constexpr int kL1Group = 256;   // level-1 Gaussians per workgroup
 constexpr int kL1Segs = 64;     // level-1 row segments of the count scan
 constexpr int kL2Chunk = 512;   // level-2 entries per workgroup (4 wavefronts x 128)
+constexpr int kL2EmitGrid = 4096;  // workgroups of l2_count and l2_emit at most (chunk loops)
 constexpr int kWideGroups = 512;  // grid of l1_wide_masks_kernel
 constexpr int kScanBatch = 32;    // loads in flight per serial-scan batch
 
@@ -1417,46 +1418,51 @@ __device__ __forceinline__ uint64_t transpose64(uint64_t row) {
     if (up) lo = recv;
     else hi = recv;
   }
-#pragma unroll
-  for (int d = 16; d >= 1; d >>= 1) {
-    const uint32_t m = d == 16 ? 0x0000FFFFu
-                     : d == 8  ? 0x00FF00FFu
-                     : d == 4  ? 0x0F0F0F0Fu
-                     : d == 2  ? 0x33333333u
-                               : 0x55555555u;
+  // the five steps written out (inside a loop over chunks the unroll pragma
+  // was not applied)
+  auto step = [&](const int d, const uint32_t m) {
     const bool up = (l & d) != 0;
     const uint32_t rl = (uint32_t)__shfl_xor((int)(up ? (lo & m) : (lo & ~m)), d);
     const uint32_t rh = (uint32_t)__shfl_xor((int)(up ? (hi & m) : (hi & ~m)), d);
     lo = up ? ((lo & ~m) | (rl >> d)) : ((lo & m) | (rl << d));
     hi = up ? ((hi & ~m) | (rh >> d)) : ((hi & m) | (rh << d));
-  }
+  };
+  step(16, 0x0000FFFFu);
+  step(8, 0x00FF00FFu);
+  step(4, 0x0F0F0F0Fu);
+  step(2, 0x33333333u);
+  step(1, 0x55555555u);
   return (uint64_t)lo | ((uint64_t)hi << 32);
 }
 
 // Level 2b: per chunk of 512 entries of one super-tile list (four
-// wavefronts, 128 entries each), the number of entries per tile.
+// wavefronts, 128 entries each), the number of entries per tile.  Workgroups
+// take chunks c = blockIdx.x, blockIdx.x + gridDim.x, ... up to the chunk
+// count on the device.
 __global__ void __launch_bounds__(kL1Group)
 l2_count_kernel(const uint32_t* __restrict__ st_start, const uint32_t* __restrict__ chunk_first,
                 const uint32_t* __restrict__ chunk_st, const uint32_t* __restrict__ nchunks,
                 int64_t cap, const uint64_t* __restrict__ masks, uint32_t* __restrict__ cnt2) {
   __shared__ uint32_t s_wc[kWavesPerBlock][kWave];
-  const uint32_t c = blockIdx.x;
-  if (c >= nchunks[0]) return;
+  const uint32_t nch = nchunks[0];
   const int t = (int)threadIdx.x, w = t / kWave, l = lane_id();
-  const uint32_t s = chunk_st[c];
-  const uint32_t e0 = st_start[s] + (c - chunk_first[s]) * kL2Chunk;
-  const uint32_t e1 = (uint32_t)imin(imin((int)st_start[s + 1], (int)(e0 + kL2Chunk)), (int)cap);
-  uint32_t cnt = 0;
-  const uint32_t q0 = e0 + (uint32_t)w * (kL2Chunk / kWavesPerBlock);
-  const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
-  for (uint32_t base = q0; base < q1; base += kWave) {
-    const uint32_t e = base + (uint32_t)l;
-    const uint64_t m = e < q1 ? masks[e] : 0ull;
-    cnt += (uint32_t)__popcll(transpose64(m));  // lane j: entries with tile j
+  for (uint32_t c = blockIdx.x; c < nch; c += gridDim.x) {
+    const uint32_t s = chunk_st[c];
+    const uint32_t e0 = st_start[s] + (c - chunk_first[s]) * kL2Chunk;
+    const uint32_t e1 = (uint32_t)imin(imin((int)st_start[s + 1], (int)(e0 + kL2Chunk)), (int)cap);
+    uint32_t cnt = 0;
+    const uint32_t q0 = e0 + (uint32_t)w * (kL2Chunk / kWavesPerBlock);
+    const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
+    for (uint32_t base = q0; base < q1; base += kWave) {
+      const uint32_t e = base + (uint32_t)l;
+      const uint64_t m = e < q1 ? masks[e] : 0ull;
+      cnt += (uint32_t)__popcll(transpose64(m));  // lane j: entries with tile j
+    }
+    s_wc[w][l] = cnt;
+    __syncthreads();
+    if (t < kWave) cnt2[(size_t)c * kWave + t] = s_wc[0][t] + s_wc[1][t] + s_wc[2][t] + s_wc[3][t];
+    __syncthreads();  // before the next chunk's counts
   }
-  s_wc[w][l] = cnt;
-  __syncthreads();
-  if (t < kWave) cnt2[(size_t)c * kWave + t] = s_wc[0][t] + s_wc[1][t] + s_wc[2][t] + s_wc[3][t];
 }
 
 // Level 2c: per super-tile, each chunk's exclusive prefix per tile (base2)
@@ -1556,24 +1562,29 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
 // Level 2e: every entry's tiles written at tile start + entries of the tile
 // in earlier chunks + rank in this chunk (list order).
 //
-// A chunk whose output fits the LDS stage (at most kL2Stage entries): four
-// wavefronts take 128 entries each.  Per round of 64 entries, a 64x64 bit
-// transpose gives lane j the ballot of the entries having tile j; each lane
-// then walks the set bits of its own mask, fetching the entry's index and
-// depth bits with ds_bpermute.  The output is staged in LDS grouped by tile
-// and written run by run (consecutive lanes, consecutive positions;
-// wavefront w writes tiles j = w mod 4).
+// The chunk's 512 entries (index, depth bits) are kept in LDS.  A chunk whose
+// output fits the stage (at most kL2Stage outputs): four wavefronts take 128
+// entries each.  Per round of 64 entries, a 64x64 bit transpose gives lane j
+// the ballot of the entries having tile j; each lane then walks the set bits
+// of its own mask and stages the entries' chunk positions (16 bits each)
+// grouped by tile.  The output is then written run by run (consecutive lanes,
+// consecutive positions; wavefront w writes tiles j = w mod 4), each slot's
+// index and depth bits read from the chunk's entries.  The stage takes 9 KB
+// and the entries 4 KB, so LDS admits more than eight workgroups per CU.
 //
 // A larger chunk (wide Gaussians, whose masks are dense) is written tile by
-// tile: every wavefront holds the chunk's 512 entries in registers (eight per
+// tile: every wavefront holds the chunk's 512 masks in registers (eight per
 // lane) and takes tiles j = w mod 4; per tile and round of 64 entries, the
 // ballot of "has tile j" and the lane's rank below it place the entries at
 // consecutive positions, so each store is one contiguous run.
+//
+// Workgroups take chunks c = blockIdx.x, blockIdx.x + gridDim.x, ... up to the
+// chunk count on the device, so the grid need not cover the host's bound.
 constexpr int kL2Stage = 4608;
 constexpr int kL2PerLane = kL2Chunk / kWave;  // 8 entries per lane on the tile-by-tile path
-static_assert(kL2Stage >= 2 * kL2Chunk, "the tile-by-tile path stages a chunk in the stage arrays");
+static_assert(kL2Stage * 2 >= kL2Chunk * 8, "the tile-by-tile path keeps a chunk's masks in the stage");
 template <bool kCarry>
-__global__ void __launch_bounds__(kL1Group)
+__global__ void __launch_bounds__(kL1Group, 8)
 l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
                const uint32_t* __restrict__ st_start, const uint32_t* __restrict__ chunk_first,
                const uint32_t* __restrict__ chunk_st, const uint32_t* __restrict__ nchunks,
@@ -1581,144 +1592,146 @@ l2_emit_kernel(StGrid sg, const uint32_t* __restrict__ list,
                const uint32_t* __restrict__ base2, const uint32_t* __restrict__ tile_start,
                int32_t P, const float* __restrict__ depths, const uint32_t* __restrict__ ldb,
                int64_t K, uint64_t* __restrict__ keys, uint32_t* __restrict__ point_list) {
-  __shared__ __align__(16) uint32_t s_g[kL2Stage];
-  __shared__ __align__(16) uint32_t s_db[kL2Stage];
+  __shared__ __align__(16) uint16_t s_idx[kL2Stage];   // staged outputs: chunk positions
+  __shared__ __align__(16) uint32_t s_eg[kL2Chunk];    // the chunk's entries: Gaussian index
+  __shared__ __align__(16) uint32_t s_edb[kL2Chunk];   // and depth bits
   __shared__ uint32_t s_wc[kWavesPerBlock][kWave];
-  const uint32_t c = blockIdx.x;
-  if (c >= nchunks[0]) return;
+  const uint32_t nch = nchunks[0];
   const int t = (int)threadIdx.x, w = t / kWave, l = lane_id();
-  const uint32_t s = chunk_st[c];
-  const uint32_t e0 = st_start[s] + (c - chunk_first[s]) * kL2Chunk;
-  const uint32_t e1 = (uint32_t)imin(imin((int)st_start[s + 1], (int)(e0 + kL2Chunk)), (int)K);
-  const int x0 = (int)(s % (uint32_t)sg.sgx) * kSt, y0 = (int)(s / (uint32_t)sg.sgx) * kSt;
-  // lane j: tile j's chunk count, staging offset and global base
-  const uint32_t cj = cnt2[(size_t)c * kWave + l];
-  const uint32_t ci = wave_incl_scan(cj);
-  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)ci, kWave - 1);
-  uint32_t gbase = 0;
-  {
-    const int x = x0 + (l % kSt), y = y0 + (l / kSt);
-    if (x < sg.gx && y < sg.gy) gbase = tile_start[y * sg.gx + x] + base2[(size_t)c * kWave + l];
-  }
-  if (total > (uint32_t)kL2Stage) {  // uniform: the tile-by-tile path
-    // the chunk's entries are loaded once per workgroup into the (here
-    // unused) staging arrays: masks in s_g, indices and depth bits in s_db
-    uint64_t* s_m = reinterpret_cast<uint64_t*>(s_g);
-    for (int q = t; q < kL2Chunk; q += kL1Group) {
-      const uint32_t e = e0 + (uint32_t)q;
-      const bool valid = e < e1;
-      const uint64_t m = valid ? masks[e] : 0ull;
-      const uint32_t g = valid ? list[e] : 0u;
-      s_m[q] = m;
-      s_db[q] = g;
-      s_db[kL2Chunk + q] =
-          kCarry ? (valid ? ldb[e] : 0xFFFFFFFFu)
-                 : ((m != 0ull && g < (uint32_t)P) ? __float_as_uint(depths[g]) : 0xFFFFFFFFu);
+  for (uint32_t c = blockIdx.x; c < nch; c += gridDim.x) {
+    const uint32_t s = chunk_st[c];
+    const uint32_t e0 = st_start[s] + (c - chunk_first[s]) * kL2Chunk;
+    const uint32_t e1 = (uint32_t)imin(imin((int)st_start[s + 1], (int)(e0 + kL2Chunk)), (int)K);
+    const int x0 = (int)(s % (uint32_t)sg.sgx) * kSt, y0 = (int)(s / (uint32_t)sg.sgx) * kSt;
+    // lane j: tile j's chunk count, staging offset and global base
+    const uint32_t cj = cnt2[(size_t)c * kWave + l];
+    const uint32_t ci = wave_incl_scan(cj);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)ci, kWave - 1);
+    uint32_t gbase = 0;
+    {
+      const int x = x0 + (l % kSt), y = y0 + (l / kSt);
+      if (x < sg.gx && y < sg.gy) gbase = tile_start[y * sg.gx + x] + base2[(size_t)c * kWave + l];
     }
-    __syncthreads();
-    uint64_t em[kL2PerLane];
-    uint32_t eg[kL2PerLane], edb[kL2PerLane];
-#pragma unroll
-    for (int r = 0; r < kL2PerLane; ++r) {
-      const int q = r * kWave + l;
-      em[r] = s_m[q];
-      eg[r] = s_db[q];
-      edb[r] = s_db[kL2Chunk + q];
-    }
-    for (int j = w; j < kWave; j += kWavesPerBlock) {
-      const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
-      if (nj == 0u) continue;
-      uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)gbase, j);
-      const uint32_t end = pos + nj;
-      const uint64_t tile = (uint64_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt)) << 32;
-#pragma unroll
-      for (int r = 0; r < kL2PerLane; ++r) {
-        const bool has = ((em[r] >> j) & 1ull) != 0ull;
-        const uint64_t bal = __ballot(has);
-        const uint32_t at = pos + (uint32_t)__popcll(bal & lanemask_lt());
-        // positions stay inside tile j's range of this chunk
-        if (has && at < end && (int64_t)at < K) {
-          keys[at] = tile | (uint64_t)edb[r];
-          point_list[at] = eg[r];
-        }
-        pos += (uint32_t)__popcll(bal);
+    if (total > (uint32_t)kL2Stage) {  // uniform: the tile-by-tile path
+      // the chunk's entries are loaded once per workgroup: masks in the
+      // (here unused) stage, indices and depth bits in the entry arrays
+      uint64_t* s_m = reinterpret_cast<uint64_t*>(s_idx);
+      for (int q = t; q < kL2Chunk; q += kL1Group) {
+        const uint32_t e = e0 + (uint32_t)q;
+        const bool valid = e < e1;
+        const uint64_t m = valid ? masks[e] : 0ull;
+        const uint32_t g = valid ? list[e] : 0u;
+        s_m[q] = m;
+        s_eg[q] = g;
+        s_edb[q] = kCarry ? (valid ? ldb[e] : 0xFFFFFFFFu)
+                          : ((m != 0ull && g < (uint32_t)P) ? __float_as_uint(depths[g]) : 0xFFFFFFFFu);
       }
-    }
-    return;
-  }
-  const uint32_t q0 = e0 + (uint32_t)w * (kL2Chunk / kWavesPerBlock);
-  const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
-  // the wavefront's entries, two rounds of 64, all loaded at once (the depth
-  // gathers follow the indices and stay in flight across the barrier)
-  constexpr int kRounds = kL2Chunk / kWavesPerBlock / kWave;
-  static_assert(kRounds == 2, "two rounds of 64 entries per wavefront");
-  uint64_t m[kRounds], bt[kRounds];
-  uint32_t g[kRounds], db[kRounds];
+      __syncthreads();
+      uint64_t em[kL2PerLane];  // the masks in registers; index and depth bits read when taken
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    const uint32_t e = q0 + (uint32_t)(r * kWave + l);
-    const bool in = e < q1;
-    m[r] = in ? masks[e] : 0ull;
-    g[r] = in ? list[e] : 0u;
-    if (kCarry) db[r] = in ? ldb[e] : 0u;
-  }
-  if (!kCarry) {
+      for (int r = 0; r < kL2PerLane; ++r) em[r] = s_m[r * kWave + l];
+      for (int j = w; j < kWave; j += kWavesPerBlock) {
+        const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
+        if (nj == 0u) continue;
+        uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)gbase, j);
+        const uint32_t end = pos + nj;
+        const uint64_t tile = (uint64_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt)) << 32;
+#pragma unroll
+        for (int r = 0; r < kL2PerLane; ++r) {
+          const bool has = ((em[r] >> j) & 1ull) != 0ull;
+          const uint64_t bal = __ballot(has);
+          const uint32_t at = pos + (uint32_t)__popcll(bal & lanemask_lt());
+          // positions stay inside tile j's range of this chunk
+          if (has && at < end && (int64_t)at < K) {
+            keys[at] = tile | (uint64_t)s_edb[r * kWave + l];
+            point_list[at] = s_eg[r * kWave + l];
+          }
+          pos += (uint32_t)__popcll(bal);
+        }
+      }
+      __syncthreads();  // before the next chunk restages the arrays
+      continue;
+    }
+    const int qw = w * (kL2Chunk / kWavesPerBlock);  // the wavefront's first chunk position
+    const uint32_t q0 = e0 + (uint32_t)qw;
+    const uint32_t q1 = (uint32_t)imin((int)e1, (int)(q0 + kL2Chunk / kWavesPerBlock));
+    // the wavefront's entries, two rounds of 64, all loaded at once (the depth
+    // gathers follow the indices and stay in flight across the barrier)
+    constexpr int kRounds = kL2Chunk / kWavesPerBlock / kWave;
+    static_assert(kRounds == 2, "two rounds of 64 entries per wavefront");
+    uint64_t m[kRounds], bt[kRounds];
+    uint32_t g[kRounds], db[kRounds];
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
       const uint32_t e = q0 + (uint32_t)(r * kWave + l);
-      db[r] = (e < q1 && g[r] < (uint32_t)P) ? __float_as_uint(depths[g[r]]) : 0xFFFFFFFFu;
+      const bool in = e < q1;
+      m[r] = in ? masks[e] : 0ull;
+      g[r] = in ? list[e] : 0u;
+      if (kCarry) db[r] = in ? ldb[e] : 0u;
     }
-  }
-  // this wavefront's entries per tile (lane j)
-  {
-    uint32_t cnt = 0;
+    if (!kCarry) {
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        const uint32_t e = q0 + (uint32_t)(r * kWave + l);
+        db[r] = (e < q1 && g[r] < (uint32_t)P) ? __float_as_uint(depths[g[r]]) : 0xFFFFFFFFu;
+      }
+    }
+    // this wavefront's entries per tile (lane j)
+    {
+      uint32_t cnt = 0;
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        bt[r] = transpose64(m[r]);
+        cnt += (uint32_t)__popcll(bt[r]);
+      }
+      s_wc[w][l] = cnt;
+    }
+    const uint32_t soff = ci - cj;
+    lds_barrier();
+    uint32_t cur = soff;
+    for (int k = 0; k < w; ++k) cur += s_wc[k][l];
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
-      bt[r] = transpose64(m[r]);
-      cnt += (uint32_t)__popcll(bt[r]);
+      // lane j: the round's entries having tile j (bit i = entry i).  Lane j
+      // walks them in entry (depth) order and stages each one's chunk
+      // position; the loop runs as often as the busiest tile of the round
+      // has entries.
+      const uint32_t qr = (uint32_t)(qw + r * kWave);
+      uint64_t b = bt[r];
+      uint32_t at = cur;
+      while (__ballot(b != 0ull) != 0ull) {
+        const bool act = b != 0ull;
+        const uint32_t src = act ? (uint32_t)__builtin_ctzll(b) : 0u;
+        b &= b - 1ull;
+        if (act && at < (uint32_t)kL2Stage) s_idx[at] = (uint16_t)(qr + src);
+        if (act) ++at;
+      }
+      cur += (uint32_t)__popcll(bt[r]);  // lane j: tile j's entries in this round
     }
-    s_wc[w][l] = cnt;
-  }
-  const uint32_t soff = ci - cj;
-  lds_barrier();
-  uint32_t cur = soff;
-  for (int k = 0; k < w; ++k) cur += s_wc[k][l];
+    // the entries themselves, after the loads have landed (the walk above
+    // needs only the masks)
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    // lane j: the round's entries having tile j (bit i = entry i).  Lane j
-    // walks them in entry (depth) order and fetches each entry's index and
-    // depth bits from its lane; the loop runs as often as the busiest tile
-    // of the round has entries.
-    uint64_t b = bt[r];
-    uint32_t at = cur;
-    while (__ballot(b != 0ull) != 0ull) {
-      const bool act = b != 0ull;
-      const int src = act ? ((int)__builtin_ctzll(b) << 2) : 0;
-      b &= b - 1ull;
-      const uint32_t gi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)g[r]);
-      const uint32_t dbi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)db[r]);
-      if (act && at < (uint32_t)kL2Stage) {
-        s_g[at] = gi;
-        s_db[at] = dbi;
-      }
-      if (act) ++at;
+    for (int r = 0; r < kRounds; ++r) {
+      s_eg[qw + r * kWave + l] = g[r];
+      s_edb[qw + r * kWave + l] = db[r];
     }
-    cur += (uint32_t)__popcll(bt[r]);  // lane j: tile j's entries in this round
-  }
-  __syncthreads();
-  for (int j = w; j < kWave; j += kWavesPerBlock) {
-    const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
-    if (nj == 0u) continue;
-    const uint32_t oj = (uint32_t)__builtin_amdgcn_readlane((int)soff, j);
-    const uint32_t gj = (uint32_t)__builtin_amdgcn_readlane((int)gbase, j);
-    const uint64_t tile = (uint64_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt)) << 32;
-    for (uint32_t k = (uint32_t)l; k < nj; k += kWave) {
-      const uint32_t pos = gj + k;
-      if ((int64_t)pos < K && oj + k < (uint32_t)kL2Stage) {
-        keys[pos] = tile | (uint64_t)s_db[oj + k];
-        point_list[pos] = s_g[oj + k];
+    lds_barrier();
+    for (int j = w; j < kWave; j += kWavesPerBlock) {
+      const uint32_t nj = (uint32_t)__builtin_amdgcn_readlane((int)cj, j);
+      if (nj == 0u) continue;
+      const uint32_t oj = (uint32_t)__builtin_amdgcn_readlane((int)soff, j);
+      const uint32_t gj = (uint32_t)__builtin_amdgcn_readlane((int)gbase, j);
+      const uint64_t tile = (uint64_t)((y0 + j / kSt) * sg.gx + x0 + (j % kSt)) << 32;
+      for (uint32_t k = (uint32_t)l; k < nj; k += kWave) {
+        const uint32_t pos = gj + k;
+        if ((int64_t)pos < K && oj + k < (uint32_t)kL2Stage) {
+          const uint32_t q = s_idx[oj + k] & (uint32_t)(kL2Chunk - 1);
+          keys[pos] = tile | (uint64_t)s_edb[q];
+          point_list[pos] = s_eg[q];
+        }
       }
     }
+    lds_barrier();  // before the next chunk restages the arrays
   }
 }
 
@@ -2084,18 +2097,19 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     hipLaunchKernelGGL(l1_wide_masks_kernel, dim3(kWideGroups), dim3(256), 0, st, sg, io->mult,
                        st_start, P, io->xys, io->conic_opacity, list, K, masks);
     const unsigned nch = (unsigned)L.max_chunks;
-    hipLaunchKernelGGL(l2_count_kernel, dim3(nch), dim3(kL1Group), 0, st, st_start, chunk_first,
+    const unsigned egrid = nch < (unsigned)kL2EmitGrid ? nch : (unsigned)kL2EmitGrid;
+    hipLaunchKernelGGL(l2_count_kernel, dim3(egrid), dim3(kL1Group), 0, st, st_start, chunk_first,
                        chunk_st, nchunks, K, masks, cnt2);
     hipLaunchKernelGGL(l2_st_scan_kernel, dim3(sg.S), dim3(kWave), 0, st, sg, chunk_first, cnt2,
                        base2, tile_total, L.max_chunks);
     hipLaunchKernelGGL(l2_tile_scan_kernel, dim3(1), dim3(1024), 0, st, T, tile_total, tile_start,
                        io->ranges, io->bucket_count, io->bucket_offsets, ww);
     if (carry)
-      hipLaunchKernelGGL(l2_emit_kernel<true>, dim3(nch), dim3(kL1Group), 0, st, sg, list,
+      hipLaunchKernelGGL(l2_emit_kernel<true>, dim3(egrid), dim3(kL1Group), 0, st, sg, list,
                          st_start, chunk_first, chunk_st, nchunks, masks, cnt2, base2, tile_start,
                          P, io->depths, ldb, K, io->point_list_keys, io->point_list);
     else
-      hipLaunchKernelGGL(l2_emit_kernel<false>, dim3(nch), dim3(kL1Group), 0, st, sg, list,
+      hipLaunchKernelGGL(l2_emit_kernel<false>, dim3(egrid), dim3(kL1Group), 0, st, sg, list,
                          st_start, chunk_first, chunk_st, nchunks, masks, cnt2, base2, tile_start,
                          P, io->depths, ldb, K, io->point_list_keys, io->point_list);
     return check_launch("binning_sorted (two-level)");
