@@ -18,7 +18,7 @@ FGS_OK = 0
 FGS_ERR_INVALID_ARGUMENT = -1
 FGS_ERR_LAUNCH = -2
 FGS_ERR_UNSUPPORTED = -3
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 
 class PreprocessParams(Structure):
@@ -36,7 +36,7 @@ class PreprocessFwdIO(Structure):
         "means3d", "dc", "sh", "colors_precomp", "opacities", "scales", "rotations",
         "cov3d_precomp", "viewmatrix", "projmatrix", "campos", "viewspace_in", "radii", "xys",
         "depths", "cov3d", "rgb", "conic_opacity", "tiles_touched", "clamped", "viewspace_out",
-        "st_base", "st_masks", "log_scales", "raw_rotations", "opacity_logits")]
+        "st_rec", "st_masks", "log_scales", "raw_rotations", "opacity_logits")]
 
 
 class PreprocessBwdIO(Structure):
@@ -55,7 +55,7 @@ class BinningIO(Structure):
         ("mult", c_float),
     ] + [(n, c_void_p) for n in (
         "xys", "depths", "conic_opacity", "tiles_touched", "point_list_keys", "point_list",
-        "ranges", "bucket_count", "bucket_offsets", "workspace", "depth_order", "st_base",
+        "ranges", "bucket_count", "bucket_offsets", "workspace", "depth_order", "st_rec",
         "st_masks", "wait_status", "host_result")]
 
 

@@ -1085,15 +1085,17 @@ __device__ __forceinline__ int rec_st(uint32_t w, int k, const StGrid& sg) {
 
 // Level 1a: per depth-ordered Gaussian its super-tiles, and per workgroup
 // the number of its Gaussians touching each super-tile.  The preprocess
-// record (st_base word != 0) gives either four super-tile masks (fits) or the
-// 256-bit super-tile set; a Gaussian without one walks its tiles into the
+// record (word != 0) gives either four super-tile masks (fits, or compact:
+// one 8x8 board expanded here) or the 256-bit super-tile set (the masks and
+// the set are gathered from st_masks; a compact record is its 16 bytes
+// alone); a Gaussian without one walks its tiles into the
 // set.  Stored in depth order for l1_place: recw[i] (the record word; 0 or
 // kStRecSet mean a set) and sets[4i..4i+3] (the masks, or the set).
 __global__ void __launch_bounds__(kL1Group)
 l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ order,
                 const uint32_t* __restrict__ nvis, const float* __restrict__ xys,
                 const float* __restrict__ conic_opacity,
-                const uint32_t* __restrict__ tiles_touched, const uint32_t* __restrict__ st_base,
+                const uint32_t* __restrict__ tiles_touched, const uint32_t* __restrict__ st_rec,
                 const uint64_t* __restrict__ st_masks, uint32_t* __restrict__ recw,
                 uint64_t* __restrict__ sets, uint32_t* __restrict__ cnt1) {
   __shared__ uint32_t s_cnt[kMaxSt];
@@ -1108,8 +1110,15 @@ l1_count_kernel(int32_t P, StGrid sg, float mult, const uint32_t* __restrict__ o
   if (i < nv) {
     const uint32_t g = order[i];
     if (g < (uint32_t)P) {
-      w = st_base ? st_base[g] : 0u;
-      if (w != 0u) {
+      uint4 rec = make_uint4(0u, 0u, 0u, 0u);
+      if (st_rec) rec = reinterpret_cast<const uint4*>(st_rec)[g];
+      w = rec.x;
+      if (w & kStRecCompact) {  // the board alone: back to the fits form
+        const uint32_t x0 = w & 0xFFFu, y0 = (w >> 12) & 0xFFFu;
+        st_expand_compact((uint64_t)rec.z | ((uint64_t)rec.w << 32), (int)(x0 & 7u),
+                          (int)(y0 & 7u), m);
+        w = (x0 >> 3) | ((y0 >> 3) << 12) | kStRecFits;
+      } else if (w != 0u) {
         const uint4* src = reinterpret_cast<const uint4*>(st_masks + 4 * (size_t)g);
         const uint4 a = src[0], b = src[1];
         m[0] = (uint64_t)a.x | ((uint64_t)a.y << 32);
@@ -2035,10 +2044,11 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
   const int32_t T = (int32_t)T64;
   if (!io->ranges || !io->bucket_count || !io->bucket_offsets || !io->workspace)
     return set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_binning_sorted: null pointer");
-  if (!io->st_base != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u))
+  if (!io->st_rec != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u) ||
+      (reinterpret_cast<uintptr_t>(io->st_rec) & 15u))
     return set_error(FGS_ERR_INVALID_ARGUMENT,
-                     "fgs_binning_sorted: st_base and st_masks must both be set (st_masks "
-                     "16-byte aligned) or both NULL");
+                     "fgs_binning_sorted: st_rec and st_masks must both be set (16-byte aligned) "
+                     "or both NULL");
   hipStream_t st = (hipStream_t)stream;
   const StGrid sg = st_grid(io->grid_x, io->grid_y);
   char* ws = (char*)io->workspace;
@@ -2079,7 +2089,7 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     uint32_t* recw = (uint32_t*)(ws + L.recw);
     const uint32_t* nvis = depth_nvis_word(dws, P);
     hipLaunchKernelGGL(l1_count_kernel, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, io->mult, order,
-                       nvis, io->xys, io->conic_opacity, io->tiles_touched, io->st_base,
+                       nvis, io->xys, io->conic_opacity, io->tiles_touched, io->st_rec,
                        io->st_masks, recw, sets, cnt1);
     hipLaunchKernelGGL(l1_seg_scan_kernel, dim3(kL1Segs), dim3(kMaxSt), 0, st, (int)nwg1, sg.S,
                        cnt1, segsum);

@@ -49,7 +49,7 @@ int32_t launch_mark(LaunchKind k, hipStream_t st, int after) {
 
 extern "C" const char* fgs_last_error(void) { return g_last_error; }
 
-extern "C" int32_t fgs_abi_version(void) { return 15; }
+extern "C" int32_t fgs_abi_version(void) { return 16; }
 
 extern "C" int32_t fgs_set_launch_events(const char* kernel, void* start, void* stop) {
   if (!kernel) return fgs::set_error(FGS_ERR_INVALID_ARGUMENT, "fgs_set_launch_events: null name");

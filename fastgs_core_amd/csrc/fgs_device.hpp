@@ -438,11 +438,37 @@ struct NoEmit {
 //    least one of the Gaussian's tiles.  Record word kStRecSet.
 // A Gaussian that touches no tile, or a wide one on a larger grid, has record
 // word 0.
+//
+// A fits record whose tile rectangle is at most 8x8 tiles, from tile (x0, y0)
+// with x0, y0 < 4096, is stored compact: its tiles as one 8x8 board relative
+// to (x0, y0) (bit (y - y0) * 8 + (x - x0)), record word
+// x0 | y0 << 12 | kStRecCompact.  The 16-byte record (word, 0, board) is all
+// the binning then gathers for it; st_expand_compact gives back the fits form.
 // ---------------------------------------------------------------------------
 constexpr int kStTiles = 8;
 constexpr int kStMaxSet = 256;
 constexpr uint32_t kStRecFits = 1u << 31;
 constexpr uint32_t kStRecSet = 1u << 30;
+constexpr uint32_t kStRecCompact = 1u << 29;
+
+// 8x8 bit boards (byte r = row r, bit c = column c): the low n bits of every
+// row, 0 <= n <= 8.
+__device__ __forceinline__ uint64_t st_byte_mask(int n) {
+  return 0x0101010101010101ull * (uint64_t)((1u << n) - 1u);
+}
+
+// The fits form (four boards of the 2x2 super-tiles from the one holding
+// (x0, y0)) of a compact board M, with (ox, oy) = (x0 mod 8, y0 mod 8):
+// board column c goes to column ox + c, left (m0, m2) or right (m1, m3);
+// board row r to row oy + r, top (m0, m1) or bottom (m2, m3).
+__device__ __forceinline__ void st_expand_compact(uint64_t M, int ox, int oy, uint64_t (&m)[4]) {
+  const uint64_t lw = (M << ox) & ~st_byte_mask(ox);
+  const uint64_t rw = ox ? ((M >> (8 - ox)) & st_byte_mask(ox)) : 0ull;
+  m[0] = lw << (8 * oy);
+  m[1] = rw << (8 * oy);
+  m[2] = oy ? (lw >> (64 - 8 * oy)) : 0ull;
+  m[3] = oy ? (rw >> (64 - 8 * oy)) : 0ull;
+}
 
 // bits [a, b) of one 8-bit mask row (0 <= a, b <= 8)
 __device__ __forceinline__ uint64_t st_row_bits(int a, int b) {
@@ -469,9 +495,11 @@ __device__ __forceinline__ uint64_t st_set_word(int lo, int hi, int k) {
 struct EmitStRecord {
   uint64_t m0 = 0ull, m1 = 0ull, m2 = 0ull, m3 = 0ull;
   int bx = 0, by = 0;
+  int ox = 0, oy = 0;    // the rectangle's corner inside super-tile (bx, by)
   int sgx = 0;           // super-tile grid width
   bool set_ok = false;   // the grid has at most kStMaxSet super-tiles
   bool fits = false;
+  bool compact = false;  // fits, in at most 8x8 tiles from a corner below 4096
   __device__ __forceinline__ EmitStRecord(int gx, int gy) {
     sgx = (gx + kStTiles - 1) / kStTiles;
     set_ok = sgx * ((gy + kStTiles - 1) / kStTiles) <= kStMaxSet;
@@ -481,6 +509,9 @@ struct EmitStRecord {
     by = y0 / kStTiles;
     fits = (x1 - 1) / kStTiles - bx <= 1 && (y1 - 1) / kStTiles - by <= 1 && bx < 4096 &&
            by < 4096;
+    ox = x0 - kStTiles * bx;
+    oy = y0 - kStTiles * by;
+    compact = fits && x1 - x0 <= kStTiles && y1 - y0 <= kStTiles && x0 < 4096 && y0 < 4096;
   }
   __device__ __forceinline__ void operator()(int u, int vmin, int vmax, bool is_y) {
     // every update is a select on all four words: a branch or an index here
@@ -533,6 +564,18 @@ struct EmitStRecord {
   __device__ __forceinline__ uint32_t word() const {
     if (fits) return (uint32_t)bx | ((uint32_t)by << 12) | kStRecFits;
     return set_ok ? kStRecSet : 0u;
+  }
+  // compact form: the word and the 8x8 board from (ox, oy) of the 16x16
+  // tiles m0..m3 cover (rows oy.., then columns ox..; every tile of a compact
+  // rectangle lies there)
+  __device__ __forceinline__ uint32_t compact_word() const {
+    return (uint32_t)(kStTiles * bx + ox) | ((uint32_t)(kStTiles * by + oy) << 12) | kStRecCompact;
+  }
+  __device__ __forceinline__ uint64_t compact_board() const {
+    const uint64_t l = oy ? ((m0 >> (8 * oy)) | (m2 << (64 - 8 * oy))) : m0;
+    const uint64_t r = oy ? ((m1 >> (8 * oy)) | (m3 << (64 - 8 * oy))) : m1;
+    const uint64_t keep = st_byte_mask(8 - ox);
+    return ((l >> ox) & keep) | (ox ? ((r << (8 - ox)) & ~keep) : 0ull);
   }
   // OR of the four words over the wavefront (after tiles_walk_wave)
   __device__ __forceinline__ void wave_or() {

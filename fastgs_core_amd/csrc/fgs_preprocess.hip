@@ -397,16 +397,24 @@ preprocess_fwd_kernel(const fgs_preprocess_params prm, const fgs_preprocess_fwd_
       io.clamped[3 * I + c] = clamp[c];
     }
   }
-  if (io.st_base) {
-    const uint32_t w = cnt != 0u ? st.word() : 0u;
-    io.st_base[I] = w;
-    if (w != 0u) {
-      uint4* dst = reinterpret_cast<uint4*>(io.st_masks + 4 * I);
-      dst[0] = make_uint4((uint32_t)st.m0, (uint32_t)(st.m0 >> 32), (uint32_t)st.m1,
-                          (uint32_t)(st.m1 >> 32));
-      dst[1] = make_uint4((uint32_t)st.m2, (uint32_t)(st.m2 >> 32), (uint32_t)st.m3,
-                          (uint32_t)(st.m3 >> 32));
+  if (io.st_rec) {
+    // a compact record is the 16 bytes alone; the others add their four
+    // words in st_masks
+    uint4 rec = make_uint4(0u, 0u, 0u, 0u);
+    if (cnt != 0u && st.compact) {
+      const uint64_t b = st.compact_board();
+      rec = make_uint4(st.compact_word(), 0u, (uint32_t)b, (uint32_t)(b >> 32));
+    } else if (cnt != 0u) {
+      rec.x = st.word();
+      if (rec.x != 0u) {
+        uint4* dst = reinterpret_cast<uint4*>(io.st_masks + 4 * I);
+        dst[0] = make_uint4((uint32_t)st.m0, (uint32_t)(st.m0 >> 32), (uint32_t)st.m1,
+                            (uint32_t)(st.m1 >> 32));
+        dst[1] = make_uint4((uint32_t)st.m2, (uint32_t)(st.m2 >> 32), (uint32_t)st.m3,
+                            (uint32_t)(st.m3 >> 32));
+      }
     }
+    reinterpret_cast<uint4*>(io.st_rec)[I] = rec;
   }
 }
 
@@ -804,8 +812,9 @@ static int32_t preprocess_fwd_check(const fgs_preprocess_params* p, const fgs_pr
   }
   if (p->image_width <= 0 || p->image_height <= 0 || p->grid_x <= 0 || p->grid_y <= 0)
     return fail("bad image size");
-  if (!io->st_base != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u))
-    return fail("st_base and st_masks must both be set (st_masks 16-byte aligned) or both NULL");
+  if (!io->st_rec != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u) ||
+      (reinterpret_cast<uintptr_t>(io->st_rec) & 15u))
+    return fail("st_rec and st_masks must both be set (16-byte aligned) or both NULL");
   return FGS_OK;
 }
 

@@ -233,7 +233,7 @@ class _Preprocess(torch.autograd.Function):
             _p(means3d), _p(dc), _p(sh), _p(colors_precomp), _p(opacities), _p(scales),
             _p(rotations), _p(cov3d_precomp), _p(viewmatrix), _p(projmatrix), _p(campos),
             _p(viewspace_in), _p(radii), _p(xys), _p(depths), _p(cov3d), _p(rgb), _p(conic),
-            _p(tiles), _p(clamped), _p(vsp_out), _p(cfg["st_base"]), _p(cfg["st_masks"]),
+            _p(tiles), _p(clamped), _p(vsp_out), _p(cfg["st_rec"]), _p(cfg["st_masks"]),
             _p(log_scales), _p(raw_rotations), _p(opacity_logits))
         if P > 0 and cfg.get("split_colour"):
             # geometry on this stream; the colour half on the side stream after
@@ -261,7 +261,7 @@ class _Preprocess(torch.autograd.Function):
             with _stage("preprocess_fwd"):
                 _lib.check(lib.fgs_preprocess_fwd(ctypes.byref(prm), ctypes.byref(io),
                                                   _stream(dev)))
-        ctx.cfg = dict(cfg, st_base=None, st_masks=None, colour_done=None,
+        ctx.cfg = dict(cfg, st_rec=None, st_masks=None, colour_done=None,
                        colour_launch=None)  # forward-only
         ctx.opacity_shape = (opacity_logits if cfg.get("raw") else opacities).shape
         ctx.sh_shape = None if sh is None else sh.shape
@@ -442,7 +442,7 @@ def _inclusive_scan_i32(x: torch.Tensor, side=None) -> torch.Tensor:
 
 def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: float,
                     depth_ws: Optional[torch.Tensor] = None,
-                    st_base: Optional[torch.Tensor] = None,
+                    st_rec: Optional[torch.Tensor] = None,
                     st_masks: Optional[torch.Tensor] = None, host_word=None):
     lib = _lib.load()
     dev = xys.device
@@ -458,7 +458,7 @@ def _binning_sorted(xys, depths, conic, tiles, K: int, gx: int, gy: int, mult: f
     ws = torch.empty(int(lib.fgs_binning_workspace_bytes(P, K, T)), dtype=torch.uint8, device=dev)
     io = _lib.BinningIO(P, gx, gy, K, mult, _p(xys), _p(depths), _p(conic), _p(tiles), _p(keys),
                         _p(plist), _p(ranges), _p(bucket_count), _p(bucket_offsets), _p(ws),
-                        _p(depth_ws), _p(st_base), _p(st_masks), _p(tbuf[4 * T:]),
+                        _p(depth_ws), _p(st_rec), _p(st_masks), _p(tbuf[4 * T:]),
                         _p(host_word[0]) if host_word is not None else None)
     with _stage("binning"):
         _lib.check(lib.fgs_binning_sorted(ctypes.byref(io), _stream(dev)))
@@ -673,10 +673,10 @@ def _run_preprocess(inputs, fn, names, image_width, image_height, block_x, block
     cfg = dict(degree=int(degree), max_sh=max_sh, W=int(image_width), H=int(image_height), gx=gx,
                gy=gy, use_cov=has_cov, use_col=has_col, scale_modifier=float(scale_modifier),
                mult=float(mult), tan_fovx=float(tan_fovx), tan_fovy=float(tan_fovy),
-               st_base=None, st_masks=None, raw=raw, split_colour=bool(st_records and SPLIT_COLOUR),
+               st_rec=None, st_masks=None, raw=raw, split_colour=bool(st_records and SPLIT_COLOUR),
                colour_done=None)
     if st_records and ((gx + 7) // 8) * ((gy + 7) // 8) <= 256:
-        cfg["st_base"] = torch.empty(P, dtype=torch.int32, device=dev)
+        cfg["st_rec"] = torch.empty((P, 4), dtype=torch.int32, device=dev)
         cfg["st_masks"] = torch.empty((P, 4), dtype=torch.int64, device=dev)
     dc = f(inputs["dc"]) if sh_path else None
     sh = f(inputs["sh"]) if sh_path else None
@@ -788,7 +788,7 @@ def rasterize_gaussians_forward(inputs: Dict[str, Any], image_width: int, image_
         with torch.no_grad():
             (point_list_keys, point_list, ranges, bucket_count, bucket_offsets,
              tbuf) = _binning_sorted(xys.detach(), depths.detach(), conic.detach(), tiles, K, gx,
-                                     gy, float(mult), depth_ws, cfg["st_base"], cfg["st_masks"],
+                                     gy, float(mult), depth_ws, cfg["st_rec"], cfg["st_masks"],
                                      host_word)
         if ws:
             # the sampled state is B * 256 entries: B is needed before the launch

@@ -105,19 +105,24 @@ typedef struct {
   float* viewspace_out;        /* [P,4] */
   /* Optional (NULL: not written) super-tile records for fgs_binning_sorted,
    * no reference counterpart.  Super-tiles are 8x8 tiles, numbered row-major
-   * on a grid ceil(grid_x/8) wide.  Two forms:
-   *  - st_base[i] = bx | by << 12 | 1u << 31: the Gaussian's tile rectangle
-   *    lies in the 2x2 super-tiles from (bx, by), the super-tile of its
-   *    corner; st_masks[4i + k] = its tiles in super-tile
-   *    (bx + (k & 1), by + (k >> 1)), bit (y mod 8) * 8 + (x mod 8);
-   *  - st_base[i] = 1u << 30 (other rectangles, grids of at most 256
-   *    super-tiles): bit s of the 256-bit st_masks[4i..4i+3] marks each
-   *    super-tile s holding one of its tiles;
-   *  - st_base[i] = 0: no tile touched (or a wide Gaussian on a larger
-   *    grid); st_masks[4i..] not written.
-   * Both set or both NULL. */
-  uint32_t* st_base;           /* [P] */
-  uint64_t* st_masks;          /* [P,4], 16-byte aligned */
+   * on a grid ceil(grid_x/8) wide.  Record i is st_rec[4i..4i+3] =
+   * (word, 0, lo, hi), in one of four forms:
+   *  - word = x0 | y0 << 12 | 1u << 29 (compact): the Gaussian's tile
+   *    rectangle has at most 8x8 tiles from tile (x0, y0), x0, y0 < 4096;
+   *    lo | hi << 32 is its 8x8 board, bit (y - y0) * 8 + (x - x0) for tile
+   *    (x, y); st_masks[4i..] not written;
+   *  - word = bx | by << 12 | 1u << 31: the rectangle lies in the 2x2
+   *    super-tiles from (bx, by), the super-tile of its corner;
+   *    st_masks[4i + k] = its tiles in super-tile (bx + (k & 1), by + (k >> 1)),
+   *    bit (y mod 8) * 8 + (x mod 8);
+   *  - word = 1u << 30 (other rectangles, grids of at most 256 super-tiles):
+   *    bit s of the 256-bit st_masks[4i..4i+3] marks each super-tile s
+   *    holding one of its tiles;
+   *  - word = 0: no tile touched (or a wide Gaussian on a larger grid);
+   *    st_masks[4i..] not written.
+   * Both set or both NULL, 16-byte aligned. */
+  uint32_t* st_rec;            /* [P,4] */
+  uint64_t* st_masks;          /* [P,4] */
   /* Training-step fusion (no reference counterpart; optional, NULL = off):
    * the raw parameters, activated here as the training scripts do
    * (train_scanner_fixed.py:523-536): scale = exp(log_scale), rotation =
@@ -307,7 +312,7 @@ typedef struct {
   const void* depth_order;
   /* NULL, or the super-tile records fgs_preprocess_fwd wrote for these
    * Gaussians (same grid): Gaussians with a record skip their tile walks. */
-  const uint32_t* st_base;
+  const uint32_t* st_rec;
   const uint64_t* st_masks;
   /* NULL, or a device word the call writes with the wait status (see above)
    * of its own waits and of the depth order it consumes (depth_order, or the
