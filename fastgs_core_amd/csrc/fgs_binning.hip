@@ -514,7 +514,10 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     const int64_t nd = (int64_t)*opt.n_dev;
     n = nd < n_max ? nd : n_max;
   }
-  const int64_t chunk = take_ticket_lds(ticket, &s_slot);  // includes a barrier
+  // chunks in workgroup order: a chunk waits only on lower-numbered chunks,
+  // which each XCD dispatches before it (the bounded waits are the backstop)
+  const int64_t chunk = (int64_t)blockIdx.x;
+  lds_barrier();  // the digit counters' clear
   if (opt.fill_tail) {
     // positions [n, n_max) get the sentinel pair (all-ones key, value)
     for (int64_t j = n + chunk * kC + t; j < n + (chunk + 1) * kC && j < n_max; j += kT) {
