@@ -1240,7 +1240,7 @@ l1_top_scan_kernel(int S, uint32_t* __restrict__ segsum, uint32_t* __restrict__ 
 // pass.  A record's masks are written as they are; a Gaussian given by its
 // super-tile set gets mask 0, filled in by l1_wide_masks_kernel (every real
 // pair has at least one tile, so 0 marks exactly those).
-constexpr int kL1Pairs = 2048;  // LDS pair capacity per round
+constexpr int kL1Pairs = 1024;  // LDS pair capacity per round
 template <bool kCarry>
 __global__ void __launch_bounds__(kL1Group)
 l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
@@ -1386,11 +1386,19 @@ l1_wide_masks_kernel(StGrid sg, float mult, const uint32_t* __restrict__ st_star
        c0 += (int64_t)gridDim.x * kWideChunk) {
     if (t == 0) s_n = 0u;
     __syncthreads();
-#pragma unroll 4
-    for (int k = 0; k < kWideChunk / 256; ++k) {
+    // every mask load is issued before the first test (entries past the end
+    // read as non-zero), so the chunk waits one memory latency, not one per
+    // group of loads
+    constexpr int kPer = kWideChunk / 256;
+    uint64_t mv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
       const int64_t e = c0 + k * 256 + t;
-      if (e < k1 && masks[e] == 0ull) s_e[atomicAdd(&s_n, 1u)] = (uint32_t)(e - c0);
+      mv[k] = e < k1 ? masks[e] : 1ull;
     }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+      if (mv[k] == 0ull) s_e[atomicAdd(&s_n, 1u)] = (uint32_t)(k * 256 + t);
     __syncthreads();
     const uint32_t n = s_n;
     for (uint32_t j = (uint32_t)t; j < n; j += 256) {
