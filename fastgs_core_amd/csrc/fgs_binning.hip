@@ -487,8 +487,8 @@ __global__ void __launch_bounds__(kT)
 radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                   K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n_max,
                   int shift, int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
-                  uint64_t* gstatus, int64_t nchunks, uint32_t* ticket, uint32_t* err,
-                  uint32_t spin_limit, SortPassOpts opt) {
+                  uint64_t* gstatus, int64_t nchunks, uint32_t* err, uint32_t spin_limit,
+                  SortPassOpts opt) {
   constexpr int kW = kT / kWave;
   constexpr int kC = kT * kIt;
   __shared__ uint32_t s_wh[kW][256];
@@ -496,7 +496,6 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
   __shared__ uint32_t s_goff[256];
   __shared__ uint32_t s_tmp[kW + 1];
   __shared__ uint32_t s_tmp2[kW + 1];
-  __shared__ uint32_t s_slot;
   __shared__ uint32_t s_total;
   __shared__ K s_keys[kC];
   __shared__ uint32_t s_vals[kC];
@@ -679,8 +678,9 @@ static int64_t sort_chunks(int64_t n) {
   return (n + c - 1) / c;
 }
 
-// Zero-initialised state of one sort: histograms (8 x 256), tickets (8),
-// error word, then the status words of every pass (per chunk), then those of
+// Zero-initialised state of one sort: histograms (8 x 256), eight reserved
+// words, the error word, the visible-key count of a depth sort, then the
+// status words of every pass (per chunk), then those of
 // the look-back groups of every pass.
 static size_t sort_state_bytes(int64_t n, int passes) {
   const int64_t nc = sort_chunks(n);
@@ -690,7 +690,7 @@ static size_t sort_state_bytes(int64_t n, int passes) {
 }
 
 // The error word inside a sort workspace (tmp keys, tmp values, then the state:
-// histograms, tickets, error word).
+// histograms, eight reserved words, error word).
 template <typename K>
 static uint32_t* sort_err_word(void* ws, int64_t n) {
   char* p = (char*)ws;
@@ -744,8 +744,8 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   uint32_t* tv = (uint32_t*)p;
   p += ((size_t)n * 4 + 255) & ~(size_t)255;
   uint32_t* hist = (uint32_t*)p;
-  uint32_t* tickets = hist + 8 * 256;
-  uint32_t* err = werr ? werr : tickets + 8;
+  uint32_t* words = hist + 8 * 256;  // eight reserved words, the error word, the count
+  uint32_t* err = werr ? werr : words + 8;
   uint64_t* status = (uint64_t*)(p + 8 * 256 * 4 + 64);
   const int64_t ngr = (nc + kLbGroup - 1) / kLbGroup;
   uint64_t* gstat = status + (size_t)pl.passes * nc * 256;
@@ -765,8 +765,8 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   const uint32_t spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   const int64_t hn = (n + kChunk - 1) / kChunk;  // histogram workgroups: 4096 keys each
   const int64_t hb = hn < 1024 ? hn : 1024;
-  // the depth sort's visible-key count, beside the pass tickets in the zeroed state
-  uint32_t* nvis = tickets + 10;
+  // the depth sort's visible-key count, in the zeroed state
+  uint32_t* nvis = words + 10;
   hipLaunchKernelGGL((radix_hist_kernel<K, kDepthKeys>), dim3((unsigned)hb), dim3(kThreads), 0, st,
                      keys_in, n, pl, hist, depths, tiles_touched, dkeys_out, nvis);
   const K* src_k = kDepthKeys ? (const K*)dkeys_out : keys_in;
@@ -789,14 +789,12 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
                          status + (size_t)pass * nc * 256, gstat + (size_t)pass * ngr * 256, nc,
-                         tickets + pass, err, spin_limit,
-                         opt);
+                         err, spin_limit, opt);
     else
       hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 4>), dim3((unsigned)nc), dim3(kSortT), 0,
                          st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
                          status + (size_t)pass * nc * 256, gstat + (size_t)pass * ngr * 256, nc,
-                         tickets + pass, err, spin_limit,
-                         opt);
+                         err, spin_limit, opt);
     const int32_t e2 = check_launch("radix_pass");
     if (e2 != FGS_OK) return e2;
     shift += pl.bits[pass];

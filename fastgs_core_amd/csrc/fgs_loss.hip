@@ -296,7 +296,6 @@ l1_ssim_bwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
       ring[sl][m] = h;
     }
     if (first && i < 2 * kLR) return;  // compile-time
-    const int orow = r0 + i - 2 * kLR;
     float B[3] = {0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < 11; ++k) {
