@@ -457,7 +457,7 @@ __device__ __forceinline__ void bwd_batch(const float4* s_a, const float4* s_b, 
 // One wavefront per 16x16 tile; lane l owns the pixels (col l&15, row 4k +
 // l/16), k = 0..3, one in each 16x4 strip.
 template <int NCH>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64, 5)
 raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, RasterShape sh) {
   __shared__ float4 s_a[kBwdBatch];
   __shared__ float4 s_b[kBwdBatch];
@@ -565,26 +565,28 @@ raster_bwd_kernel(const fgs_raster_params prm, const fgs_raster_bwd_io io, Raste
       bwd_batch<NCH, true>(s_a, s_b, s_h, s_cull, s_rec, lo, cnt, l, pxf, pyf0, nc, nc_max,
                            T, SdL, dL);
     __syncthreads();
-    // Flush: item q = (splat q/12, term q%12), so the lanes of one atomic
-    // instruction cover the consecutive terms of about five splats.
-    const uint32_t C = (uint32_t)prm.num_channels;
-#pragma unroll 1
-    for (int i = 0; i < kRec; ++i) {
-      const int q = i * kBwdBatch + l;
-      const int s = q / kRec, t = q - (q / kRec) * kRec;
-      if (s < cnt && t < 8 + NCH) {
+    // Flush: lane l takes term ft = l & 15 of splats 4i + (l >> 4), so every
+    // lane keeps one term (its array, row stride, column and factor) for the
+    // whole flush, and one atomic instruction covers the rows of four splats.
+    // Terms 0..3 are viewspace, 4..7 conic and opacity, 8.. colour (rows of
+    // 4, 4 and num_channels floats).
+    const int ft = l & 15, fs0 = l >> 4;
+    const bool ft_ok = ft < 8 + NCH;
+    float* const fbase = ft < 4 ? io.dL_dviewspace : (ft < 8 ? io.dL_dconic_opacity : io.dL_dcolors);
+    const uint32_t fstride = ft < 8 ? 4u : (uint32_t)prm.num_channels;
+    const uint32_t fcol = (uint32_t)(ft < 4 ? ft : (ft < 8 ? ft - 4 : ft - 8));
+#pragma unroll 4
+    for (int i = 0; i < (cnt + 3) / 4; ++i) {
+      const int s = 4 * i + fs0;
+      if (s < cnt && ft_ok) {
         // the splat's factor on its geometry terms: -o for the means2d
         // terms, |o| for their magnitudes, -o/2 for the conic's
         const float hz = s_cull[s].z;  // -o/2
-        const float f = t < 2 ? 2.0f * hz : (t < 4 ? fabsf(2.0f * hz) : (t < 7 ? hz : 1.0f));
-        const float w = s_rec[q] * f;
+        const float f = ft >= 7 ? 1.0f : (ft < 4 ? (ft < 2 ? 2.0f * hz : fabsf(2.0f * hz)) : hz);
+        const float w = s_rec[s * kRec + ft] * f;
         const uint32_t g = s_g[s];
-        if (w != 0.0f && g < (uint32_t)P) {
-          float* dst = t < 4 ? io.dL_dviewspace + 4 * (size_t)g + t
-                             : (t < 8 ? io.dL_dconic_opacity + 4 * (size_t)g + (t - 4)
-                                      : io.dL_dcolors + (size_t)g * C + (t - 8));
-          unsafeAtomicAdd(dst, w);
-        }
+        if (w != 0.0f && g < (uint32_t)P)
+          unsafeAtomicAdd(fbase + ((uint64_t)g * fstride + fcol), w);
       }
     }
     __syncthreads();
