@@ -108,7 +108,11 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
   const int tile = (int)blockIdx.x;
   const int tx = tile % sh.gx, ty = tile / sh.gx;
   const int t = (int)threadIdx.x;
-  const int lx = t & 15, ly = t >> 4;
+  // wavefront w blends the 8x8 quarter (w & 1, w >> 1) of the tile: compact
+  // blocks stop at more similar times than 16x4 strips
+  const int w8 = t >> 6;
+  const int lx = ((w8 & 1) << 3) | (t & 7), ly = ((w8 >> 1) << 3) | ((t >> 3) & 7);
+  const int tp = ly * 16 + lx;  // the pixel's index in the tile
   const int px = tx * kTile + lx, py = ty * kTile + ly;
   const bool inside = px < sh.W && py < sh.H;
   const size_t HW = (size_t)sh.W * (size_t)sh.H;
@@ -178,10 +182,10 @@ raster_fwd_kernel(const fgs_raster_params prm, const fgs_raster_fwd_io io, Raste
           if (kSampled && (jj & 31) == 0 && jj < n && live) {
             const size_t bk = (size_t)bbm0 + (size_t)(jj >> 5);
             if ((int64_t)bk < prm.bucket_sum) {
-              io.sampled_t[bk * 256 + t] = T;
+              io.sampled_t[bk * 256 + tp] = T;
 #pragma unroll
               for (int c = 0; c < NCH; ++c)
-                io.sampled_ar[bk * (size_t)prm.num_channels * 256 + (size_t)c * 256 + t] = acc[c];
+                io.sampled_ar[bk * (size_t)prm.num_channels * 256 + (size_t)c * 256 + tp] = acc[c];
             }
           }
           const float4 a = s_a[j];
