@@ -1019,7 +1019,6 @@ constexpr int kL1Group = 256;   // level-1 Gaussians per workgroup
 constexpr int kL1Segs = 64;     // level-1 row segments of the count scan
 constexpr int kL2Chunk = 512;   // level-2 entries per workgroup (4 wavefronts x 128)
 constexpr int kL2EmitGrid = 4096;  // workgroups of l2_count and l2_emit at most (chunk loops)
-constexpr int kWideGroups = 512;  // grid of l1_wide_masks_kernel
 constexpr int kScanBatch = 32;    // loads in flight per serial-scan batch
 
 struct StGrid {
@@ -1235,10 +1234,30 @@ l1_top_scan_kernel(int S, uint32_t* __restrict__ segsum, uint32_t* __restrict__ 
 // distinct, so their order among themselves is free) and ranked per
 // super-tile in that order, 256 at a time: wave64 match-any over the 8
 // super-tile bits, then the four waves through LDS counters, as in a radix
-// pass.  A record's masks are written as they are; a Gaussian given by its
-// super-tile set gets mask 0, filled in by l1_wide_masks_kernel (every real
-// pair has at least one tile, so 0 marks exactly those).
+// pass.  A record's masks are written as they are.  The pairs of a Gaussian
+// given by its super-tile set (a wide one) carry no mask: the workgroup
+// collects them in LDS and, after its last round, walks each one clipped to
+// its super-tile's window, one pair per thread, so the few walks run side by
+// side (beyond kL1Wide pairs, the thread that places a pair walks it).
 constexpr int kL1Pairs = 1024;  // LDS pair capacity per round
+constexpr int kL1Wide = 256;    // wide pairs a workgroup collects before walking them
+
+// The tile mask of Gaussian g in super-tile sid: its walk clipped to the
+// super-tile's 8x8-tile window.
+__device__ __forceinline__ uint64_t wide_pair_mask(const StGrid& sg, float mult,
+                                                   const float* __restrict__ xys,
+                                                   const float* __restrict__ conic_opacity,
+                                                   uint32_t g, int sid) {
+  EmitTileMask em;
+  em.m = 0ull;
+  em.x0 = (sid % sg.sgx) * kSt;
+  em.y0 = (sid / sg.sgx) * kSt;
+  const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
+  const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
+  tiles_walk_window(xy.x, xy.y, co, sg.gx, sg.gy, mult, em.x0, em.x0 + kSt, em.y0, em.y0 + kSt,
+                    em);
+  return em.m;
+}
 template <bool kCarry>
 __global__ void __launch_bounds__(kL1Group)
 l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
@@ -1247,8 +1266,13 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
                 const uint64_t* __restrict__ sets, const uint32_t* __restrict__ cnt1,
                 const uint32_t* __restrict__ segsum, const uint32_t* __restrict__ st_start,
                 int64_t cap, uint32_t* __restrict__ list, uint64_t* __restrict__ masks,
-                uint32_t* __restrict__ ldb) {
+                uint32_t* __restrict__ ldb, float mult, const float* __restrict__ xys,
+                const float* __restrict__ conic_opacity) {
   __shared__ uint64_t s_pm[kL1Pairs];  // mask of each pair (0: walk it)
+  __shared__ uint32_t s_wpos[kL1Wide];  // wide pairs: list position
+  __shared__ uint32_t s_wg[kL1Wide];    // its Gaussian
+  __shared__ uint8_t s_wd[kL1Wide];     // and super-tile
+  __shared__ uint32_t s_nw;
   __shared__ uint32_t s_pg[kL1Pairs];  // Gaussian of each pair
   __shared__ uint32_t s_pd[kCarry ? kL1Pairs : 1];  // kCarry: its depth bits (sorted key)
   __shared__ uint8_t s_ps[kL1Pairs];   // super-tile of each pair
@@ -1259,6 +1283,7 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
   const int t = (int)threadIdx.x;
   const int w = t / kWave;
   const int i = (int)blockIdx.x * kL1Group + t;
+  if (t == 0) s_nw = 0u;  // ordered before its use by the barriers of the scan below
   uint64_t m[4] = {0ull, 0ull, 0ull, 0ull};
   uint32_t g = 0, rw = 0, db = 0;
   // the sentinel tail from the visible count on was not written by l1_count
@@ -1348,9 +1373,22 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
         uint32_t pos = s_base[d] + rk;
         for (int k = 0; k < w; ++k) pos += s_wh[k][d];
         if ((int64_t)pos < cap) {
-          list[pos] = s_pg[q];
-          masks[pos] = s_pm[q];
+          const uint32_t g = s_pg[q];
+          const uint64_t pm = s_pm[q];
+          list[pos] = g;
           if (kCarry) ldb[pos] = s_pd[q];
+          if (pm != 0ull || g >= (uint32_t)P) {
+            masks[pos] = pm;
+          } else {  // a wide pair: its mask is walked below (here, if the list is full)
+            const uint32_t k = atomicAdd(&s_nw, 1u);
+            if (k < (uint32_t)kL1Wide) {
+              s_wpos[k] = pos;
+              s_wg[k] = g;
+              s_wd[k] = (uint8_t)d;
+            } else {
+              masks[pos] = wide_pair_mask(sg, mult, xys, conic_opacity, g, (int)d);
+            }
+          }
         }
       }
       __syncthreads();
@@ -1358,68 +1396,10 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
       __syncthreads();
     }
   }
-}
-
-// Level 1e: the mask of every list entry l1_place left 0 (a Gaussian given
-// by its super-tile set; every real pair has at least one tile, so 0 marks
-// exactly those): its walk clipped to the super-tile window.  A workgroup
-// takes 4096 entries at a time, collects the chunk's zero masks in LDS, then
-// walks them one per thread, so the few walks run side by side.  The
-// super-tile of entry e is the list holding it (binary search over the list
-// starts, staged in LDS).
-constexpr int kWideChunk = 4096;
-__global__ void __launch_bounds__(256)
-l1_wide_masks_kernel(StGrid sg, float mult, const uint32_t* __restrict__ st_start, int32_t P,
-                     const float* __restrict__ xys, const float* __restrict__ conic_opacity,
-                     const uint32_t* __restrict__ list, int64_t cap,
-                     uint64_t* __restrict__ masks) {
-  __shared__ uint32_t s_ss[kMaxSt + 1];
-  __shared__ uint32_t s_e[kWideChunk];
-  __shared__ uint32_t s_n;
-  const int t = (int)threadIdx.x;
-  for (int k = t; k <= sg.S; k += 256) s_ss[k] = st_start[k];
-  __syncthreads();
-  const int64_t k1 = (int64_t)s_ss[sg.S] < cap ? (int64_t)s_ss[sg.S] : cap;
-  for (int64_t c0 = (int64_t)blockIdx.x * kWideChunk; c0 < k1;
-       c0 += (int64_t)gridDim.x * kWideChunk) {
-    if (t == 0) s_n = 0u;
-    __syncthreads();
-    // every mask load is issued before the first test (entries past the end
-    // read as non-zero), so the chunk waits one memory latency, not one per
-    // group of loads
-    constexpr int kPer = kWideChunk / 256;
-    uint64_t mv[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int64_t e = c0 + k * 256 + t;
-      mv[k] = e < k1 ? masks[e] : 1ull;
-    }
-#pragma unroll
-    for (int k = 0; k < kPer; ++k)
-      if (mv[k] == 0ull) s_e[atomicAdd(&s_n, 1u)] = (uint32_t)(k * 256 + t);
-    __syncthreads();
-    const uint32_t n = s_n;
-    for (uint32_t j = (uint32_t)t; j < n; j += 256) {
-      const int64_t e = c0 + s_e[j];
-      int lo = 0, hi = sg.S;  // largest s with st_start[s] <= e
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if ((int64_t)s_ss[mid] <= e) lo = mid; else hi = mid;
-      }
-      const uint32_t g = list[e];
-      EmitTileMask em;
-      em.m = 0ull;
-      em.x0 = (lo % sg.sgx) * kSt;
-      em.y0 = (lo / sg.sgx) * kSt;
-      if (g < (uint32_t)P) {
-        const float2 xy = *reinterpret_cast<const float2*>(xys + 2 * (size_t)g);
-        const float4 co = *reinterpret_cast<const float4*>(conic_opacity + 4 * (size_t)g);
-        tiles_walk_window(xy.x, xy.y, co, sg.gx, sg.gy, mult, em.x0, em.x0 + kSt, em.y0,
-                          em.y0 + kSt, em);
-      }
-      masks[e] = em.m;
-    }
-    __syncthreads();
+  // the workgroup's wide pairs, one walk per thread, side by side
+  const uint32_t nw = s_nw < (uint32_t)kL1Wide ? s_nw : (uint32_t)kL1Wide;
+  for (uint32_t k = (uint32_t)t; k < nw; k += kL1Group) {
+    masks[s_wpos[k]] = wide_pair_mask(sg, mult, xys, conic_opacity, s_wg[k], (int)s_wd[k]);
   }
 }
 
@@ -2109,12 +2089,12 @@ extern "C" int32_t fgs_binning_sorted(const fgs_binning_io* io, void* stream) {
     uint32_t* ldb = carry ? (uint32_t*)(ws + L.ldb) : nullptr;
     if (carry)
       hipLaunchKernelGGL(l1_place_kernel<true>, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order,
-                         nvis, skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
+                         nvis, skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb,
+                         io->mult, io->xys, io->conic_opacity);
     else
       hipLaunchKernelGGL(l1_place_kernel<false>, dim3(nwg1), dim3(kL1Group), 0, st, P, sg, order,
-                         nvis, skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb);
-    hipLaunchKernelGGL(l1_wide_masks_kernel, dim3(kWideGroups), dim3(256), 0, st, sg, io->mult,
-                       st_start, P, io->xys, io->conic_opacity, list, K, masks);
+                         nvis, skeys, recw, sets, cnt1, segsum, st_start, K, list, masks, ldb,
+                         io->mult, io->xys, io->conic_opacity);
     const unsigned nch = (unsigned)L.max_chunks;
     const unsigned egrid = nch < (unsigned)kL2EmitGrid ? nch : (unsigned)kL2EmitGrid;
     hipLaunchKernelGGL(l2_count_kernel, dim3(egrid), dim3(kL1Group), 0, st, st_start, chunk_first,
