@@ -1567,8 +1567,10 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
 // of its own mask and stages the entries' chunk positions (16 bits each)
 // grouped by tile.  The output is then written run by run (consecutive lanes,
 // consecutive positions; wavefront w writes tiles j = w mod 4), each slot's
-// index and depth bits read from the chunk's entries.  The stage takes 9 KB
-// and the entries 4 KB, so LDS admits more than eight workgroups per CU.
+// index and depth bits read from the chunk's entries.  The stage holds 9216
+// outputs in 18 KB and the entries take 4 KB, so LDS admits six workgroups
+// per CU (with 4608 outputs, eight: fewer chunks fit the stage, and at 1M
+// Gaussians / 1080p the binning took 5 us longer).
 //
 // A larger chunk (wide Gaussians, whose masks are dense) is written tile by
 // tile: every wavefront holds the chunk's 512 masks in registers (eight per
@@ -1578,7 +1580,7 @@ l2_tile_scan_kernel(int32_t T, const uint32_t* __restrict__ tile_total,
 //
 // Workgroups take chunks c = blockIdx.x, blockIdx.x + gridDim.x, ... up to the
 // chunk count on the device, so the grid need not cover the host's bound.
-constexpr int kL2Stage = 4608;
+constexpr int kL2Stage = 9216;
 constexpr int kL2PerLane = kL2Chunk / kWave;  // 8 entries per lane on the tile-by-tile path
 static_assert(kL2Stage * 2 >= kL2Chunk * 8, "the tile-by-tile path keeps a chunk's masks in the stage");
 template <bool kCarry>
