@@ -1,8 +1,9 @@
 // fgs_raster.hip -- tile rasterization forward and backward (gfx950, wave64).
 //
 // Forward (semantics of fastgs_rasterize.metal:25-159): one 256-thread
-// workgroup per 16x16 tile, one pixel per thread, wavefront w owning rows
-// 4w..4w+3.  The tile's sorted splat list is streamed through LDS in batches
+// workgroup per 16x16 tile, one pixel per thread, wavefront w owning the 8x8
+// quarter (w & 1, w >> 1).  The tile's sorted splat list is streamed through
+// LDS in batches
 // of 256 (each thread stages one splat: 2D mean, conic, opacity, colour and
 // opacity), then every pixel blends the batch front to back.  Pixels stop at
 // T < 1e-4; a wavefront whose pixels have all stopped skips the blend loop,
