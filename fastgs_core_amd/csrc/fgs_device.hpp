@@ -492,6 +492,60 @@ __device__ __forceinline__ uint64_t st_set_word(int lo, int hi, int k) {
   return ((n >= 64) ? ~0ull : ((1ull << n) - 1ull)) << (a - 64 * k);
 }
 
+// The record bits of one walk span (tile row u, columns [vmin, vmax), or
+// column u, rows [vmin, vmax)) for a Gaussian with the given record geometry
+// (fits: the 2x2 super-tiles from (bx, by); otherwise, when set_ok, the
+// super-tile set on a grid sgx super-tiles wide).  Every update is a select on
+// all four words: a branch or an index here becomes a scratch access.
+__device__ __forceinline__ void st_span_bits(bool fits, bool set_ok, int bx, int by, int sgx, int u,
+                                             int vmin, int vmax, bool is_y, uint64_t (&d)[4]) {
+  d[0] = d[1] = d[2] = d[3] = 0ull;
+  if (fits) {
+    if (is_y) {  // tile row u, columns [vmin, vmax)
+      const int r = u - kStTiles * by;
+      const int c0 = vmin - kStTiles * bx, c1 = vmax - kStTiles * bx;
+      const int sh = (r & 7) * 8;
+      const uint64_t a = st_row_bits(c0, imin(c1, 8)) << sh;
+      const uint64_t b = st_row_bits(imax(c0, 8) - 8, c1 - 8) << sh;
+      const bool top = r < 8;
+      d[0] = top ? a : 0ull;
+      d[1] = top ? b : 0ull;
+      d[2] = top ? 0ull : a;
+      d[3] = top ? 0ull : b;
+    } else {  // tile column u, rows [vmin, vmax)
+      const int c = u - kStTiles * bx;
+      const int r0 = vmin - kStTiles * by, r1 = vmax - kStTiles * by;
+      const uint64_t a = st_col_bits(r0, imin(r1, 8), c & 7);
+      const uint64_t b = st_col_bits(imax(r0, 8) - 8, r1 - 8, c & 7);
+      const bool left = c < 8;
+      d[0] = left ? a : 0ull;
+      d[2] = left ? b : 0ull;
+      d[1] = left ? 0ull : a;
+      d[3] = left ? 0ull : b;
+    }
+  } else if (set_ok) {
+    const int b = u / kStTiles;
+    const int c0 = vmin / kStTiles, c1 = (vmax - 1) / kStTiles;
+    if (is_y) {  // row u: super-tiles b*sgx + c0 .. b*sgx + c1
+      const int lo = b * sgx + c0, hi = b * sgx + c1;
+      d[0] = st_set_word(lo, hi, 0);
+      d[1] = st_set_word(lo, hi, 1);
+      d[2] = st_set_word(lo, hi, 2);
+      d[3] = st_set_word(lo, hi, 3);
+    } else {  // column u: super-tiles c*sgx + b, c = c0..c1
+      for (int c = c0; c <= c1; ++c) {
+        const int sb = c * sgx + b;
+        const uint64_t bit = 1ull << (sb & 63);
+        const int k = sb >> 6;
+        d[0] |= k == 0 ? bit : 0ull;
+        d[1] |= k == 1 ? bit : 0ull;
+        d[2] |= k == 2 ? bit : 0ull;
+        d[3] |= k == 3 ? bit : 0ull;
+      }
+    }
+  }
+}
+
 struct EmitStRecord {
   uint64_t m0 = 0ull, m1 = 0ull, m2 = 0ull, m3 = 0ull;
   int bx = 0, by = 0;
@@ -514,52 +568,12 @@ struct EmitStRecord {
     compact = fits && x1 - x0 <= kStTiles && y1 - y0 <= kStTiles && x0 < 4096 && y0 < 4096;
   }
   __device__ __forceinline__ void operator()(int u, int vmin, int vmax, bool is_y) {
-    // every update is a select on all four words: a branch or an index here
-    // becomes a scratch access
-    if (fits) {
-      if (is_y) {  // tile row u, columns [vmin, vmax)
-        const int r = u - kStTiles * by;
-        const int c0 = vmin - kStTiles * bx, c1 = vmax - kStTiles * bx;
-        const int sh = (r & 7) * 8;
-        const uint64_t a = st_row_bits(c0, imin(c1, 8)) << sh;
-        const uint64_t b = st_row_bits(imax(c0, 8) - 8, c1 - 8) << sh;
-        const bool top = r < 8;
-        m0 |= top ? a : 0ull;
-        m1 |= top ? b : 0ull;
-        m2 |= top ? 0ull : a;
-        m3 |= top ? 0ull : b;
-      } else {  // tile column u, rows [vmin, vmax)
-        const int c = u - kStTiles * bx;
-        const int r0 = vmin - kStTiles * by, r1 = vmax - kStTiles * by;
-        const uint64_t a = st_col_bits(r0, imin(r1, 8), c & 7);
-        const uint64_t b = st_col_bits(imax(r0, 8) - 8, r1 - 8, c & 7);
-        const bool left = c < 8;
-        m0 |= left ? a : 0ull;
-        m2 |= left ? b : 0ull;
-        m1 |= left ? 0ull : a;
-        m3 |= left ? 0ull : b;
-      }
-    } else if (set_ok) {
-      const int b = u / kStTiles;
-      const int c0 = vmin / kStTiles, c1 = (vmax - 1) / kStTiles;
-      if (is_y) {  // row u: super-tiles b*sgx + c0 .. b*sgx + c1
-        const int lo = b * sgx + c0, hi = b * sgx + c1;
-        m0 |= st_set_word(lo, hi, 0);
-        m1 |= st_set_word(lo, hi, 1);
-        m2 |= st_set_word(lo, hi, 2);
-        m3 |= st_set_word(lo, hi, 3);
-      } else {  // column u: super-tiles c*sgx + b, c = c0..c1
-        for (int c = c0; c <= c1; ++c) {
-          const int sb = c * sgx + b;
-          const uint64_t bit = 1ull << (sb & 63);
-          const int k = sb >> 6;
-          m0 |= k == 0 ? bit : 0ull;
-          m1 |= k == 1 ? bit : 0ull;
-          m2 |= k == 2 ? bit : 0ull;
-          m3 |= k == 3 ? bit : 0ull;
-        }
-      }
-    }
+    uint64_t d[4];
+    st_span_bits(fits, set_ok, bx, by, sgx, u, vmin, vmax, is_y, d);
+    m0 |= d[0];
+    m1 |= d[1];
+    m2 |= d[2];
+    m3 |= d[3];
   }
   __device__ __forceinline__ uint32_t word() const {
     if (fits) return (uint32_t)bx | ((uint32_t)by << 12) | kStRecFits;
