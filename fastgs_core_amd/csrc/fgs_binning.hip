@@ -42,11 +42,18 @@ constexpr int kWavesPerBlock = kThreads / kWave;
 // Radix passes keep their status words chunk-major ([chunk][digit]): a
 // chunk's 256 counters are published and read as one contiguous block.  They
 // look back in two levels: a chunk sums its predecessors inside its group of
-// kLbGroup chunks directly and looks back over group totals, which the last
-// chunk of each group publishes (a walk over every earlier chunk had made the
-// last chunks of a 1M-key pass wait about 13 us longer than the first).
-// The spin is bounded as a backstop; it cannot run out while chunks are
-// taken in ticket order.
+// kLbGroup chunks directly, and every chunk also adds its counts into its
+// group's running word ((arrivals << 32) + count, an atomic add), which is
+// complete once all kLbGroup chunks have arrived.  The earlier groups are
+// then walked from the nearest, adding complete group words, until one whose
+// inclusive prefix the group's last chunk has published.  No chunk waits for
+// another's look-back while the group words complete (a walk over every
+// earlier chunk had made the last chunks of a 1M-key pass wait about 13 us
+// longer than the first; group totals summed by each group's last chunk
+// added about a microsecond per pass).
+// Radix passes take their chunk number from the workgroup index: a chunk
+// waits only on lower-numbered chunks, which each XCD dispatches before it.
+// The spins are bounded as a backstop.
 // ---------------------------------------------------------------------------
 // Padded LDS index so that thread t reading its 16 consecutive elements is
 // free of bank conflicts.
@@ -68,68 +75,101 @@ __device__ __forceinline__ void status_store(uint64_t* p, uint32_t flag, uint32_
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Exclusive prefix for chunk `chunk` of one counter whose status words are
-// `stride` apart (status[c * stride], c < chunk).  The nearest unread
-// predecessor is polled alone (with a short sleep) until it has published;
-// the 16 predecessors below it are then read at once (independent loads in
-// flight) and walked from the nearest, adding aggregates until an inclusive
-// prefix is met or an unpublished one is reached.  After spin_limit polls of
-// one predecessor the wait gives up: kWaitLookBack is set in *err and the
-// partial prefix (never above the true one, so every position stays in
-// bounds) is used.  spin_limit == 0 gives up at once without polling.
-__device__ __forceinline__ uint32_t look_back(const uint64_t* status, int64_t chunk,
-                                              int64_t stride, uint32_t* err,
-                                              uint32_t spin_limit) {
+// The two parts of the exclusive prefix of a chunk, chunk q of look-back
+// group g, for one counter whose words are `stride` apart:
+//  in_group: the counts of chunks first .. first + q - 1 (its predecessors
+//    in the group), from their status words st[c] = (flag << 32) + count;
+//    all are read at once (independent loads in flight), then the ones not
+//    yet published are read again;
+//  gexcl: the counts of groups 0 .. g - 1, from their words gsum[h] =
+//    (arrivals << 32) + the arrived chunks' counts, complete at kLbGroup
+//    arrivals, and gpre[h] = (kFlagPrefix << 32) + the inclusive prefix
+//    through group h, once its last chunk has published it.  Windows of 16
+//    groups are read at once and walked from the nearest: a published prefix
+//    ends the walk, a complete group word is added, an incomplete one is read
+//    again with its window.
+// The group words are read after the predecessors: they complete about
+// when those have published (one polling loop over both, whose batches need
+// three times the registers, measured slower beside the preprocess's colour
+// half, which then shared fewer CUs with the pass).  Rereads follow a short
+// sleep.  After spin_limit rereads a wait gives up: kWaitLookBack is set in
+// *err and the partial sums (never above the true ones, so every position
+// stays in bounds) are used.  spin_limit == 0 gives up at once without
+// polling.
+constexpr int kLbGroup = 16;  // chunks per look-back group
+__device__ __forceinline__ void chunk_offsets(const uint64_t* st, int64_t first, int q,
+                                              const uint64_t* gsum, const uint64_t* gpre,
+                                              int64_t g, int64_t stride, uint32_t* err,
+                                              uint32_t spin_limit, uint32_t& in_group,
+                                              uint32_t& gexcl) {
   constexpr int kWin = 16;
-  uint32_t excl = 0;
-  uint32_t spins = 0;
-  int64_t c = chunk - 1;
+  in_group = 0u;
+  gexcl = 0u;
+  if (q == 0 && g == 0) return;
   if (spin_limit == 0u) {
-    if (c >= 0) wait_gave_up(err, kWaitLookBack);
-    return 0u;
+    wait_gave_up(err, kWaitLookBack);
+    return;
   }
-  while (c >= 0) {
-    const uint64_t w0 = __hip_atomic_load(status + c * stride, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t f0 = (uint32_t)(w0 >> 32);
-    if (f0 == 0u) {
+  uint32_t spins = 0;
+  uint32_t pending = (1u << q) - 1u;  // q < kLbGroup
+  while (pending) {
+    uint64_t w[kLbGroup];
+#pragma unroll
+    for (int i = 0; i < kLbGroup; ++i)
+      w[i] = ((pending >> i) & 1u) ? __hip_atomic_load(st + (first + i) * stride,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0ull;
+#pragma unroll
+    for (int i = 0; i < kLbGroup; ++i) {
+      if (((pending >> i) & 1u) && (uint32_t)(w[i] >> 32) != 0u) {
+        in_group += (uint32_t)w[i];
+        pending &= ~(1u << i);
+      }
+    }
+    if (pending) {
       if (++spins > spin_limit) {
         wait_gave_up(err, kWaitLookBack);
-        break;
+        return;
       }
       __builtin_amdgcn_s_sleep(1);
-      continue;
     }
-    excl += (uint32_t)w0;
-    if (f0 == kFlagPrefix) break;
-    --c;
-    if (c < 0) break;
+  }
+  int64_t c = g - 1;  // the nearest group not added yet
+  while (c >= 0) {
     const int64_t lo = c >= kWin - 1 ? c - (kWin - 1) : 0;
-    uint64_t w[kWin];
+    uint64_t wp[kWin], ws[kWin];
 #pragma unroll
-    for (int i = 0; i < kWin; ++i)
-      w[i] = (lo + i <= c) ? __hip_atomic_load(status + (lo + i) * stride, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT)
-                           : 0ull;
-    bool stop = false, done = false;
+    for (int i = 0; i < kWin; ++i) {
+      const bool in = lo + i <= c;
+      wp[i] = in ? __hip_atomic_load(gpre + (lo + i) * stride, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT)
+                 : 0ull;
+      ws[i] = in ? __hip_atomic_load(gsum + (lo + i) * stride, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT)
+                 : 0ull;
+    }
+    bool stalled = false;
 #pragma unroll
     for (int i = kWin - 1; i >= 0; --i) {
-      if (stop || lo + i > c) continue;
-      const uint32_t flag = (uint32_t)(w[i] >> 32);
-      if (flag == 0u) {  // not published yet: poll it alone next
-        stop = true;
-        continue;
-      }
-      excl += (uint32_t)w[i];
-      --c;
-      if (flag == kFlagPrefix) {
-        stop = true;
-        done = true;
+      if (stalled || lo + i > c) continue;
+      if ((uint32_t)(wp[i] >> 32) == kFlagPrefix) {
+        gexcl += (uint32_t)wp[i];
+        c = -1;
+      } else if ((uint32_t)(ws[i] >> 32) == (uint32_t)kLbGroup) {
+        gexcl += (uint32_t)ws[i];
+        --c;
+      } else {
+        stalled = true;  // group c is still incomplete
       }
     }
-    if (done) break;
+    if (stalled) {
+      if (++spins > spin_limit) {
+        wait_gave_up(err, kWaitLookBack);
+        return;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
   }
-  return excl;
 }
 
 // Exclusive prefix of chunk `chunk` of a single counter from the aggregates
@@ -163,45 +203,6 @@ __device__ __forceinline__ uint32_t block_sum_predecessors(const uint64_t* statu
   uint32_t total;
   block_excl_scan(acc, s_tmp, &total);
   return total;
-}
-
-// Sum of the published counts of chunks first .. first + q - 1 (one status
-// word each, `stride` apart): all of them are loaded at once, and the ones
-// not yet published are polled again.  Bounded like look_back.
-constexpr int kLbGroup = 16;  // chunks per look-back group
-__device__ __forceinline__ uint32_t sum_group_preds(const uint64_t* status, int64_t first, int q,
-                                                    int64_t stride, uint32_t* err,
-                                                    uint32_t spin_limit) {
-  if (spin_limit == 0u) {  // the forced error path: give up at once, as look_back
-    if (q > 0) wait_gave_up(err, kWaitLookBack);
-    return 0u;
-  }
-  uint32_t sum = 0;
-  uint32_t pending = (1u << q) - 1u;  // q < kLbGroup
-  uint32_t spins = 0;
-  while (pending) {
-    uint64_t w[kLbGroup];
-#pragma unroll
-    for (int i = 0; i < kLbGroup; ++i)
-      w[i] = ((pending >> i) & 1u) ? __hip_atomic_load(status + (first + i) * stride,
-                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                   : 0ull;
-#pragma unroll
-    for (int i = 0; i < kLbGroup; ++i) {
-      if (((pending >> i) & 1u) && (uint32_t)(w[i] >> 32) != 0u) {
-        sum += (uint32_t)w[i];
-        pending &= ~(1u << i);
-      }
-    }
-    if (pending) {
-      if (++spins > spin_limit) {
-        wait_gave_up(err, kWaitLookBack);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-  }
-  return sum;
 }
 
 // take_ticket with a barrier that orders LDS only: the workgroup's other
@@ -481,14 +482,18 @@ struct SortPassOpts {
 };
 
 // kT threads per workgroup, kT * kIt keys per chunk.  Digit-wise steps
-// (histograms, offsets, look-back) run on the first 256 threads.
-template <typename K, int kT, int kIt>
+// (histograms, offsets, look-back) run on the first 256 threads.  kBits: the
+// digit width when fixed at compile time (8), else 0 (nbits at run time).
+// status: [chunk][digit] words; gsum, gpre: [group][digit] words.
+template <typename K, int kT, int kIt, int kBits>
 __global__ void __launch_bounds__(kT)
 radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                   K* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int64_t n_max,
-                  int shift, int nbits, const uint32_t* __restrict__ hist, uint64_t* status,
-                  uint64_t* gstatus, int64_t nchunks, uint32_t* err, uint32_t spin_limit,
-                  SortPassOpts opt) {
+                  int shift, int nbits_rt, const uint32_t* __restrict__ hist, uint64_t* status,
+                  uint64_t* gsum, uint64_t* gpre, int64_t nchunks, uint32_t* err,
+                  uint32_t spin_limit, SortPassOpts opt) {
+  static_assert(kBits == 0 || kBits == 8, "fixed digits are 8 bits wide");
+  const int nbits = kBits ? kBits : nbits_rt;
   constexpr int kW = kT / kWave;
   constexpr int kC = kT * kIt;
   __shared__ uint32_t s_wh[kW][256];
@@ -558,10 +563,26 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     if (!valid) key[it] = (K)0;
     const uint32_t d = (uint32_t)(key[it] >> shift) & mask;
     uint64_t peers = __ballot(valid);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const uint64_t m = __ballot(bit);
-      peers &= bit ? m : ~m;
+    if constexpr (kBits > 0) {
+      // the lanes that share each bit: sel is all ones where bit b of d is
+      // 0, so (m ^ sel) is the ballot m or its complement (one three-input
+      // bit operation per half with the AND)
+      const uint32_t nd = ~d;
+      uint32_t plo = (uint32_t)peers, phi = (uint32_t)(peers >> 32);
+#pragma unroll
+      for (int b = 0; b < kBits; ++b) {
+        const uint32_t sel = (uint32_t)__builtin_amdgcn_sbfe((int32_t)nd, (uint32_t)b, 1u);
+        const uint64_t m = __ballot(sel == 0u);
+        plo &= (uint32_t)m ^ sel;
+        phi &= (uint32_t)(m >> 32) ^ sel;
+      }
+      peers = ((uint64_t)phi << 32) | plo;
+    } else {
+      for (int b = 0; b < nbits; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
     }
     const uint32_t r = (uint32_t)__popcll(peers & lt);
     uint32_t old = 0;
@@ -621,20 +642,18 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     }
     if (dig) {
       // Two-level offsets: the chunk's predecessors in its group of
-      // kLbGroup chunks are summed directly; the group's offset comes from a
-      // look-back over group totals, which the last chunk of each group
-      // publishes.  A chunk thus waits a few memory round trips, not a chain
-      // of windows over every earlier chunk.
+      // kLbGroup chunks are summed directly; the earlier groups come from
+      // their running words (the chunk's own counts join its group's word
+      // first) and the prefixes the groups' last chunks publish.
       const int64_t g = chunk / kLbGroup;
       const int q = (int)(chunk - g * kLbGroup);
-      const uint32_t in_group =
-          q ? sum_group_preds(st, g * kLbGroup, q, 256, err, spin_limit) : 0u;
-      uint64_t* gst = gstatus + (size_t)t;
-      const bool last_in_group = q == kLbGroup - 1;
-      if (last_in_group)
-        status_store(gst + g * 256, g == 0 ? kFlagPrefix : kFlagAggregate, in_group + tot);
-      const uint32_t gexcl = g ? look_back(gst, g, 256, err, spin_limit) : 0u;
-      if (last_in_group && g > 0) status_store(gst + g * 256, kFlagPrefix, gexcl + in_group + tot);
+      uint64_t* gs = gsum + (size_t)t;
+      uint64_t* gp = gpre + (size_t)t;
+      __hip_atomic_fetch_add(gs + g * 256, (1ull << 32) | (uint64_t)tot, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      uint32_t in_group, gexcl;
+      chunk_offsets(st, g * kLbGroup, q, gs, gp, g, 256, err, spin_limit, in_group, gexcl);
+      if (q == kLbGroup - 1) status_store(gp + g * 256, kFlagPrefix, gexcl + in_group + tot);
       const uint32_t excl = gexcl + in_group;
       s_goff[t] = gbase + excl;
     }
@@ -680,12 +699,13 @@ static int64_t sort_chunks(int64_t n) {
 
 // Zero-initialised state of one sort: histograms (8 x 256), eight reserved
 // words, the error word, the visible-key count of a depth sort, then the
-// status words of every pass (per chunk), then those of
-// the look-back groups of every pass.
+// status words of every pass (per chunk), then the running words of the
+// look-back groups of every pass, then their prefix words.
 static size_t sort_state_bytes(int64_t n, int passes) {
   const int64_t nc = sort_chunks(n);
   const int64_t ng = (nc + kLbGroup - 1) / kLbGroup;
-  return (size_t)((8 * 256 * 4 + 64 + (int64_t)passes * ((nc < 1 ? 1 : nc) + ng) * 256 * 8 + 255) &
+  return (size_t)((8 * 256 * 4 + 64 + (int64_t)passes * ((nc < 1 ? 1 : nc) + 2 * ng) * 256 * 8 +
+                   255) &
                   ~(int64_t)255);
 }
 
@@ -748,7 +768,8 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
   uint32_t* err = werr ? werr : words + 8;
   uint64_t* status = (uint64_t*)(p + 8 * 256 * 4 + 64);
   const int64_t ngr = (nc + kLbGroup - 1) / kLbGroup;
-  uint64_t* gstat = status + (size_t)pl.passes * nc * 256;
+  uint64_t* gsum = status + (size_t)pl.passes * nc * 256;
+  uint64_t* gpre = gsum + (size_t)pl.passes * ngr * 256;
   {
     FillSpans f{};
     f.value = 0u;
@@ -785,16 +806,26 @@ static int32_t radix_sort_pairs(const K* keys_in, const uint32_t* vals_in, K* ke
       opt.n_dev = pass > 0 ? nvis : nullptr;
       opt.fill_tail = pass == pl.passes - 1;
     }
-    if (items == 8)
-      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
-                         st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, gstat + (size_t)pass * ngr * 256, nc,
-                         err, spin_limit, opt);
+    uint64_t* const ps = status + (size_t)pass * nc * 256;
+    uint64_t* const pgs = gsum + (size_t)pass * ngr * 256;
+    uint64_t* const pgp = gpre + (size_t)pass * ngr * 256;
+    const int nb = pl.bits[pass];
+    if (items == 8 && nb == 8)
+      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
+                         st, src_k, src_v, dk, dv, n, shift, nb, hist + pass * 256, ps, pgs, pgp,
+                         nc, err, spin_limit, opt);
+    else if (items == 8)
+      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 8, 0>), dim3((unsigned)nc), dim3(kSortT), 0,
+                         st, src_k, src_v, dk, dv, n, shift, nb, hist + pass * 256, ps, pgs, pgp,
+                         nc, err, spin_limit, opt);
+    else if (nb == 8)
+      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 4, 8>), dim3((unsigned)nc), dim3(kSortT), 0,
+                         st, src_k, src_v, dk, dv, n, shift, nb, hist + pass * 256, ps, pgs, pgp,
+                         nc, err, spin_limit, opt);
     else
-      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 4>), dim3((unsigned)nc), dim3(kSortT), 0,
-                         st, src_k, src_v, dk, dv, n, shift, pl.bits[pass], hist + pass * 256,
-                         status + (size_t)pass * nc * 256, gstat + (size_t)pass * ngr * 256, nc,
-                         err, spin_limit, opt);
+      hipLaunchKernelGGL((radix_pass_kernel<K, kSortT, 4, 0>), dim3((unsigned)nc), dim3(kSortT), 0,
+                         st, src_k, src_v, dk, dv, n, shift, nb, hist + pass * 256, ps, pgs, pgp,
+                         nc, err, spin_limit, opt);
     const int32_t e2 = check_launch("radix_pass");
     if (e2 != FGS_OK) return e2;
     shift += pl.bits[pass];
