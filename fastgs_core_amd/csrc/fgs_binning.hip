@@ -606,7 +606,16 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     uint64_t* st = status + (size_t)t;  // chunk-major: [chunk][digit]
     // the chunk's digit counts are published before the scans, so that the
     // look-backs of later chunks can pass this one sooner
-    if (dig) status_store(st + chunk * 256, kFlagAggregate, tot);
+    const int64_t g = chunk / kLbGroup;
+    const int q = (int)(chunk - g * kLbGroup);
+    uint64_t* gs = gsum + (size_t)t;
+    uint64_t* gp = gpre + (size_t)t;
+    if (dig) {
+      status_store(st + chunk * 256, kFlagAggregate, tot);
+      // the chunk's counts join its group's running word
+      __hip_atomic_fetch_add(gs + g * 256, (1ull << 32) | (uint64_t)tot, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
     // both exclusive scans (global digit bases, chunk digit starts) at once
     uint32_t gbase, ds, total;
     {
@@ -640,32 +649,28 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
       }
       s_dstart[t] = ds;
     }
+    lds_barrier();
+    // the chunk in digit order in LDS (chunk-local positions), before the
+    // look-back: its time overlaps the predecessors' publishing, and the
+    // keys' registers are free during the wait
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      if (vld[it]) {
+        const uint32_t d = (uint32_t)(key[it] >> shift) & mask;
+        const uint32_t pos = s_wh[w][d] + rank[it];
+        s_keys[pos] = key[it];
+        s_vals[pos] = val[it];
+      }
+    }
     if (dig) {
       // Two-level offsets: the chunk's predecessors in its group of
       // kLbGroup chunks are summed directly; the earlier groups come from
-      // their running words (the chunk's own counts join its group's word
-      // first) and the prefixes the groups' last chunks publish.
-      const int64_t g = chunk / kLbGroup;
-      const int q = (int)(chunk - g * kLbGroup);
-      uint64_t* gs = gsum + (size_t)t;
-      uint64_t* gp = gpre + (size_t)t;
-      __hip_atomic_fetch_add(gs + g * 256, (1ull << 32) | (uint64_t)tot, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+      // their running words and the prefixes the groups' last chunks publish.
       uint32_t in_group, gexcl;
       chunk_offsets(st, g * kLbGroup, q, gs, gp, g, 256, err, spin_limit, in_group, gexcl);
       if (q == kLbGroup - 1) status_store(gp + g * 256, kFlagPrefix, gexcl + in_group + tot);
       const uint32_t excl = gexcl + in_group;
       s_goff[t] = gbase + excl;
-    }
-  }
-  lds_barrier();
-#pragma unroll
-  for (int it = 0; it < kIt; ++it) {
-    if (vld[it]) {
-      const uint32_t d = (uint32_t)(key[it] >> shift) & mask;
-      const uint32_t pos = s_wh[w][d] + rank[it];
-      s_keys[pos] = key[it];
-      s_vals[pos] = val[it];
     }
   }
   lds_barrier();
