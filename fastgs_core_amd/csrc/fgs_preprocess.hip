@@ -289,10 +289,13 @@ constexpr int kWaveWalkLines = 16;
 // for the longest walk of their wavefront (at 1M Gaussians / 1080p it ran 7.4
 // lines against 2.9 on average, at 3M with 2 % large Gaussians 14.5 plus 3.7
 // whole-wavefront walks against 6.1 rounds).
+// 6.5 KB per wavefront, so that six wavefronts per SIMD fit in the LDS (the
+// discriminant is recomputed from the conic; the integers are packed).
 struct PackedWalk {
-  enum { kPx, kPy, kCa, kCb, kCc, kDisc, kT, kAm1, kAM1, kBmin0, kBmax0, kBmin1, kBmax1, kIl0, kIl1,
-         kNF };
-  enum { kRmin0, kRmin1, kRmax1, kFlags, kBx, kBy, kStart, kSlot, kCnt, kNI };
+  enum { kPx, kPy, kCa, kCb, kCc, kT, kAm1, kAM1, kBmax0, kBmin1, kBmax1, kIl0, kIl1, kNF };
+  // kOff: rmin0 - start (line u of position p is p + kOff); kR1: rmin1 | rmax1 << 16;
+  // kGeo: is_y | fits << 1 | bx << 2 | by << 17 (the record's corner super-tile)
+  enum { kOff, kR1, kGeo, kSlot, kCnt, kNI };
   float f[kNF][kWave];
   int i[kNI][kWave];
   unsigned long long rec[4][kWave];
@@ -334,24 +337,19 @@ __device__ __forceinline__ uint32_t packed_walk(PackedWalk& S, int nl, const Wal
     S.f[PackedWalk::kCa][l] = co.x;
     S.f[PackedWalk::kCb][l] = co.y;
     S.f[PackedWalk::kCc][l] = co.z;
-    S.f[PackedWalk::kDisc][l] = ws.disc;
     S.f[PackedWalk::kT][l] = ws.t;
     S.f[PackedWalk::kAm1][l] = ws.am1;
     S.f[PackedWalk::kAM1][l] = ws.aM1;
-    S.f[PackedWalk::kBmin0][l] = ws.bmin0;
     S.f[PackedWalk::kBmax0][l] = ws.bmax0;
     S.f[PackedWalk::kBmin1][l] = ws.bmin1;
     S.f[PackedWalk::kBmax1][l] = ws.bmax1;
     S.f[PackedWalk::kIl0][l] = il0;
     S.f[PackedWalk::kIl1][l] = il1;
-    S.i[PackedWalk::kRmin0][l] = ws.rmin0;
-    S.i[PackedWalk::kRmin1][l] = ws.rmin1;
-    S.i[PackedWalk::kRmax1][l] = ws.rmax1;
-    S.i[PackedWalk::kFlags][l] = (ws.is_y ? 1 : 0) | (st.fits ? 2 : 0);
-    S.i[PackedWalk::kBx][l] = st.bx;
-    S.i[PackedWalk::kBy][l] = st.by;
+    S.i[PackedWalk::kOff][l] = ws.rmin0 - start;
+    S.i[PackedWalk::kR1][l] = (int)((uint32_t)ws.rmin1 | ((uint32_t)ws.rmax1 << 16));
+    S.i[PackedWalk::kGeo][l] = (int)((ws.is_y ? 1u : 0u) | (st.fits ? 2u : 0u) |
+                                     ((uint32_t)st.bx << 2) | ((uint32_t)st.by << 17));
   }
-  S.i[PackedWalk::kStart][l] = start;
   S.i[PackedWalk::kCnt][l] = 0;
 #pragma unroll
   for (int k = 0; k < 4; ++k) S.rec[k][l] = 0ull;
@@ -363,6 +361,9 @@ __device__ __forceinline__ uint32_t packed_walk(PackedWalk& S, int nl, const Wal
     if (nl > 0 && start >= base && start < base + kWave) S.i[PackedWalk::kSlot][start - base] = l;
     wave_lds_order();
     int v = S.i[PackedWalk::kSlot][l];
+    // a Gaussian's walk starts at this line: the largest start at or below it
+    // is that Gaussian's, so it is g below
+    const bool first = v >= 0;
     if (l == 0 && v < 0) v = carry_owner;
     const int g = wave_incl_max(v);  // the Gaussian of line base + l
     carry_owner = __builtin_amdgcn_readlane(g, kWave - 1);
@@ -373,12 +374,12 @@ __device__ __forceinline__ uint32_t packed_walk(PackedWalk& S, int nl, const Wal
     w.aM1 = S.f[PackedWalk::kAM1][g];
     w.bmin1 = S.f[PackedWalk::kBmin1][g];
     w.bmax1 = S.f[PackedWalk::kBmax1][g];
-    w.rmin1 = S.i[PackedWalk::kRmin1][g];
-    w.rmax1 = S.i[PackedWalk::kRmax1][g];
-    const int flags = S.i[PackedWalk::kFlags][g];
-    const bool is_y = (flags & 1) != 0;
-    const bool first = p == S.i[PackedWalk::kStart][g];
-    const int u = S.i[PackedWalk::kRmin0][g] + (p - S.i[PackedWalk::kStart][g]);
+    const uint32_t r1 = (uint32_t)S.i[PackedWalk::kR1][g];
+    w.rmin1 = (int)(r1 & 0xFFFFu);
+    w.rmax1 = (int)(r1 >> 16);
+    const uint32_t geo = (uint32_t)S.i[PackedWalk::kGeo][g];
+    const bool is_y = (geo & 1u) != 0u;
+    const int u = p + S.i[PackedWalk::kOff][g];
     const float min_line = (float)u * 16.0f;
     const float max_line = min_line + 16.0f;
     const bool far = valid && max_line <= S.f[PackedWalk::kBmax0][g];
@@ -386,7 +387,8 @@ __device__ __forceinline__ uint32_t packed_walk(PackedWalk& S, int nl, const Wal
     if (far) {
       const float4 gco = make_float4(S.f[PackedWalk::kCa][g], S.f[PackedWalk::kCb][g],
                                      S.f[PackedWalk::kCc][g], 0.0f);
-      ellipse_isect(gco, S.f[PackedWalk::kDisc][g], S.f[PackedWalk::kT][g], S.f[PackedWalk::kPx][g],
+      const float disc = gco.y * gco.y - gco.x * gco.z;  // as walk_setup forms it
+      ellipse_isect(gco, disc, S.f[PackedWalk::kT][g], S.f[PackedWalk::kPx][g],
                     S.f[PackedWalk::kPy][g], is_y, max_line, iM0, iM1);
     }
     float il0 = __shfl_up(iM0, 1u, kWave), il1 = __shfl_up(iM1, 1u, kWave);
@@ -410,7 +412,7 @@ __device__ __forceinline__ uint32_t packed_walk(PackedWalk& S, int nl, const Wal
       if (vmax > vmin) {
         atomicAdd(&S.i[PackedWalk::kCnt][g], vmax - vmin);
         uint64_t d[4];
-        st_span_bits((flags & 2) != 0, st.set_ok, S.i[PackedWalk::kBx][g], S.i[PackedWalk::kBy][g],
+        st_span_bits((geo & 2u) != 0u, st.set_ok, (int)((geo >> 2) & 0x7FFFu), (int)(geo >> 17),
                      st.sgx, u, vmin, vmax, is_y, d);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -1020,6 +1022,8 @@ static int32_t preprocess_fwd_check(const fgs_preprocess_params* p, const fgs_pr
   }
   if (p->image_width <= 0 || p->image_height <= 0 || p->grid_x <= 0 || p->grid_y <= 0)
     return fail("bad image size");
+  // the packed tile walks keep tile coordinates in 16 bits
+  if (p->grid_x > 65535 || p->grid_y > 65535) return fail("more than 65535 tiles on a side");
   if (!io->st_rec != !io->st_masks || (reinterpret_cast<uintptr_t>(io->st_masks) & 15u) ||
       (reinterpret_cast<uintptr_t>(io->st_rec) & 15u))
     return fail("st_rec and st_masks must both be set (16-byte aligned) or both NULL");
