@@ -69,8 +69,8 @@ typedef struct {
   int32_t max_sh_coeffs;      /* sh.shape[1]: rest coefficients per Gaussian */
   int32_t image_width;
   int32_t image_height;
-  int32_t grid_x;             /* ceil(W/16) */
-  int32_t grid_y;             /* ceil(H/16) */
+  int32_t grid_x;             /* ceil(W/16), at most 65535 */
+  int32_t grid_y;             /* ceil(H/16), at most 65535 */
   int32_t use_cov3d_precomp;  /* geometry path: 1 = cov3d_precomp, 0 = scales+rotations */
   int32_t use_colors_precomp; /* colour path: 1 = colors_precomp, 0 = dc+sh */
   float scale_modifier;
