@@ -48,6 +48,22 @@ def test_workspace_queries_and_error_path():
         _lib.check(rc)
 
 
+def test_preprocess_rejects_grids_beyond_16_bit_tiles():
+    """The packed tile walks keep tile coordinates in 16 bits: a grid with
+    more than 65535 tiles on a side is rejected before any launch (the
+    pointers are placeholders the check never dereferences)."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(256)
+    io = _lib.PreprocessFwdIO(*([fake] * len(_lib.PreprocessFwdIO._fields_)))
+    io.st_rec = None
+    io.st_masks = None
+    for gx, gy in ((65536, 4), (4, 70000)):
+        prm = _lib.PreprocessParams(10, 0, 0, gx * 16, gy * 16, gx, gy, 0, 0, 1.0, 1.0, 1.0, 1.0)
+        rc = lib.fgs_preprocess_geometry_fwd(ctypes.byref(prm), ctypes.byref(io), None)
+        assert rc == _lib.FGS_ERR_INVALID_ARGUMENT
+        assert b"65535" in lib.fgs_last_error()
+
+
 def test_wait_spin_limit_setting():
     """fgs_set_wait_spin_limit swaps the process-wide poll bound (default 2^24)
     and returns the previous value; it touches no GPU."""
