@@ -361,6 +361,8 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
   const float Bdx = a.w * dx;
   const float Adxdx = (a.z * dx) * dx;
   const float Cc = b.x;
+  // the means2d terms' parts in dx, the same for the lane's four strips
+  const float hxdx = h.x * dx, hwdx = h.w * dx;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     if (jj >= nc_max[k]) continue;  // every pixel of the strip ends before this splat
@@ -416,16 +418,25 @@ __device__ __forceinline__ bool bwd_splat_terms(const float4 a, const float4 b, 
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] += geo ? t[i] : 0.0f;
       } else {
-        v[0] = __builtin_fmaf(qg, mx, v[0]);
-        v[1] = __builtin_fmaf(qg, my, v[1]);
-        v[2] = __builtin_fmaf(fabsf(qg), fabsf(mx), v[2]);
-        v[3] = __builtin_fmaf(fabsf(qg), fabsf(my), v[3]);
-        v[4] = __builtin_fmaf(qg, dxdx, v[4]);
-        v[5] = __builtin_fmaf(qdy, dx, v[5]);
+        // the terms linear in qg are summed as sum(qg) and sum(qg dy) here
+        // (v[7], v[5]) and formed from them once per splat below; the
+        // magnitudes and the dy^2 term need each strip's own factor
+        const float mxs = __builtin_fmaf(h.y, dy, hxdx);
+        const float mys = __builtin_fmaf(h.z, dy, hwdx);
+        v[2] = __builtin_fmaf(fabsf(qg), fabsf(mxs), v[2]);
+        v[3] = __builtin_fmaf(fabsf(qg), fabsf(mys), v[3]);
+        v[5] += qdy;
         v[6] = __builtin_fmaf(qdy, dy, v[6]);
         v[7] += qg;
       }
     }
+  }
+  if (!kSafe && any) {  // wave-uniform
+    const float sq = v[7], sqdy = v[5];
+    v[0] = __builtin_fmaf(h.y, sqdy, hxdx * sq);  // sum qg (h.x dx + h.y dy)
+    v[1] = __builtin_fmaf(h.z, sqdy, hwdx * sq);  // sum qg (h.z dy + h.w dx)
+    v[4] = dxdx * sq;                             // sum qg dx^2
+    v[5] = dx * sqdy;                             // sum qg dx dy
   }
   return any;
 }
