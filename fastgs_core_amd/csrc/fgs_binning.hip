@@ -375,6 +375,23 @@ __global__ void copy_pairs_kernel(const K* __restrict__ ki, const uint32_t* __re
   }
 }
 
+// Wave64 match-any over the low 8 bits of d: the lanes of `peers` whose d
+// has the same 8 bits.  sel is all ones where bit b of d is 0, so (m ^ sel)
+// is the ballot m or its complement; with the AND that is one three-input
+// bit operation per 32-bit half on gfx950 (v_bitop3_b32), after one compare.
+__device__ __forceinline__ uint64_t match_any_8(uint32_t d, uint64_t peers) {
+  const uint32_t nd = ~d;
+  uint32_t plo = (uint32_t)peers, phi = (uint32_t)(peers >> 32);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const uint32_t sel = (uint32_t)__builtin_amdgcn_sbfe((int32_t)nd, (uint32_t)b, 1u);
+    const uint64_t m = __ballot(sel == 0u);
+    plo &= (uint32_t)m ^ sel;
+    phi &= (uint32_t)(m >> 32) ^ sel;
+  }
+  return ((uint64_t)phi << 32) | plo;
+}
+
 // ---------------------------------------------------------------------------
 // One-sweep LSD radix sort: one histogram kernel for every digit pass, then
 // one kernel per pass that ranks its chunk, gets each digit's offset by
@@ -564,19 +581,7 @@ radix_pass_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ va
     const uint32_t d = (uint32_t)(key[it] >> shift) & mask;
     uint64_t peers = __ballot(valid);
     if constexpr (kBits > 0) {
-      // the lanes that share each bit: sel is all ones where bit b of d is
-      // 0, so (m ^ sel) is the ballot m or its complement (one three-input
-      // bit operation per half with the AND)
-      const uint32_t nd = ~d;
-      uint32_t plo = (uint32_t)peers, phi = (uint32_t)(peers >> 32);
-#pragma unroll
-      for (int b = 0; b < kBits; ++b) {
-        const uint32_t sel = (uint32_t)__builtin_amdgcn_sbfe((int32_t)nd, (uint32_t)b, 1u);
-        const uint64_t m = __ballot(sel == 0u);
-        plo &= (uint32_t)m ^ sel;
-        phi &= (uint32_t)(m >> 32) ^ sel;
-      }
-      peers = ((uint64_t)phi << 32) | plo;
+      peers = match_any_8(d, peers);
     } else {
       for (int b = 0; b < nbits; ++b) {
         const bool bit = (d >> b) & 1u;
@@ -1395,13 +1400,7 @@ l1_place_kernel(int32_t P, StGrid sg, const uint32_t* __restrict__ order,
       const uint32_t q = q0 + (uint32_t)t;
       const bool valid = q < rn;
       const uint32_t d = valid ? s_ps[q] : 0u;
-      uint64_t peers = __ballot(valid);
-#pragma unroll
-      for (int bit = 0; bit < 8; ++bit) {
-        const bool on = (d >> bit) & 1u;
-        const uint64_t mb = __ballot(on);
-        peers &= on ? mb : ~mb;
-      }
+      const uint64_t peers = match_any_8(d, __ballot(valid));
       const uint32_t rk = (uint32_t)__popcll(peers & lt);
       if (valid && rk == 0) s_wh[w][d] = (uint32_t)__popcll(peers);
       __syncthreads();
