@@ -139,15 +139,29 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
 #pragma unroll
     for (int m = 0; m < 2; ++m) load_row(src[m], a, pf, c0, l, rq.v0[m][sl], rq.v1[m][sl]);
     lds_barrier();
-    float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
+    // the window is symmetric (win[k] == win[10 - k] exactly): taps k and
+    // 10 - k share one weight, so the pair's values (and products) are added
+    // before the multiply-add: 73 instructions per row instead of 88
+    const float xc = sx[l + kLR], yc = sy[l + kLR];
+    float m0, m1, m2, m3, m4;
+    {
+      const float w = a.win[kLR];
+      m0 = w * xc;
+      m1 = w * yc;
+      m2 = w * (xc * xc);
+      m3 = w * (yc * yc);
+      m4 = w * (xc * yc);
+    }
 #pragma unroll
-    for (int k = 0; k < 11; ++k) {
-      const float x = sx[l + k], y = sy[l + k], w = a.win[k];
-      m0 = __builtin_fmaf(w, x, m0);
-      m1 = __builtin_fmaf(w, y, m1);
-      m2 = __builtin_fmaf(w, x * x, m2);
-      m3 = __builtin_fmaf(w, y * y, m3);
-      m4 = __builtin_fmaf(w, x * y, m4);
+    for (int k = 0; k < kLR; ++k) {
+      const float xa = sx[l + k], xb = sx[l + 2 * kLR - k];
+      const float ya = sy[l + k], yb = sy[l + 2 * kLR - k];
+      const float w = a.win[k];
+      m0 = __builtin_fmaf(w, xa + xb, m0);
+      m1 = __builtin_fmaf(w, ya + yb, m1);
+      m2 = __builtin_fmaf(w, __builtin_fmaf(xa, xa, xb * xb), m2);
+      m3 = __builtin_fmaf(w, __builtin_fmaf(ya, ya, yb * yb), m3);
+      m4 = __builtin_fmaf(w, __builtin_fmaf(xa, ya, xb * yb), m4);
     }
     ring[sl][0] = m0;
     ring[sl][1] = m1;
@@ -156,7 +170,6 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
     ring[sl][4] = m4;
     // |x - y| of the strip's own pixels, from the staged centre column (zero
     // outside the image, where both values read zero)
-    const float xc = sx[l + kLR], yc = sy[l + kLR];
     l1_sum += (i >= kLR && i < kLR + kSH) ? fabsf(xc - yc) : 0.f;
     if (first && i < 2 * kLR) return;  // compile-time
     const int orow = r0 + i - 2 * kLR;
@@ -175,7 +188,9 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
     const float sxx = exx - mx * mx, syy = eyy - my * my, sxy = exy - mx * my;
     const float A = 2.f * mx * my + C1, Bv = 2.f * sxy + C2;
     const float Cv = mx * mx + my * my + C1, D = sxx + syy + C2;
-    const float inv = 1.0f / (Cv * D);  // 1/Cv = D inv, 1/D = Cv inv
+    // 1/Cv = D inv, 1/D = Cv inv; the hardware reciprocal (1 ulp; Cv D >= C1 C2
+    // when the variances are not negative), no decision depends on it
+    const float inv = __builtin_amdgcn_rcpf(Cv * D);
     const float S = A * Bv * inv;
     ssim_sum += out ? S : 0.f;
     if (kMaps) {
