@@ -185,24 +185,29 @@ l1_ssim_fwd_kernel(const LossArgs a, const float* __restrict__ img, const float*
       exy = __builtin_fmaf(w, ring[q][4], exy);
     }
     const bool out = orow < a.H && col_in;
-    const float sxx = exx - mx * mx, syy = eyy - my * my, sxy = exy - mx * my;
-    const float A = 2.f * mx * my + C1, Bv = 2.f * sxy + C2;
-    const float Cv = mx * mx + my * my + C1, D = sxx + syy + C2;
-    // 1/Cv = D inv, 1/D = Cv inv; the hardware reciprocal (1 ulp; Cv D >= C1 C2
-    // when the variances are not negative), no decision depends on it
-    const float inv = __builtin_amdgcn_rcpf(Cv * D);
-    const float S = A * Bv * inv;
-    ssim_sum += out ? S : 0.f;
-    if (kMaps) {
-      // partials w.r.t. mu_x, sigma_xx, sigma_xy, then to the raw moments
-      const float dS_dmu = 2.f * my * Bv * inv - S * 2.f * mx * (D * inv);
-      const float dS_dsxx = -S * (Cv * inv);
-      const float dS_dsxy = 2.f * A * inv;
-      const float d1 = dS_dmu + dS_dsxx * (-2.f * mx) + dS_dsxy * (-my);
-      const uint32_t po = out ? (uint32_t)(orow * a.W + gc) * 4u : kOob;
-      buf_store(dst[0], po, d1);
-      buf_store(dst[1], po, dS_dsxx);
-      buf_store(dst[2], po, dS_dsxy);
+    {
+      // contracted: the SSIM terms take no decision, and fused products
+      // round less (the loss stays inside the tests' bounds)
+#pragma clang fp contract(fast)
+      const float sxx = exx - mx * mx, syy = eyy - my * my, sxy = exy - mx * my;
+      const float A = 2.f * mx * my + C1, Bv = 2.f * sxy + C2;
+      const float Cv = mx * mx + my * my + C1, D = sxx + syy + C2;
+      // 1/Cv = D inv, 1/D = Cv inv; the hardware reciprocal (1 ulp; Cv D >= C1 C2
+      // when the variances are not negative), no decision depends on it
+      const float inv = __builtin_amdgcn_rcpf(Cv * D);
+      const float S = A * Bv * inv;
+      ssim_sum += out ? S : 0.f;
+      if (kMaps) {
+        // partials w.r.t. mu_x, sigma_xx, sigma_xy, then to the raw moments
+        const float dS_dmu = 2.f * my * Bv * inv - S * 2.f * mx * (D * inv);
+        const float dS_dsxx = -S * (Cv * inv);
+        const float dS_dsxy = 2.f * A * inv;
+        const float d1 = dS_dmu + dS_dsxx * (-2.f * mx) + dS_dsxy * (-my);
+        const uint32_t po = out ? (uint32_t)(orow * a.W + gc) * 4u : kOob;
+        buf_store(dst[0], po, d1);
+        buf_store(dst[1], po, dS_dsxx);
+        buf_store(dst[2], po, dS_dsxy);
+      }
     }
   };
   // rows are kept apart in the schedule: interleaving them lengthens
