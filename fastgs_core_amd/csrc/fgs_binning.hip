@@ -205,13 +205,6 @@ __device__ __forceinline__ uint32_t block_sum_predecessors(const uint64_t* statu
   return total;
 }
 
-// take_ticket with a barrier that orders LDS only: the workgroup's other
-// loads (issued before it) stay in flight.
-__device__ __forceinline__ int64_t take_ticket_lds(uint32_t* ticket, uint32_t* s_slot) {
-  if (threadIdx.x == 0) *s_slot = atomicAdd(ticket, 1u);
-  lds_barrier();
-  return (int64_t)*s_slot;
-}
 __device__ __forceinline__ int64_t take_ticket(uint32_t* ticket, uint32_t* s_slot) {
   if (threadIdx.x == 0) *s_slot = atomicAdd(ticket, 1u);
   __syncthreads();
