@@ -205,6 +205,7 @@ __device__ __forceinline__ uint32_t block_sum_predecessors(const uint64_t* statu
   return total;
 }
 
+// The workgroup's chunk number from an atomic ticket (the chained scans).
 __device__ __forceinline__ int64_t take_ticket(uint32_t* ticket, uint32_t* s_slot) {
   if (threadIdx.x == 0) *s_slot = atomicAdd(ticket, 1u);
   __syncthreads();
